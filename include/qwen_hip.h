@@ -1,0 +1,231 @@
+/*
+ * libqwen_hip.so: the MI355X (gfx950) backend for the Qwen2.5 engine's GPU layer.
+ *
+ * This C ABI is the drop-in boundary. It replaces the operator surface the
+ * reference's model loop calls into src/gpu (abho7/llm-inference-webgpu):
+ * GpuContext (src/gpu/device.js:21-392), the eight WGSL kernels
+ * (src/gpu/kernels.js:33-530) and GpuModel (src/gpu/model.js:69-403). A
+ * Node-API addon (js/addon/qwen_napi.cpp) and a ctypes module (qwen_hip.py)
+ * bind it; both only marshal arguments.
+ *
+ * Conventions
+ *   - Plain C: opaque handles, plain pointers and sizes, int status (QH_OK = 0).
+ *     On failure, qh_last_error() returns a message for the calling thread.
+ *   - Pointers named d_* are device pointers (from qh_alloc or any HIP
+ *     allocation on the context's device); h_* are host pointers, borrowed for
+ *     the duration of the call.
+ *   - Operators are asynchronous on the context's one stream, in call order,
+ *     like WebGPU's queue (device.js:152-165). qh_download / qh_sync / calls
+ *     returning host results wait.
+ *   - A context is used by one thread at a time; forward/decode refuse
+ *     reentrancy (src/gpu/model.js:228-232).
+ *   - Every operator checks its arguments on the host before launching, so a
+ *     shape the kernels do not support is an error, never a device fault.
+ */
+#ifndef QWEN_HIP_H
+#define QWEN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QH_ABI_VERSION 1
+
+/* Status codes. The reference throws Error / RangeError synchronously for misuse
+ * (src/gpu/model.js:231,249-254; src/gpu/device.js:48-56,153,254). */
+enum {
+  QH_OK = 0,
+  QH_ERR_INVALID = 1, /* bad argument or unsupported shape (Error) */
+  QH_ERR_RANGE = 2,   /* cache capacity, rope table, vocabulary (RangeError) */
+  QH_ERR_BUSY = 3,    /* forward() already running (model.js:231) */
+  QH_ERR_DEVICE = 4,  /* HIP runtime failure, or no device */
+  QH_ERR_NOMEM = 5,
+  QH_ERR_STATE = 6    /* e.g. model not finalized, tensor missing */
+};
+
+/* Weight storage formats. QH_FMT_INT8 / QH_FMT_INT4 take the reference
+ * quantizer's arrays verbatim (src/core/quantize.js:36-151): int8 codes
+ * row-major + one f32 scale per row; int4 codes two per byte, low nibble =
+ * even flat index, + one f32 scale and one f32 integer zero point per group. */
+enum {
+  QH_FMT_F32 = 0,  /* norms and biases */
+  QH_FMT_F16 = 1,  /* the reference's shipping weight format (model.js:165-173) */
+  QH_FMT_INT8 = 2,
+  QH_FMT_INT4 = 3,
+  QH_FMT_BF16 = 4  /* the checkpoint format; the embedding gather table */
+};
+
+const char* qh_last_error(void);
+int qh_abi_version(void);
+
+/* ------------------------------------------------------------------ context
+ * GpuContext.create (device.js:47-77), describe (:382-391), done (:272). */
+typedef struct qh_ctx qh_ctx;
+int qh_device_count(int* count);
+int qh_open(int device, qh_ctx** out);
+int qh_close(qh_ctx* ctx);
+/* JSON text: device name, arch, CU count, HBM bytes, LDS per workgroup. */
+int qh_describe(qh_ctx* ctx, char* buf, size_t len);
+int qh_sync(qh_ctx* ctx);
+/* The context's hipStream_t, for callers that time or order their own work on it. */
+void* qh_stream(qh_ctx* ctx);
+
+/* ------------------------------------------------------------------- memory
+ * GpuContext.upload / empty / readF32 (device.js:80-99, 229-251). */
+int qh_alloc(qh_ctx* ctx, size_t bytes, void** d_out);
+int qh_free(qh_ctx* ctx, void* d_ptr);
+int qh_upload(qh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);
+int qh_download(qh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);
+int qh_memset(qh_ctx* ctx, void* d_dst, int value, size_t bytes);
+
+/* Device events on the context stream (GpuContext.timed, device.js:301-338). */
+typedef struct qh_event qh_event;
+int qh_event_create(qh_ctx* ctx, qh_event** out);
+int qh_event_record(qh_ctx* ctx, qh_event* ev);
+int qh_event_elapsed_ms(qh_event* start, qh_event* stop, float* ms); /* waits for stop */
+int qh_event_destroy(qh_event* ev);
+
+/* ---------------------------------------------------------------- operators
+ * One descriptor for a weight matrix [rows, cols] in device memory. */
+typedef struct {
+  int32_t format;      /* QH_FMT_F16 | QH_FMT_INT8 | QH_FMT_INT4 */
+  int32_t rows, cols;
+  int32_t group;       /* int4 group size (a multiple of 32 dividing cols); else 0 */
+  const void* d_data;  /* f16 [rows*cols] | int8 [rows*cols] | u8 [rows*cols/2] */
+  const float* d_scales; /* int8 [rows] | int4 [rows*cols/group] */
+  const float* d_zeros;  /* int4 [rows*cols/group] */
+} qh_weight;
+
+/* MATVEC / batchedMatvec (kernels.js:33-79, 232-290; dispatch model.js:284-317):
+ * y[b, r] = sum_c W[r, c] * x[b, c] (+ bias[r]) for b < seq. Every position is summed in
+ * the same order whatever `seq` is, so prefill agrees with decode bit for bit.
+ * x f32 [seq, cols], bias f32 [rows] or NULL, y f32 [seq, rows]. */
+int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+              float* d_y, int32_t seq);
+/* The isolated-matvec form: f16 activation x [cols], f32 y [rows]. */
+int qh_matvec_xh(qh_ctx* ctx, const qh_weight* w, const uint16_t* d_x, float* d_y);
+/* A list of `count` same-shape matrices in one launch: weight i starts at
+ * d_data + i*data_stride bytes (scales / zeros at i*scale_stride floats), x_i at
+ * d_x + i*x_stride halves (x_stride 0: one shared x), y_i at d_y + i*rows floats.
+ * This is how a working set larger than the last-level cache is streamed in one launch. */
+int qh_matvec_xh_list(qh_ctx* ctx, const qh_weight* w, int32_t count, size_t data_stride,
+                      size_t scale_stride, const uint16_t* d_x, size_t x_stride, float* d_y);
+
+/* RMSNORM (kernels.js:300-343): y = x / sqrt(mean(x^2) + eps) * gain, eps inside the root.
+ * x, y f32 [rows, cols]; gain f32 [cols]. */
+int qh_rmsnorm(qh_ctx* ctx, const float* d_x, const float* d_gain, float* d_y, int32_t rows,
+               int32_t cols, double eps);
+
+/* ROPE (kernels.js:360-389), in place over v [rows, heads*head_dim], half-split pairs
+ * (j, j + head_dim/2), cos/sin tables [positions, head_dim/2] f32 indexed at base_pos + row.
+ * `table_positions` bounds the index: base_pos + rows > table_positions is QH_ERR_RANGE. */
+int qh_rope(qh_ctx* ctx, float* d_v, const float* d_cos, const float* d_sin,
+            int32_t table_positions, int32_t rows, int32_t heads, int32_t head_dim,
+            int32_t base_pos);
+/* Host helper that builds the tables in f64 and stores f32 (src/core/ops.js:99-136). */
+int qh_rope_tables(int32_t head_dim, double theta, int32_t positions, float* h_cos,
+                   float* h_sin);
+
+/* The KV append (model.js:336-338): k, v f32 [seq, kv_heads*head_dim] written as f16 into a
+ * head-major cache [kv_heads, capacity, head_dim] at positions past .. past+seq-1. */
+int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_key_cache,
+                 uint16_t* d_value_cache, int32_t capacity, int32_t kv_heads, int32_t head_dim,
+                 int32_t past, int32_t seq);
+
+/* ATTENTION (kernels.js:404-499): causal GQA over an f16 head-major cache. Query t (absolute
+ * position past+t) attends to positions 0..past+t. Query head h reads kv head
+ * h / (heads/kv_heads). Scale 1/sqrt(head_dim). q, out f32 [seq, heads*head_dim].
+ * Split-K online softmax over fixed 64-position chunks. head_dim must be 64. */
+int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                 const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                 int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim);
+
+/* SWIGLU (kernels.js:502-515): gate = silu(gate) * up, in place. */
+int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n);
+/* ADD (kernels.js:518-530): x += delta. */
+int qh_add(qh_ctx* ctx, float* d_x, const float* d_delta, int32_t n);
+/* The caller's argmax (web/bench.html:129-131): strict '>' scan semantics -- the lowest index
+ * of the maximum, NaN never wins unless at index 0. Waits; writes one int to *h_index. */
+int qh_argmax(qh_ctx* ctx, const float* d_v, int32_t n, int32_t* h_index);
+
+/* ------------------------------------------------------------ host helpers
+ * The reference quantizer (src/core/quantize.js:36-132), restated for the load path. */
+int qh_quantize_int8(const float* h_w, int32_t rows, int32_t cols, int8_t* h_q,
+                     float* h_scales);
+int qh_quantize_int4(const float* h_w, int32_t rows, int32_t cols, int32_t group,
+                     uint8_t* h_q, float* h_scales, float* h_zeros);
+
+/* Seeded synthetic inputs (the reference has no random-init facility). Counter-based, so any
+ * element can be generated independently and every platform produces the same bits.
+ * Values: std * (sum of 12 uniform u32 / 2^32 - 6), the Irwin-Hall approximation of N(0,1),
+ * computed exactly in f64 and rounded once to f32. `name` selects the stream. */
+int qh_synth_f32(uint64_t seed, const char* name, double std, size_t offset, size_t n,
+                 float* h_out);
+/* As qh_synth_f32, then rounded to bf16 (round to nearest even): a checkpoint tensor. */
+int qh_synth_bf16(uint64_t seed, const char* name, double std, size_t offset, size_t n,
+                  uint16_t* h_out);
+/* Uniform token ids in [0, vocab). */
+int qh_synth_tokens(uint64_t seed, const char* name, int32_t vocab, size_t n, int32_t* h_out);
+
+/* -------------------------------------------------------------------- model
+ * GpuModel (model.js:86-403) and GpuKVCache (model.js:69-84). */
+typedef struct {
+  int32_t hidden, intermediate, layers, heads, kv_heads, head_dim, vocab;
+  double rope_theta, eps;
+  int32_t max_positions; /* rope table rows (GpuModel.load maxPositions, model.js:148) */
+} qh_config;
+
+typedef struct qh_model qh_model;
+typedef struct qh_cache qh_cache;
+
+int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out);
+/* Upload one tensor by its checkpoint name (src/core/config.js:88-119), copied from host.
+ *   model.embed_tokens.weight  QH_FMT_BF16 [vocab, hidden]: the input gather table
+ *   lm_head.weight             F16 | INT8 | INT4 [vocab, hidden]: the output projection (for a
+ *                              tied model, the loader's copy of the embedding, model.js:184)
+ *   model.norm.weight, model.layers.N.{input_layernorm,post_attention_layernorm}.weight  F32
+ *   model.layers.N.self_attn.{q,k,v}_proj.bias  F32
+ *   model.layers.N.self_attn.{q,k,v,o}_proj.weight, model.layers.N.mlp.{gate,up,down}_proj.weight
+ *                              F16 | INT8 | INT4; all seven of a layer in one format.
+ * rows/cols give the shape (cols = 1 for vectors); data/scales/zeros as in qh_weight. */
+int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t rows,
+                        int32_t cols, int32_t group, const void* h_data, const float* h_scales,
+                        const float* h_zeros);
+/* Checks that every tensor is present with its shape, builds the rope tables and the fused
+ * device layouts. Afterwards the model is immutable. */
+int qh_model_finalize(qh_model* m);
+int qh_model_free(qh_model* m);
+/* Device bytes held by the model's weights. */
+int qh_model_bytes(qh_model* m, size_t* bytes);
+
+int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out);  /* model.js:209 */
+int qh_cache_free(qh_cache* c);
+int qh_cache_length(qh_cache* c, int32_t* length);
+/* Rewind to an earlier length (cache.reset() is length 0, model.js:83). */
+int qh_cache_set_length(qh_cache* c, int32_t length);
+/* [kv_heads, length, head_dim] f32 per layer (the ONNX 'present' layout, src/cpu/cache.js:97-115). */
+int qh_cache_present(qh_cache* c, int32_t layer, float* h_key, float* h_value);
+
+/* GpuModel.forward (model.js:227-402): `hidden` is the embedded input [seq, hidden] f32.
+ * h_logits (may be NULL) receives the last position's [vocab] logits; h_argmax (may be NULL)
+ * the device argmax of them. */
+int qh_forward(qh_model* m, qh_cache* c, const float* h_hidden, int32_t seq, float* h_logits,
+               int32_t* h_argmax);
+/* As qh_forward, with the embedding gather done on the device from token ids. */
+int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t seq,
+                      float* h_logits, int32_t* h_argmax);
+/* Greedy decode (the loop of web/bench.html:121-134) as `steps` replays of a hipGraph-captured
+ * decode step: token -> gather -> 24 layers -> lm_head -> argmax -> next token, all on the device.
+ * h_tokens [steps] receives the generated ids; the first step consumes `first_token`. */
+int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int32_t* h_tokens);
+/* Enqueue the graph replays without waiting (for timing); qh_decode_collect waits and copies. */
+int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps);
+int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

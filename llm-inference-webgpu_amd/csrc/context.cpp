@@ -1,0 +1,358 @@
+// Context, memory, events and the standalone operator entry points of the C ABI.
+// Every entry point validates its arguments on the host before anything is
+// launched, so an unsupported shape is an error code, never a device fault.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "qh_internal.h"
+
+namespace qh {
+
+static thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+void clear_error() { g_error.clear(); }
+
+int weights_per_chunk(int format) {
+  switch (format) {
+    case QH_FMT_F16: return 8;
+    case QH_FMT_INT8: return 16;
+    case QH_FMT_INT4: return 32;
+    default: return 0;
+  }
+}
+
+int make_dmat(const qh_weight* w, DMat* out) {
+  QH_CHECK(w, QH_ERR_INVALID, "weight descriptor is NULL");
+  const int per = weights_per_chunk(w->format);
+  QH_CHECK(per > 0, QH_ERR_INVALID, "weight format %d is not a matrix format", w->format);
+  QH_CHECK(w->rows > 0 && w->cols > 0, QH_ERR_INVALID, "weight shape [%d, %d] is empty", w->rows,
+           w->cols);
+  QH_CHECK(w->cols % per == 0, QH_ERR_INVALID,
+           "cols %d must be a multiple of %d for this format (16-byte row chunks)", w->cols, per);
+  QH_CHECK(w->d_data, QH_ERR_INVALID, "weight data is NULL");
+  QH_CHECK(((uintptr_t)w->d_data & 15) == 0, QH_ERR_INVALID, "weight data must be 16-byte aligned");
+  DMat m{};
+  m.format = w->format;
+  m.data = static_cast<const uint8_t*>(w->d_data);
+  m.rows = w->rows;
+  m.cols = w->cols;
+  m.row_bytes = w->format == QH_FMT_F16 ? w->cols * 2 : w->format == QH_FMT_INT8 ? w->cols : w->cols / 2;
+  m.nchunks = m.row_bytes / 16;
+  if (w->format == QH_FMT_INT8) {
+    QH_CHECK(w->d_scales, QH_ERR_INVALID, "int8 weight needs per-row scales");
+    m.scales = w->d_scales;
+  }
+  if (w->format == QH_FMT_INT4) {
+    QH_CHECK(w->group >= 32 && w->group % 32 == 0 && w->cols % w->group == 0, QH_ERR_INVALID,
+             "int4 group %d must be a multiple of 32 dividing cols %d", w->group, w->cols);
+    QH_CHECK(w->d_scales && w->d_zeros, QH_ERR_INVALID, "int4 weight needs scales and zeros");
+    m.scales = w->d_scales;
+    m.zeros = w->d_zeros;
+    m.gpr = w->cols / w->group;
+    m.cpg = w->group / 32;
+  }
+  *out = m;
+  return QH_OK;
+}
+
+}  // namespace qh
+
+using qh::fail;
+
+extern "C" {
+
+const char* qh_last_error(void) { return qh::g_error.c_str(); }
+int qh_abi_version(void) { return QH_ABI_VERSION; }
+
+int qh_device_count(int* count) {
+  QH_CHECK(count, QH_ERR_INVALID, "count is NULL");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) n = 0;
+  *count = n;
+  return QH_OK;
+}
+
+int qh_open(int device, qh_ctx** out) {
+  QH_CHECK(out, QH_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    return fail(QH_ERR_DEVICE, "no HIP device is available (this library has no CPU fallback)");
+  }
+  QH_CHECK(device >= 0 && device < n, QH_ERR_INVALID, "device %d out of range (have %d)", device, n);
+  QH_HIP(hipSetDevice(device));
+  hipDeviceProp_t p;
+  QH_HIP(hipGetDeviceProperties(&p, device));
+  qh_ctx* c = new qh_ctx();
+  c->device = device;
+  c->name = p.name;
+  c->arch = p.gcnArchName;
+  c->cus = p.multiProcessorCount;
+  c->hbm_bytes = p.totalGlobalMem;
+  c->lds_per_block = p.sharedMemPerBlock;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(QH_ERR_DEVICE, "hipStreamCreate failed");
+  }
+  c->scratch_bytes = 1 << 20;
+  if (hipMalloc(&c->d_scratch, c->scratch_bytes) != hipSuccess ||
+      hipMemset(c->d_scratch, 0, c->scratch_bytes) != hipSuccess ||
+      hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
+    hipFree(c->d_scratch);
+    hipStreamDestroy(c->stream);
+    delete c;
+    return fail(QH_ERR_NOMEM, "context scratch allocation failed");
+  }
+  *out = c;
+  return QH_OK;
+}
+
+int qh_close(qh_ctx* ctx) {
+  if (!ctx) return QH_OK;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  hipFree(ctx->d_scratch);
+  hipHostFree(ctx->h_pinned);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return QH_OK;
+}
+
+int qh_describe(qh_ctx* ctx, char* buf, size_t len) {
+  QH_CHECK(ctx && buf && len > 0, QH_ERR_INVALID, "describe needs a context and a buffer");
+  snprintf(buf, len,
+           "{\"name\": \"%s\", \"arch\": \"%s\", \"compute_units\": %d, \"hbm_bytes\": %zu, "
+           "\"lds_per_block\": %zu, \"abi\": %d}",
+           ctx->name.c_str(), ctx->arch.c_str(), ctx->cus, ctx->hbm_bytes, ctx->lds_per_block,
+           QH_ABI_VERSION);
+  return QH_OK;
+}
+
+int qh_sync(qh_ctx* ctx) {
+  QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
+  QH_HIP(hipStreamSynchronize(ctx->stream));
+  return QH_OK;
+}
+
+void* qh_stream(qh_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int qh_alloc(qh_ctx* ctx, size_t bytes, void** d_out) {
+  QH_CHECK(ctx && d_out, QH_ERR_INVALID, "alloc needs a context and an output pointer");
+  *d_out = nullptr;
+  QH_HIP(hipSetDevice(ctx->device));
+  if (hipMalloc(d_out, bytes ? bytes : 4) != hipSuccess) {
+    return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", bytes);
+  }
+  return QH_OK;
+}
+
+int qh_free(qh_ctx* ctx, void* d_ptr) {
+  QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
+  if (!d_ptr) return QH_OK;
+  QH_HIP(hipStreamSynchronize(ctx->stream));
+  QH_HIP(hipFree(d_ptr));
+  return QH_OK;
+}
+
+int qh_upload(qh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes) {
+  QH_CHECK(ctx && d_dst && (h_src || !bytes), QH_ERR_INVALID, "upload needs buffers");
+  QH_HIP(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, ctx->stream));
+  QH_HIP(hipStreamSynchronize(ctx->stream));
+  return QH_OK;
+}
+
+int qh_download(qh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes) {
+  QH_CHECK(ctx && d_src && (h_dst || !bytes), QH_ERR_INVALID, "download needs buffers");
+  QH_HIP(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+  QH_HIP(hipStreamSynchronize(ctx->stream));
+  return QH_OK;
+}
+
+int qh_memset(qh_ctx* ctx, void* d_dst, int value, size_t bytes) {
+  QH_CHECK(ctx && d_dst, QH_ERR_INVALID, "memset needs a buffer");
+  QH_HIP(hipMemsetAsync(d_dst, value, bytes, ctx->stream));
+  return QH_OK;
+}
+
+int qh_event_create(qh_ctx* ctx, qh_event** out) {
+  QH_CHECK(ctx && out, QH_ERR_INVALID, "event_create needs a context");
+  qh_event* e = new qh_event();
+  if (hipEventCreate(&e->ev) != hipSuccess) {
+    delete e;
+    return fail(QH_ERR_DEVICE, "hipEventCreate failed");
+  }
+  *out = e;
+  return QH_OK;
+}
+
+int qh_event_record(qh_ctx* ctx, qh_event* ev) {
+  QH_CHECK(ctx && ev, QH_ERR_INVALID, "event_record needs a context and an event");
+  QH_HIP(hipEventRecord(ev->ev, ctx->stream));
+  return QH_OK;
+}
+
+int qh_event_elapsed_ms(qh_event* start, qh_event* stop, float* ms) {
+  QH_CHECK(start && stop && ms, QH_ERR_INVALID, "elapsed needs two events");
+  QH_HIP(hipEventSynchronize(stop->ev));
+  QH_HIP(hipEventElapsedTime(ms, start->ev, stop->ev));
+  return QH_OK;
+}
+
+int qh_event_destroy(qh_event* ev) {
+  if (!ev) return QH_OK;
+  hipEventDestroy(ev->ev);
+  delete ev;
+  return QH_OK;
+}
+
+// --------------------------------------------------------------- operators --
+
+int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias, float* d_y,
+              int32_t seq) {
+  QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
+  qh::DMat m;
+  int rc = qh::make_dmat(w, &m);
+  if (rc) return rc;
+  QH_CHECK(d_x && d_y, QH_ERR_INVALID, "matvec needs x and y");
+  QH_CHECK(seq >= 1, QH_ERR_INVALID, "seq %d must be at least 1", seq);
+  QH_HIP(qh::launch_matvec(ctx->stream, m, d_x, d_bias, d_y, seq));
+  return QH_OK;
+}
+
+int qh_matvec_xh(qh_ctx* ctx, const qh_weight* w, const uint16_t* d_x, float* d_y) {
+  return qh_matvec_xh_list(ctx, w, 1, 0, 0, d_x, 0, d_y);
+}
+
+int qh_matvec_xh_list(qh_ctx* ctx, const qh_weight* w, int32_t count, size_t data_stride,
+                      size_t scale_stride, const uint16_t* d_x, size_t x_stride, float* d_y) {
+  QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
+  qh::DMat m;
+  int rc = qh::make_dmat(w, &m);
+  if (rc) return rc;
+  QH_CHECK(m.format == QH_FMT_INT8, QH_ERR_INVALID,
+           "the f16-activation matvec takes int8 weights (format %d given)", m.format);
+  QH_CHECK(count >= 1, QH_ERR_INVALID, "count %d must be at least 1", count);
+  QH_CHECK(d_x && d_y, QH_ERR_INVALID, "matvec needs x and y");
+  QH_CHECK(((uintptr_t)d_x & 15) == 0 && x_stride % 8 == 0, QH_ERR_INVALID,
+           "x must be 16-byte aligned with a stride that is a multiple of 8 halves");
+  QH_CHECK(count == 1 || (data_stride >= (size_t)m.rows * m.row_bytes && data_stride % 16 == 0 &&
+                          scale_stride >= (size_t)m.rows),
+           QH_ERR_INVALID, "list strides overlap the matrices or break 16-byte alignment");
+  QH_HIP(qh::launch_matvec_xh_list(ctx->stream, m, count, data_stride, scale_stride, d_x, x_stride,
+                                   d_y));
+  return QH_OK;
+}
+
+int qh_rmsnorm(qh_ctx* ctx, const float* d_x, const float* d_gain, float* d_y, int32_t rows,
+               int32_t cols, double eps) {
+  QH_CHECK(ctx && d_x && d_gain && d_y, QH_ERR_INVALID, "rmsnorm needs x, gain and y");
+  QH_CHECK(rows >= 1 && cols >= 1 && cols <= 16384, QH_ERR_INVALID,
+           "rmsnorm shape [%d, %d] unsupported (cols up to 16384)", rows, cols);
+  QH_HIP(qh::launch_rmsnorm(ctx->stream, d_x, d_gain, d_y, rows, cols, eps));
+  return QH_OK;
+}
+
+int qh_rope(qh_ctx* ctx, float* d_v, const float* d_cos, const float* d_sin,
+            int32_t table_positions, int32_t rows, int32_t heads, int32_t head_dim,
+            int32_t base_pos) {
+  QH_CHECK(ctx && d_v && d_cos && d_sin, QH_ERR_INVALID, "rope needs v and the tables");
+  QH_CHECK(rows >= 1 && heads >= 1 && head_dim >= 2 && head_dim % 2 == 0 && base_pos >= 0,
+           QH_ERR_INVALID, "rope shape rows=%d heads=%d head_dim=%d base=%d unsupported", rows,
+           heads, head_dim, base_pos);
+  QH_CHECK(base_pos + rows <= table_positions, QH_ERR_RANGE,
+           "position %d exceeds the %d-entry rope table", base_pos + rows, table_positions);
+  QH_HIP(qh::launch_rope(ctx->stream, d_v, d_cos, d_sin, rows, heads, head_dim, base_pos));
+  return QH_OK;
+}
+
+int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_key_cache,
+                 uint16_t* d_value_cache, int32_t capacity, int32_t kv_heads, int32_t head_dim,
+                 int32_t past, int32_t seq) {
+  QH_CHECK(ctx && d_k && d_v && d_key_cache && d_value_cache, QH_ERR_INVALID,
+           "kv_append needs k, v and both caches");
+  QH_CHECK(kv_heads >= 1 && head_dim >= 1 && seq >= 1 && past >= 0, QH_ERR_INVALID,
+           "kv_append shape unsupported");
+  QH_CHECK(past + seq <= capacity, QH_ERR_RANGE, "cache holds %d of %d; cannot add %d", past,
+           capacity, seq);
+  QH_HIP(qh::launch_kv_append(ctx->stream, d_k, d_v, d_key_cache, d_value_cache, capacity, kv_heads,
+                              head_dim, past, seq));
+  return QH_OK;
+}
+
+int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                 const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                 int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  QH_CHECK(ctx && d_q && d_key_cache && d_value_cache && d_out, QH_ERR_INVALID,
+           "attention needs q, both caches and out");
+  QH_CHECK(head_dim == 64, QH_ERR_INVALID, "attention supports head_dim 64 (got %d)", head_dim);
+  QH_CHECK(kv_heads >= 1 && heads >= kv_heads && heads % kv_heads == 0 && heads / kv_heads <= 8,
+           QH_ERR_INVALID, "heads %d / kv_heads %d must group evenly, at most 8 per kv head", heads,
+           kv_heads);
+  QH_CHECK(seq >= 1 && past >= 0, QH_ERR_INVALID, "attention needs seq >= 1 and past >= 0");
+  QH_CHECK(past + seq <= capacity, QH_ERR_RANGE, "attention over %d positions exceeds capacity %d",
+           past + seq, capacity);
+  const size_t pf = qh::attention_partials_floats(seq, heads, kv_heads, past + seq);
+  const size_t need = pf * sizeof(float) + (size_t)seq * kv_heads * sizeof(int) + 256;
+  void* parts = nullptr;
+  int* counters = nullptr;
+  if (need <= ctx->scratch_bytes) {
+    counters = static_cast<int*>(ctx->d_scratch);
+    parts = static_cast<char*>(ctx->d_scratch) + (((size_t)seq * kv_heads * sizeof(int) + 255) & ~(size_t)255);
+    QH_HIP(qh::launch_attention(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out, seq,
+                                past, heads, kv_heads, static_cast<float*>(parts), counters));
+    return QH_OK;
+  }
+  // Larger prefill shapes get a temporary buffer.
+  void* tmp = nullptr;
+  QH_HIP(hipMallocAsync(&tmp, need, ctx->stream));
+  QH_HIP(hipMemsetAsync(tmp, 0, 256 + (size_t)seq * kv_heads * sizeof(int), ctx->stream));
+  counters = static_cast<int*>(tmp);
+  parts = static_cast<char*>(tmp) + (((size_t)seq * kv_heads * sizeof(int) + 255) & ~(size_t)255);
+  hipError_t e = qh::launch_attention(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out,
+                                      seq, past, heads, kv_heads, static_cast<float*>(parts),
+                                      counters);
+  QH_HIP(hipFreeAsync(tmp, ctx->stream));
+  QH_HIP(e);
+  return QH_OK;
+}
+
+int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n) {
+  QH_CHECK(ctx && d_gate && d_up && n >= 1, QH_ERR_INVALID, "swiglu needs gate, up and n >= 1");
+  QH_HIP(qh::launch_swiglu(ctx->stream, d_gate, d_up, n));
+  return QH_OK;
+}
+
+int qh_add(qh_ctx* ctx, float* d_x, const float* d_delta, int32_t n) {
+  QH_CHECK(ctx && d_x && d_delta && n >= 1, QH_ERR_INVALID, "add needs x, delta and n >= 1");
+  QH_HIP(qh::launch_add(ctx->stream, d_x, d_delta, n));
+  return QH_OK;
+}
+
+int qh_argmax(qh_ctx* ctx, const float* d_v, int32_t n, int32_t* h_index) {
+  QH_CHECK(ctx && d_v && h_index && n >= 1, QH_ERR_INVALID, "argmax needs v, n >= 1 and an output");
+  QH_CHECK(qh::argmax_scratch_bytes(n) + 64 <= ctx->scratch_bytes, QH_ERR_INVALID,
+           "argmax over %d values exceeds the context scratch", n);
+  int32_t* d_out = reinterpret_cast<int32_t*>(static_cast<char*>(ctx->d_scratch) + ctx->scratch_bytes - 64);
+  QH_HIP(qh::launch_argmax(ctx->stream, d_v, n, ctx->d_scratch, d_out));
+  QH_HIP(hipMemcpyAsync(ctx->h_pinned, d_out, 4, hipMemcpyDeviceToHost, ctx->stream));
+  QH_HIP(hipStreamSynchronize(ctx->stream));
+  *h_index = ctx->h_pinned[0];
+  return QH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,694 @@
+// GpuModel / GpuKVCache (src/gpu/model.js:69-403) as C-ABI objects.
+//
+// Loading: tensors arrive by checkpoint name (src/core/config.js:88-119) in the
+// formats the reference quantizer produces, are uploaded as-is, and finalize()
+// rearranges them into the fused device layouts the decode kernels read: q|k|v
+// stacked into one matrix, gate and up rows interleaved. Rows are only moved,
+// never requantized, so every code and scale is the quantizer's own.
+//
+// Stepping: forward() runs one decode position at a time through the same
+// launches as decode() (so a prefill and a decode of the same tokens produce
+// the same bits, the reference's prefill == decode property, README.md:256-272);
+// decode() replays a hipGraph of one step whose kernels read the position and
+// the token from device memory, so nothing is re-encoded per token.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "model_dev.h"
+#include "qh_internal.h"
+
+using qh::fail;
+
+namespace {
+
+struct Staged {
+  int format = -1;
+  int rows = 0, cols = 0, group = 0;
+  void* data = nullptr;
+  float* scales = nullptr;
+  float* zeros = nullptr;
+};
+
+const char* const kLayerNames[] = {
+    "input_layernorm.weight", "self_attn.q_proj.weight", "self_attn.q_proj.bias",
+    "self_attn.k_proj.weight", "self_attn.k_proj.bias",  "self_attn.v_proj.weight",
+    "self_attn.v_proj.bias",   "self_attn.o_proj.weight", "post_attention_layernorm.weight",
+    "mlp.gate_proj.weight",    "mlp.up_proj.weight",      "mlp.down_proj.weight"};
+
+bool is_matrix_format(int f) { return f == QH_FMT_F16 || f == QH_FMT_INT8 || f == QH_FMT_INT4; }
+
+size_t data_bytes(int format, size_t rows, size_t cols) {
+  switch (format) {
+    case QH_FMT_F32: return rows * cols * 4;
+    case QH_FMT_F16:
+    case QH_FMT_BF16: return rows * cols * 2;
+    case QH_FMT_INT8: return rows * cols;
+    case QH_FMT_INT4: return rows * cols / 2;
+    default: return 0;
+  }
+}
+
+float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu, out;
+  if (exp == 0x1f) {
+    out = sign | 0x7f800000u | (mant << 13);
+  } else if (exp == 0) {
+    if (mant == 0) {
+      out = sign;
+    } else {
+      int e = -1;
+      do { mant <<= 1; e++; } while ((mant & 0x400u) == 0);
+      out = sign | ((uint32_t)(127 - 15 - e) << 23) | ((mant & 0x3ffu) << 13);
+    }
+  } else {
+    out = sign | ((exp - 15 + 127) << 23) | (mant << 13);
+  }
+  float f;
+  std::memcpy(&f, &out, 4);
+  return f;
+}
+
+}  // namespace
+
+struct qh_model {
+  qh_ctx* ctx = nullptr;
+  qh_config cfg{};
+  std::map<std::string, Staged> staged;
+  bool finalized = false;
+  std::vector<void*> allocs;
+  std::vector<qh::LayerDev> layers;
+  qh::ModelDev dev{};
+  size_t bytes = 0;
+  int live_caches = 0;
+
+  int alloc(size_t n, void** p) {
+    if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
+    allocs.push_back(*p);
+    bytes += n;
+    return QH_OK;
+  }
+  // Moves a staged buffer into the model's permanent set.
+  void keep(void* p) {
+    if (p) allocs.push_back(p);
+  }
+};
+
+struct qh_cache {
+  qh_model* m = nullptr;
+  qh::CacheDev dev{};
+  int length = 0;
+  std::vector<void*> allocs;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  bool busy = false;
+  int pending_start = 0, pending_steps = 0;
+  float* d_hidden = nullptr;
+  size_t hidden_cap = 0;
+  int32_t* h_pinned = nullptr;  // [0..1] state staging, [2] argmax readback
+
+  int alloc(size_t n, void** p) {
+    if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
+    allocs.push_back(*p);
+    return QH_OK;
+  }
+};
+
+static void free_staged(Staged& s) {
+  hipFree(s.data);
+  hipFree(s.scales);
+  hipFree(s.zeros);
+  s = Staged{};
+}
+
+extern "C" {
+
+int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out) {
+  QH_CHECK(ctx && cfg && out, QH_ERR_INVALID, "model_create needs a context, a config and an output");
+  *out = nullptr;
+  const qh_config& c = *cfg;
+  QH_CHECK(c.hidden > 0 && c.intermediate > 0 && c.layers > 0 && c.heads > 0 && c.kv_heads > 0 &&
+               c.vocab > 0 && c.max_positions > 0,
+           QH_ERR_INVALID, "config dimensions must be positive");
+  QH_CHECK(c.head_dim == 64 && c.hidden == c.heads * c.head_dim, QH_ERR_INVALID,
+           "the kernels implement head_dim 64 with hidden = heads * head_dim (got %d, %d x %d)",
+           c.hidden, c.heads, c.head_dim);
+  QH_CHECK(c.heads % c.kv_heads == 0 && c.heads / c.kv_heads <= 8, QH_ERR_INVALID,
+           "num_attention_heads %d is not divisible by num_key_value_heads %d (or groups > 8)",
+           c.heads, c.kv_heads);
+  QH_CHECK(c.hidden % 32 == 0 && c.intermediate % 32 == 0 && c.hidden <= 16384 &&
+               c.intermediate <= 16384,
+           QH_ERR_INVALID, "hidden and intermediate must be multiples of 32 up to 16384");
+  qh_model* m = new qh_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  *out = m;
+  return QH_OK;
+}
+
+int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t rows, int32_t cols,
+                        int32_t group, const void* h_data, const float* h_scales,
+                        const float* h_zeros) {
+  QH_CHECK(m && name && h_data, QH_ERR_INVALID, "set_tensor needs a model, a name and data");
+  QH_CHECK(!m->finalized, QH_ERR_STATE, "model is finalized; tensors are immutable");
+  const qh_config& c = m->cfg;
+  const int kv_dim = c.kv_heads * c.head_dim;
+  const std::string n = name;
+  // Expected shape and whether a matrix format is allowed.
+  int er = 0, ec = 0;
+  bool matrix = false, bf16 = false;
+  if (n == "model.embed_tokens.weight") {
+    er = c.vocab, ec = c.hidden, bf16 = true;
+  } else if (n == "lm_head.weight") {
+    er = c.vocab, ec = c.hidden, matrix = true;
+  } else if (n == "model.norm.weight") {
+    er = c.hidden, ec = 1;
+  } else if (n.rfind("model.layers.", 0) == 0) {
+    const char* p = name + 13;
+    char* end = nullptr;
+    const long L = strtol(p, &end, 10);
+    QH_CHECK(end != p && *end == '.' && L >= 0 && L < c.layers, QH_ERR_INVALID,
+             "unexpected tensor %s", name);
+    const std::string suffix = end + 1;
+    if (suffix == "input_layernorm.weight" || suffix == "post_attention_layernorm.weight") {
+      er = c.hidden, ec = 1;
+    } else if (suffix == "self_attn.q_proj.bias") {
+      er = c.hidden, ec = 1;
+    } else if (suffix == "self_attn.k_proj.bias" || suffix == "self_attn.v_proj.bias") {
+      er = kv_dim, ec = 1;
+    } else if (suffix == "self_attn.q_proj.weight" || suffix == "self_attn.o_proj.weight") {
+      er = c.hidden, ec = c.hidden, matrix = true;
+    } else if (suffix == "self_attn.k_proj.weight" || suffix == "self_attn.v_proj.weight") {
+      er = kv_dim, ec = c.hidden, matrix = true;
+    } else if (suffix == "mlp.gate_proj.weight" || suffix == "mlp.up_proj.weight") {
+      er = c.intermediate, ec = c.hidden, matrix = true;
+    } else if (suffix == "mlp.down_proj.weight") {
+      er = c.hidden, ec = c.intermediate, matrix = true;
+    } else {
+      return fail(QH_ERR_INVALID, "unexpected tensor %s", name);
+    }
+  } else {
+    return fail(QH_ERR_INVALID, "unexpected tensor %s", name);
+  }
+  const bool vector = ec == 1;
+  if (vector) {
+    QH_CHECK(format == QH_FMT_F32 && (size_t)rows * cols == (size_t)er, QH_ERR_INVALID,
+             "%s: expected f32 [%d], got format %d [%d, %d]", name, er, format, rows, cols);
+    rows = er, cols = 1;
+  } else {
+    QH_CHECK(rows == er && cols == ec, QH_ERR_INVALID, "%s: expected shape [%d,%d], got [%d,%d]",
+             name, er, ec, rows, cols);
+    if (bf16) {
+      QH_CHECK(format == QH_FMT_BF16, QH_ERR_INVALID, "%s is the bf16 gather table", name);
+    } else {
+      QH_CHECK(matrix && is_matrix_format(format), QH_ERR_INVALID,
+               "%s must be f16, int8 or int4 (format %d)", name, format);
+      qh_weight w{format, rows, cols, format == QH_FMT_INT4 ? group : 0, (const void*)16, nullptr, nullptr};
+      w.d_scales = (const float*)16;
+      w.d_zeros = (const float*)16;
+      qh::DMat probe;
+      int rc = qh::make_dmat(&w, &probe);
+      if (rc) return fail(rc, "%s: %s", name, qh_last_error());
+      QH_CHECK(format == QH_FMT_F16 || h_scales, QH_ERR_INVALID, "%s needs scales", name);
+      QH_CHECK(format != QH_FMT_INT4 || h_zeros, QH_ERR_INVALID, "%s needs zero points", name);
+    }
+  }
+  QH_HIP(hipSetDevice(m->ctx->device));
+  Staged s;
+  s.format = format;
+  s.rows = rows;
+  s.cols = cols;
+  s.group = format == QH_FMT_INT4 ? group : 0;
+  const size_t nb = data_bytes(format, rows, cols);
+  const size_t ns = format == QH_FMT_INT8 ? (size_t)rows : format == QH_FMT_INT4 ? (size_t)rows * (cols / group) : 0;
+  bool ok = hipMalloc(&s.data, nb) == hipSuccess &&
+            hipMemcpy(s.data, h_data, nb, hipMemcpyHostToDevice) == hipSuccess;
+  if (ok && ns) {
+    ok = hipMalloc((void**)&s.scales, ns * 4) == hipSuccess &&
+         hipMemcpy(s.scales, h_scales, ns * 4, hipMemcpyHostToDevice) == hipSuccess;
+  }
+  if (ok && format == QH_FMT_INT4) {
+    ok = hipMalloc((void**)&s.zeros, ns * 4) == hipSuccess &&
+         hipMemcpy(s.zeros, h_zeros, ns * 4, hipMemcpyHostToDevice) == hipSuccess;
+  }
+  if (!ok) {
+    free_staged(s);
+    return fail(QH_ERR_NOMEM, "uploading %s failed", name);
+  }
+  auto it = m->staged.find(n);
+  if (it != m->staged.end()) free_staged(it->second);
+  m->staged[n] = s;
+  return QH_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int dmat_of(const Staged& s, void* data, float* scales, float* zeros, int rows, qh::DMat* out) {
+  qh_weight w{s.format, rows, s.cols, s.group, data, scales, zeros};
+  return qh::make_dmat(&w, out);
+}
+
+// Stacks matrices of one format and width row-wise into a new buffer.
+int stack_rows(qh_model* m, const std::vector<const Staged*>& parts, qh::DMat* out) {
+  const Staged& a = *parts[0];
+  int rows = 0;
+  for (const Staged* p : parts) {
+    QH_CHECK(p->format == a.format && p->cols == a.cols && p->group == a.group, QH_ERR_INVALID,
+             "fused projections must share format, width and group");
+    rows += p->rows;
+  }
+  const size_t rb = data_bytes(a.format, 1, a.cols);
+  const size_t gpr = a.format == QH_FMT_INT4 ? (size_t)(a.cols / a.group) : 1;
+  void* data = nullptr;
+  float *scales = nullptr, *zeros = nullptr;
+  int rc = m->alloc(rb * rows, &data);
+  if (!rc && a.format != QH_FMT_F16) rc = m->alloc(gpr * rows * 4, (void**)&scales);
+  if (!rc && a.format == QH_FMT_INT4) rc = m->alloc(gpr * rows * 4, (void**)&zeros);
+  if (rc) return rc;
+  size_t r0 = 0;
+  for (const Staged* p : parts) {
+    QH_HIP(hipMemcpy((char*)data + r0 * rb, p->data, rb * p->rows, hipMemcpyDeviceToDevice));
+    if (scales) QH_HIP(hipMemcpy(scales + r0 * gpr, p->scales, gpr * p->rows * 4, hipMemcpyDeviceToDevice));
+    if (zeros) QH_HIP(hipMemcpy(zeros + r0 * gpr, p->zeros, gpr * p->rows * 4, hipMemcpyDeviceToDevice));
+    r0 += p->rows;
+  }
+  return dmat_of(a, data, scales, zeros, rows, out);
+}
+
+// Interleaves the rows of two same-shape matrices: row 2i = a[i], row 2i+1 = b[i].
+int interleave_rows(qh_model* m, const Staged& a, const Staged& b, qh::DMat* out) {
+  QH_CHECK(a.format == b.format && a.cols == b.cols && a.group == b.group && a.rows == b.rows,
+           QH_ERR_INVALID, "gate and up projections must share format and shape");
+  const size_t rb = data_bytes(a.format, 1, a.cols);
+  const size_t gpr = a.format == QH_FMT_INT4 ? (size_t)(a.cols / a.group) : 1;
+  const int rows = 2 * a.rows;
+  void* data = nullptr;
+  float *scales = nullptr, *zeros = nullptr;
+  int rc = m->alloc(rb * rows, &data);
+  if (!rc && a.format != QH_FMT_F16) rc = m->alloc(gpr * rows * 4, (void**)&scales);
+  if (!rc && a.format == QH_FMT_INT4) rc = m->alloc(gpr * rows * 4, (void**)&zeros);
+  if (rc) return rc;
+  for (int k = 0; k < 2; k++) {
+    const Staged& s = k == 0 ? a : b;
+    QH_HIP(hipMemcpy2D((char*)data + k * rb, 2 * rb, s.data, rb, rb, s.rows, hipMemcpyDeviceToDevice));
+    if (scales)
+      QH_HIP(hipMemcpy2D((char*)scales + k * gpr * 4, 2 * gpr * 4, s.scales, gpr * 4, gpr * 4, s.rows,
+                         hipMemcpyDeviceToDevice));
+    if (zeros)
+      QH_HIP(hipMemcpy2D((char*)zeros + k * gpr * 4, 2 * gpr * 4, s.zeros, gpr * 4, gpr * 4, s.rows,
+                         hipMemcpyDeviceToDevice));
+  }
+  return dmat_of(a, data, scales, zeros, rows, out);
+}
+
+}  // namespace
+
+extern "C" {
+
+int qh_model_finalize(qh_model* m) {
+  QH_CHECK(m, QH_ERR_INVALID, "model is NULL");
+  QH_CHECK(!m->finalized, QH_ERR_STATE, "model is already finalized");
+  const qh_config& c = m->cfg;
+  // Every tensor the architecture implies must be present (config.js:126-152).
+  std::vector<std::string> missing;
+  auto need = [&](const std::string& n) {
+    if (!m->staged.count(n)) missing.push_back(n);
+  };
+  need("model.embed_tokens.weight");
+  need("lm_head.weight");
+  need("model.norm.weight");
+  for (int L = 0; L < c.layers; L++)
+    for (const char* s : kLayerNames) need("model.layers." + std::to_string(L) + "." + s);
+  if (!missing.empty()) {
+    std::string list;
+    for (size_t i = 0; i < missing.size() && i < 5; i++) list += (i ? ", " : "") + missing[i];
+    return fail(QH_ERR_STATE, "missing %zu tensors: %s%s", missing.size(), list.c_str(),
+                missing.size() > 5 ? ", ..." : "");
+  }
+  QH_HIP(hipSetDevice(m->ctx->device));
+  const int kv_dim = c.kv_heads * c.head_dim;
+  m->layers.resize(c.layers);
+  std::vector<std::string> consumed;
+  for (int L = 0; L < c.layers; L++) {
+    const std::string p = "model.layers." + std::to_string(L) + ".";
+    auto& S = m->staged;
+    qh::LayerDev& d = m->layers[L];
+    int rc = stack_rows(m, {&S[p + "self_attn.q_proj.weight"], &S[p + "self_attn.k_proj.weight"],
+                            &S[p + "self_attn.v_proj.weight"]},
+                        &d.qkv);
+    if (!rc) rc = interleave_rows(m, S[p + "mlp.gate_proj.weight"], S[p + "mlp.up_proj.weight"], &d.gu);
+    if (rc) return rc;
+    const Staged& o = S[p + "self_attn.o_proj.weight"];
+    const Staged& dn = S[p + "mlp.down_proj.weight"];
+    if ((rc = dmat_of(o, o.data, o.scales, o.zeros, o.rows, &d.o))) return rc;
+    if ((rc = dmat_of(dn, dn.data, dn.scales, dn.zeros, dn.rows, &d.down))) return rc;
+    float* bias = nullptr;
+    if ((rc = m->alloc((size_t)(c.hidden + 2 * kv_dim) * 4, (void**)&bias))) return rc;
+    QH_HIP(hipMemcpy(bias, S[p + "self_attn.q_proj.bias"].data, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice));
+    QH_HIP(hipMemcpy(bias + c.hidden, S[p + "self_attn.k_proj.bias"].data, (size_t)kv_dim * 4, hipMemcpyDeviceToDevice));
+    QH_HIP(hipMemcpy(bias + c.hidden + kv_dim, S[p + "self_attn.v_proj.bias"].data, (size_t)kv_dim * 4, hipMemcpyDeviceToDevice));
+    d.qkv_bias = bias;
+    d.in_norm = static_cast<const float*>(S[p + "input_layernorm.weight"].data);
+    d.post_norm = static_cast<const float*>(S[p + "post_attention_layernorm.weight"].data);
+    for (const char* keep : {"self_attn.o_proj.weight", "mlp.down_proj.weight", "input_layernorm.weight",
+                             "post_attention_layernorm.weight"}) {
+      Staged& s = S[p + keep];
+      m->keep(s.data);
+      m->keep(s.scales);
+      m->keep(s.zeros);
+      m->bytes += data_bytes(s.format, s.rows, s.cols);
+      s = Staged{};
+    }
+    for (const char* used : {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                             "mlp.gate_proj.weight", "mlp.up_proj.weight", "self_attn.q_proj.bias",
+                             "self_attn.k_proj.bias", "self_attn.v_proj.bias"}) {
+      consumed.push_back(p + used);
+    }
+  }
+  Staged& lm = m->staged["lm_head.weight"];
+  int rc = dmat_of(lm, lm.data, lm.scales, lm.zeros, lm.rows, &m->dev.lm_head);
+  if (rc) return rc;
+  m->keep(lm.data), m->keep(lm.scales), m->keep(lm.zeros);
+  m->bytes += data_bytes(lm.format, lm.rows, lm.cols);
+  lm = Staged{};
+  Staged& fn = m->staged["model.norm.weight"];
+  m->dev.final_norm = static_cast<const float*>(fn.data);
+  m->keep(fn.data);
+  fn = Staged{};
+  Staged& em = m->staged["model.embed_tokens.weight"];
+  m->dev.embed = static_cast<const uint16_t*>(em.data);
+  m->keep(em.data);
+  m->bytes += data_bytes(QH_FMT_BF16, em.rows, em.cols);
+  em = Staged{};
+  for (auto& n : consumed) free_staged(m->staged[n]);
+  m->staged.clear();
+
+  // Rope tables from host f64 (src/core/ops.js:123-136, src/gpu/model.js:201-205).
+  std::vector<float> cs((size_t)c.max_positions * 32), sn((size_t)c.max_positions * 32);
+  if ((rc = qh_rope_tables(c.head_dim, c.rope_theta, c.max_positions, cs.data(), sn.data()))) return rc;
+  float *dcos = nullptr, *dsin = nullptr;
+  if ((rc = m->alloc(cs.size() * 4, (void**)&dcos)) || (rc = m->alloc(sn.size() * 4, (void**)&dsin))) return rc;
+  QH_HIP(hipMemcpy(dcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  QH_HIP(hipMemcpy(dsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+
+  qh::ModelDev& d = m->dev;
+  d.hidden = c.hidden;
+  d.intermediate = c.intermediate;
+  d.layers = c.layers;
+  d.heads = c.heads;
+  d.kv_heads = c.kv_heads;
+  d.head_dim = c.head_dim;
+  d.vocab = c.vocab;
+  d.max_positions = c.max_positions;
+  d.eps = c.eps;
+  d.layers_host = m->layers.data();
+  d.rope_cos = dcos;
+  d.rope_sin = dsin;
+  m->finalized = true;
+  return QH_OK;
+}
+
+int qh_model_free(qh_model* m) {
+  if (!m) return QH_OK;
+  QH_CHECK(m->live_caches == 0, QH_ERR_STATE, "free the model's %d caches first", m->live_caches);
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+  for (auto& kv : m->staged) free_staged(kv.second);
+  for (void* p : m->allocs) hipFree(p);
+  delete m;
+  return QH_OK;
+}
+
+int qh_model_bytes(qh_model* m, size_t* bytes) {
+  QH_CHECK(m && bytes, QH_ERR_INVALID, "model_bytes needs a model and an output");
+  *bytes = m->bytes;
+  return QH_OK;
+}
+
+int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
+  QH_CHECK(m && out, QH_ERR_INVALID, "cache_create needs a model and an output");
+  *out = nullptr;
+  QH_CHECK(m->finalized, QH_ERR_STATE, "finalize the model before creating a cache");
+  QH_CHECK(capacity >= 1, QH_ERR_RANGE, "cache capacity must be a positive integer, got %d", capacity);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  const qh::ModelDev& md = m->dev;
+  qh_cache* c = new qh_cache();
+  c->m = m;
+  qh::CacheDev& d = c->dev;
+  d.capacity = capacity;
+  const int kv_dim = md.kv_heads * md.head_dim;
+  int nchunks, cps, splits;
+  qh::attn_splits_host(capacity, &nchunks, &cps, &splits);
+  const size_t kv_bytes = (size_t)md.layers * 2 * md.kv_heads * capacity * md.head_dim * 2;
+  int rc = QH_OK;
+  auto A = [&](size_t n, void** p) {
+    if (!rc) rc = c->alloc(n, p);
+  };
+  A(kv_bytes, (void**)&d.kv);
+  A(256, (void**)&d.state);
+  A((size_t)(capacity + 1) * 4, (void**)&d.tokens);
+  A((size_t)capacity * 4, (void**)&d.pred);
+  A((size_t)md.hidden * 4, (void**)&d.x);
+  A((size_t)(md.hidden + 2 * kv_dim) * 4, (void**)&d.qkv);
+  A((size_t)md.hidden * 4, (void**)&d.attn);
+  A((size_t)md.intermediate * 4, (void**)&d.h);
+  A((size_t)md.vocab * 4, (void**)&d.logits);
+  A((size_t)splits * md.kv_heads * (md.heads / md.kv_heads) * (md.head_dim + 2) * 4, (void**)&d.attn_partials);
+  A(256, (void**)&d.attn_counters);
+  A(qh::lm_partials_bytes(md), &d.lm_partials);
+  A(256, (void**)&d.lm_counter);
+  if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
+    rc = fail(QH_ERR_NOMEM, "pinned allocation failed");
+  }
+  if (!rc && (hipMemset(d.kv, 0, kv_bytes) != hipSuccess || hipMemset(d.state, 0, 256) != hipSuccess ||
+              hipMemset(d.tokens, 0, (size_t)(capacity + 1) * 4) != hipSuccess ||
+              hipMemset(d.pred, 0, (size_t)capacity * 4) != hipSuccess ||
+              hipMemset(d.attn_counters, 0, 256) != hipSuccess ||
+              hipMemset(d.lm_counter, 0, 256) != hipSuccess)) {
+    rc = fail(QH_ERR_DEVICE, "clearing the cache failed");
+  }
+  d.lm_blocks = qh::lm_head_blocks(md);
+  if (rc) {
+    for (void* p : c->allocs) hipFree(p);
+    if (c->h_pinned) hipHostFree(c->h_pinned);
+    delete c;
+    return rc;
+  }
+  m->live_caches++;
+  *out = c;
+  return QH_OK;
+}
+
+int qh_cache_free(qh_cache* c) {
+  if (!c) return QH_OK;
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight; collect it first");
+  hipSetDevice(c->m->ctx->device);
+  hipStreamSynchronize(c->m->ctx->stream);
+  if (c->exec) hipGraphExecDestroy(c->exec);
+  if (c->graph) hipGraphDestroy(c->graph);
+  for (void* p : c->allocs) hipFree(p);
+  hipFree(c->d_hidden);
+  hipHostFree(c->h_pinned);
+  c->m->live_caches--;
+  delete c;
+  return QH_OK;
+}
+
+int qh_cache_length(qh_cache* c, int32_t* length) {
+  QH_CHECK(c && length, QH_ERR_INVALID, "cache_length needs a cache and an output");
+  *length = c->length;
+  return QH_OK;
+}
+
+int qh_cache_set_length(qh_cache* c, int32_t length) {
+  QH_CHECK(c, QH_ERR_INVALID, "cache is NULL");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight");
+  QH_CHECK(length >= 0 && length <= c->length, QH_ERR_RANGE,
+           "can rewind to 0..%d positions, not %d", c->length, length);
+  c->length = length;
+  return QH_OK;
+}
+
+int qh_cache_present(qh_cache* c, int32_t layer, float* h_key, float* h_value) {
+  QH_CHECK(c && h_key && h_value, QH_ERR_INVALID, "cache_present needs a cache and outputs");
+  const qh::ModelDev& md = c->m->dev;
+  QH_CHECK(layer >= 0 && layer < md.layers, QH_ERR_RANGE, "layer %d out of range", layer);
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight");
+  const size_t kv_layer = (size_t)md.kv_heads * c->dev.capacity * md.head_dim;
+  std::vector<uint16_t> buf(2 * kv_layer);
+  QH_HIP(hipStreamSynchronize(c->m->ctx->stream));
+  QH_HIP(hipMemcpy(buf.data(), c->dev.kv + (size_t)layer * 2 * kv_layer, buf.size() * 2, hipMemcpyDeviceToHost));
+  const int n = c->length, hd = md.head_dim;
+  for (int h = 0; h < md.kv_heads; h++) {
+    for (int t = 0; t < n; t++) {
+      for (int i = 0; i < hd; i++) {
+        const size_t from = ((size_t)h * c->dev.capacity + t) * hd + i;
+        const size_t to = ((size_t)h * n + t) * hd + i;
+        h_key[to] = f16_to_f32(buf[from]);
+        h_value[to] = f16_to_f32(buf[kv_layer + from]);
+      }
+    }
+  }
+  return QH_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Guards of GpuModel.#forward (src/gpu/model.js:247-254).
+int check_room(qh_cache* c, int add) {
+  const int total = c->length + add;
+  QH_CHECK(total <= c->dev.capacity, QH_ERR_RANGE, "cache holds %d of %d; cannot add %d", c->length,
+           c->dev.capacity, add);
+  QH_CHECK(total <= c->m->dev.max_positions, QH_ERR_RANGE,
+           "position %d exceeds the %d-entry rope table", total, c->m->dev.max_positions);
+  return QH_OK;
+}
+
+int set_state(qh_cache* c, int pos, int forced) {
+  c->h_pinned[0] = pos;
+  c->h_pinned[1] = forced;
+  QH_HIP(hipMemcpyAsync(c->dev.state, c->h_pinned, 8, hipMemcpyHostToDevice, c->m->ctx->stream));
+  return QH_OK;
+}
+
+int finish_forward(qh_cache* c, int seq, float* h_logits, int32_t* h_argmax) {
+  hipStream_t s = c->m->ctx->stream;
+  const int last = c->length + seq - 1;
+  if (h_logits) {
+    QH_HIP(hipMemcpyAsync(h_logits, c->dev.logits, (size_t)c->m->dev.vocab * 4, hipMemcpyDeviceToHost, s));
+  }
+  if (h_argmax) QH_HIP(hipMemcpyAsync(c->h_pinned + 2, c->dev.pred + last, 4, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
+  if (h_argmax) *h_argmax = c->h_pinned[2];
+  c->length += seq;
+  return QH_OK;
+}
+
+struct BusyGuard {
+  qh_cache* c;
+  explicit BusyGuard(qh_cache* c_) : c(c_) { c->busy = true; }
+  ~BusyGuard() { c->busy = false; }
+};
+
+}  // namespace
+
+extern "C" {
+
+int qh_forward(qh_model* m, qh_cache* c, const float* h_hidden, int32_t seq, float* h_logits,
+               int32_t* h_argmax) {
+  QH_CHECK(m && c && h_hidden && c->m == m, QH_ERR_INVALID, "forward needs a model, its cache and input");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(seq >= 1, QH_ERR_INVALID, "forward: need at least one position");
+  int rc = check_room(c, seq);
+  if (rc) return rc;
+  BusyGuard guard(c);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  const size_t need = (size_t)seq * m->dev.hidden * 4;
+  if (need > c->hidden_cap) {
+    QH_HIP(hipStreamSynchronize(s));
+    hipFree(c->d_hidden);
+    c->d_hidden = nullptr;
+    c->hidden_cap = 0;
+    QH_HIP(hipMalloc((void**)&c->d_hidden, need));
+    c->hidden_cap = need;
+  }
+  QH_HIP(hipMemcpyAsync(c->d_hidden, h_hidden, need, hipMemcpyHostToDevice, s));
+  if ((rc = set_state(c, c->length, INT_MAX))) return rc;
+  const bool want = h_logits || h_argmax;
+  for (int t = 0; t < seq; t++) {
+    QH_HIP(hipMemcpyAsync(c->dev.x, c->d_hidden + (size_t)t * m->dev.hidden, (size_t)m->dev.hidden * 4,
+                          hipMemcpyDeviceToDevice, s));
+    QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_HIDDEN, want && t == seq - 1));
+  }
+  return finish_forward(c, seq, h_logits, h_argmax);
+}
+
+int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t seq, float* h_logits,
+                      int32_t* h_argmax) {
+  QH_CHECK(m && c && h_ids && c->m == m, QH_ERR_INVALID, "forward needs a model, its cache and ids");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(seq >= 1, QH_ERR_INVALID, "forward: need at least one token");
+  for (int t = 0; t < seq; t++) {
+    QH_CHECK(h_ids[t] >= 0 && h_ids[t] < m->dev.vocab, QH_ERR_RANGE,
+             "token %d at position %d is outside the vocabulary", h_ids[t], t);
+  }
+  int rc = check_room(c, seq);
+  if (rc) return rc;
+  BusyGuard guard(c);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, h_ids, (size_t)seq * 4, hipMemcpyHostToDevice, s));
+  if ((rc = set_state(c, c->length, c->length + seq))) return rc;
+  const bool want = h_logits || h_argmax;
+  for (int t = 0; t < seq; t++) {
+    QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, want && t == seq - 1));
+  }
+  return finish_forward(c, seq, h_logits, h_argmax);
+}
+
+int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps) {
+  QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode needs a model and its cache");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(steps >= 1, QH_ERR_INVALID, "decode needs steps >= 1");
+  QH_CHECK(first_token >= 0 && first_token < m->dev.vocab, QH_ERR_RANGE,
+           "token %d is outside the vocabulary", first_token);
+  int rc = check_room(c, steps);
+  if (rc) return rc;
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  if (!c->exec) {
+    QH_HIP(hipStreamSynchronize(s));
+    QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    hipError_t e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, true);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(s, &g);
+    QH_HIP(e);
+    QH_HIP(e2);
+    c->graph = g;
+    QH_HIP(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
+  }
+  c->h_pinned[3] = first_token;
+  QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s));
+  if ((rc = set_state(c, c->length, c->length + 1))) return rc;
+  for (int i = 0; i < steps; i++) QH_HIP(hipGraphLaunch(c->exec, s));
+  c->busy = true;
+  c->pending_start = c->length;
+  c->pending_steps = steps;
+  c->length += steps;
+  return QH_OK;
+}
+
+int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens) {
+  QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode needs a model and its cache");
+  QH_CHECK(c->busy && c->pending_steps > 0, QH_ERR_STATE, "no decode in flight");
+  QH_CHECK(steps == c->pending_steps, QH_ERR_INVALID, "collect %d steps, %d were launched", steps,
+           c->pending_steps);
+  hipStream_t s = m->ctx->stream;
+  hipError_t e = hipSuccess;
+  if (h_tokens) e = hipMemcpyAsync(h_tokens, c->dev.pred + c->pending_start, (size_t)steps * 4, hipMemcpyDeviceToHost, s);
+  hipError_t e2 = hipStreamSynchronize(s);
+  c->busy = false;
+  c->pending_steps = 0;
+  QH_HIP(e);
+  QH_HIP(e2);
+  return QH_OK;
+}
+
+int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int32_t* h_tokens) {
+  int rc = qh_decode_launch(m, c, first_token, steps);
+  if (rc) return rc;
+  return qh_decode_collect(m, c, steps, h_tokens);
+}
+
+}  // extern "C"

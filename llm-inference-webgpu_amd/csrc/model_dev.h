@@ -1,0 +1,63 @@
+// Device-side description of a finalized model and of one KV cache with its
+// decode state: plain pointers and shapes, built once by model.cpp (the
+// persistent equivalent of the reference's bind groups and uniform pool,
+// src/gpu/device.js:187-206, src/gpu/model.js:100-124) and read by the
+// launchers in decode.hip.
+#pragma once
+
+#include "qh_internal.h"
+
+namespace qh {
+
+struct LayerDev {
+  DMat qkv;          // [hidden + 2*kv_dim, hidden]: q rows, then k rows, then v rows
+  DMat o;            // [hidden, hidden]
+  DMat gu;           // [2*intermediate, hidden]: row 2i = gate row i, row 2i+1 = up row i
+  DMat down;         // [hidden, intermediate]
+  const float* qkv_bias;   // [hidden + 2*kv_dim]
+  const float* in_norm;    // [hidden]
+  const float* post_norm;  // [hidden]
+};
+
+struct ModelDev {
+  int hidden, intermediate, layers, heads, kv_heads, head_dim, vocab, max_positions;
+  double eps;
+  const LayerDev* layers_host;  // host array of per-layer descriptors
+  DMat lm_head;                 // [vocab, hidden]
+  const float* final_norm;
+  const uint16_t* embed;        // [vocab, hidden] bf16
+  const float* rope_cos;        // [max_positions, 32]
+  const float* rope_sin;
+};
+
+struct CacheDev {
+  int capacity;
+  uint16_t* kv;        // [layers][2][kv_heads][capacity][64] f16
+  int* state;          // [0] position, [1] forced length (tokens below it are the caller's)
+  int* tokens;         // [capacity + 1] token consumed at each position
+  int* pred;           // [capacity] argmax after each position
+  float* x;            // [hidden] residual stream
+  float* qkv;          // [hidden + 2*kv_dim]
+  float* attn;         // [hidden]
+  float* h;            // [intermediate]
+  float* logits;       // [vocab]
+  float* attn_partials;
+  int* attn_counters;  // [kv_heads]
+  void* lm_partials;   // argmax block partials
+  int* lm_counter;
+  int lm_blocks;
+};
+
+// How a step obtains its input row.
+enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1 };
+
+// Launches one decode position: [gather] -> layers -> (lm_head + argmax, or a
+// position advance when `logits` is false). With STEP_HIDDEN the caller has
+// already written the input row into cache.x.
+hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
+                        bool logits);
+// Blocks the lm_head launch uses (sizes lm_partials).
+int lm_head_blocks(const ModelDev& m);
+size_t lm_partials_bytes(const ModelDev& m);
+
+}  // namespace qh

@@ -1,0 +1,94 @@
+// Host-side internals of libqwen_hip.so: the context, error reporting, and the
+// launchers the C-ABI entry points call. Device code lives in *.hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "qwen_hip.h"
+
+namespace qh {
+
+// Records a message for qh_last_error() on this thread and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+#define QH_HIP(expr)                                                               \
+  do {                                                                             \
+    hipError_t qh_e_ = (expr);                                                     \
+    if (qh_e_ != hipSuccess)                                                       \
+      return ::qh::fail(QH_ERR_DEVICE, "%s failed: %s", #expr, hipGetErrorString(qh_e_)); \
+  } while (0)
+
+#define QH_CHECK(cond, code, ...)                 \
+  do {                                            \
+    if (!(cond)) return ::qh::fail(code, __VA_ARGS__); \
+  } while (0)
+
+// Device view of one weight matrix, in the reference quantizer's layout.
+// A "chunk" is 16 bytes of one row: 8 f16, 16 int8 or 32 int4 weights.
+struct DMat {
+  int32_t format;       // QH_FMT_F16 | QH_FMT_INT8 | QH_FMT_INT4
+  const uint8_t* data;
+  const float* scales;  // int8: [rows]; int4: [rows * gpr]
+  const float* zeros;   // int4: [rows * gpr]
+  int32_t rows, cols;
+  int32_t row_bytes;    // bytes of one row
+  int32_t nchunks;      // row_bytes / 16
+  int32_t gpr;          // int4 groups per row
+  int32_t cpg;          // int4 chunks per group (group / 32)
+};
+
+// Checks a qh_weight against what the kernels support and fills a DMat.
+int make_dmat(const qh_weight* w, DMat* out);
+int weights_per_chunk(int format);
+
+}  // namespace qh
+
+struct qh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string name, arch;
+  int cus = 0;
+  size_t hbm_bytes = 0;
+  size_t lds_per_block = 0;
+  // Small reusable scratch for operators that reduce across blocks (argmax).
+  void* d_scratch = nullptr;
+  size_t scratch_bytes = 0;
+  int32_t* h_pinned = nullptr;  // 4-byte pinned readback slots
+};
+
+struct qh_event {
+  hipEvent_t ev = nullptr;
+};
+
+// Kernel launchers (defined in the .hip files). They assume validated arguments.
+namespace qh {
+hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
+                         int seq);
+hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
+                                 size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
+hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
+                          int cols, double eps);
+hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float* sin_t, int rows,
+                       int heads, int head_dim, int base_pos);
+hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint16_t* kc,
+                            uint16_t* vc, int capacity, int kv_heads, int head_dim, int past,
+                            int seq);
+// Attention over an f16 head-major cache. `partials` must hold attention_partials_floats(...)
+// floats and `counters` seq*kv_heads ints, zeroed before first use (kernels leave them zeroed).
+hipError_t launch_attention(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc,
+                            int capacity, float* out, int seq, int past, int heads, int kv_heads,
+                            float* partials, int* counters);
+size_t attention_partials_floats(int seq, int heads, int kv_heads, int capacity);
+// Split structure of one query at context ctx (see attention.h).
+void attn_splits_host(int ctx, int* nchunks, int* cps, int* splits);
+hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
+hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n);
+// Argmax into d_out[0]; `scratch` holds argmax_scratch_bytes(n) bytes, counter zeroed.
+hipError_t launch_argmax(hipStream_t s, const float* v, int n, void* scratch, int32_t* d_out);
+size_t argmax_scratch_bytes(int n);
+}  // namespace qh

@@ -1,0 +1,209 @@
+"""End-to-end parity of the decode step against the CPU oracle: logits within
+the reference's model tolerance (test/model.test.js:39-40: logits 1e-4
+relative), greedy tokens identical, and the bit-exact properties the reference
+holds its GPU path to (prefill == incremental decode, web/model.html:169-198;
+every replay of a step equal, web/decode-profile.html:162-167)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_REL = 1e-4      # test/model.test.js:40
+
+
+def rel_err(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+
+
+def tiny(hip, **kw):
+    base = dict(hidden=128, intermediate=256, layers=2, heads=2, kv_heads=1, vocab=1000)
+    base.update(kw)
+    return hip.ModelConfig(**base)
+
+
+@pytest.fixture(scope="module", params=["f16", "int8", "int4"])
+def tiny_model(request, ctx, hip):
+    scheme = request.param
+    cfg = tiny(hip)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=3)
+    lm = "int8" if scheme != "f16" else "f16"
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, scheme, 128, lm), cfg, maxPositions=256)
+    oracle = O.OracleModel(cfg, ckpt, scheme=scheme, group=128, lm_head=lm, kv_f16=True)
+    yield cfg, model, oracle, scheme
+    model.destroy()
+
+
+def test_prompt_logits_and_greedy_tokens_match_oracle(hip, tiny_model):
+    cfg, model, oracle, scheme = tiny_model
+    prompt = hip.synth_tokens(3, "prompt", cfg.vocab, 12)
+    cache = model.newCache(64)
+    out = model.forward_tokens(prompt, cache)
+    ologits = oracle.forward(prompt, oracle.new_cache(64))
+    print(f"{scheme}: logits rel {rel_err(out['logits'], ologits):.2e}")
+    assert rel_err(out["logits"], ologits) <= LOGIT_REL
+    assert out["argmax"] == O.argmax(ologits) == int(np.argmax(out["logits"]))
+    gen = model.decode(cache, out["argmax"], 20)
+    want, _ = oracle.generate(prompt, 21)
+    assert [out["argmax"]] + list(gen[:-1]) == list(want[:-1])
+    assert gen[-1] == want[-1]
+    assert cache.length == 12 + 20
+    cache.destroy()
+
+
+def test_prefill_equals_incremental_decode_bitwise(hip, tiny_model):
+    cfg, model, _, _ = tiny_model
+    ids = hip.synth_tokens(5, "ids", cfg.vocab, 9)
+    full = model.newCache(16)
+    a = model.forward_tokens(ids, full)
+    inc = model.newCache(16)
+    model.forward_tokens(ids[:4], inc, wantLogits=False)
+    for t in ids[4:]:
+        b = model.forward_tokens([t], inc)
+    np.testing.assert_array_equal(a["logits"].view(np.uint32), b["logits"].view(np.uint32))
+    for L in range(cfg.layers):
+        pa, pb = full.present(L), inc.present(L)
+        np.testing.assert_array_equal(pa["key"].view(np.uint32), pb["key"].view(np.uint32))
+        np.testing.assert_array_equal(pa["value"].view(np.uint32), pb["value"].view(np.uint32))
+    full.destroy()
+    inc.destroy()
+
+
+def test_graph_replay_equals_direct_steps(hip, tiny_model):
+    cfg, model, _, _ = tiny_model
+    prompt = hip.synth_tokens(6, "p", cfg.vocab, 5)
+    c1, c2 = model.newCache(32), model.newCache(32)
+    first = model.forward_tokens(prompt, c1)["argmax"]
+    assert model.forward_tokens(prompt, c2)["argmax"] == first
+    graph = model.decode(c1, first, 10)
+    direct, tok = [], first
+    for _ in range(10):
+        tok = model.forward_tokens([tok], c2)["argmax"]
+        direct.append(tok)
+    assert list(graph) == direct
+    for L in range(cfg.layers):
+        np.testing.assert_array_equal(c1.present(L)["key"], c2.present(L)["key"])
+    c1.destroy()
+    c2.destroy()
+
+
+def test_hidden_input_equals_token_gather(hip, tiny_model):
+    cfg, model, _, _ = tiny_model
+    ckpt_embed = hip.synthesize_checkpoint(cfg, seed=3)["model.embed_tokens.weight"]
+    ids = hip.synth_tokens(8, "h", cfg.vocab, 4)
+    hidden = hip.bf16_to_f32(ckpt_embed[ids]).reshape(-1)
+    c1, c2 = model.newCache(8), model.newCache(8)
+    a = model.forward(hidden, 4, cache=c1)
+    b = model.forward_tokens(ids, c2)
+    np.testing.assert_array_equal(a["logits"].view(np.uint32), b["logits"].view(np.uint32))
+    c1.destroy()
+    c2.destroy()
+
+
+def test_rewind_replays_the_same_step(hip, tiny_model):
+    # The profiler's replay (web/decode-profile.html:151): rewinding the length and
+    # repeating a step reproduces its logits bit for bit.
+    cfg, model, _, _ = tiny_model
+    c = model.newCache(8)
+    model.forward_tokens([1, 2, 3], c)
+    a = model.forward_tokens([4], c)
+    c.length = 3
+    b = model.forward_tokens([4], c)
+    np.testing.assert_array_equal(a["logits"].view(np.uint32), b["logits"].view(np.uint32))
+    c.destroy()
+
+
+def test_errors_are_raised_before_any_work(hip, tiny_model):
+    cfg, model, _, _ = tiny_model
+    c = model.newCache(4)
+    with pytest.raises(hip.RangeError, match="cannot add"):
+        model.forward_tokens([1, 2, 3, 4, 5], c)
+    assert c.length == 0
+    with pytest.raises(hip.RangeError, match="outside the vocabulary"):
+        model.forward_tokens([cfg.vocab], c)
+    with pytest.raises(hip.RangeError):
+        model.decode(c, 1, 5)
+    model.decode_launch(c, 1, 2)
+    with pytest.raises(hip.BusyError):
+        model.forward_tokens([1], c)
+    model.decode_collect(c, 2)
+    assert c.length == 2
+    with pytest.raises(hip.RangeError):
+        c.length = 3
+    c.destroy()
+
+
+def test_rope_table_bound(ctx, hip):
+    cfg = tiny(hip, layers=1, vocab=256)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=1)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "int8", 128, "int8"), cfg, maxPositions=4)
+    c = model.newCache(8)
+    model.forward_tokens([1, 2, 3, 4], c)
+    with pytest.raises(hip.RangeError, match="rope table"):
+        model.forward_tokens([5], c)
+    c.destroy()
+    model.destroy()
+
+
+def test_missing_tensor_is_reported(ctx, hip):
+    cfg = tiny(hip, layers=1, vocab=256)
+    t = hip.device_tensors(hip.synthesize_checkpoint(cfg, seed=1), cfg, "int4", 128, "int8")
+    del t["model.layers.0.mlp.up_proj.weight"]
+    with pytest.raises(hip.QwenHipError, match="missing 1 tensors: model.layers.0.mlp.up_proj"):
+        hip.GpuModel.load(ctx, t, cfg, maxPositions=8)
+
+
+# ---------------------------------------------------------------- full size
+
+@pytest.fixture(scope="module")
+def full_ckpt(hip):
+    return hip.synthesize_checkpoint(hip.QWEN25_05B, seed=1)
+
+
+def test_config1_full_shape_greedy_matches_oracle(ctx, hip, full_ckpt):
+    """Config 1: 16 seeded prompt ids, 32 greedy tokens, Qwen2.5-0.5B shape. Weights are
+    the reference GPU path's f16; the oracle sees the same f16 weights and f16 cache."""
+    cfg = hip.QWEN25_05B
+    model = hip.GpuModel.load(ctx, hip.device_tensors(full_ckpt, cfg, "f16", 128, "f16"), cfg,
+                              maxPositions=64)
+    prompt = hip.synth_tokens(1, "config1.prompt", cfg.vocab, 16)
+    cache = model.newCache(48)
+    out = model.forward_tokens(prompt, cache)
+    gen = model.decode(cache, out["argmax"], 31)
+    tokens = [out["argmax"]] + list(gen)
+    oracle = O.OracleModel(cfg, full_ckpt, scheme="f16", lm_head="f16", kv_f16=True)
+    ocache = oracle.new_cache(48)
+    ologits = oracle.forward(prompt, ocache)
+    print(f"config1 logits rel {rel_err(out['logits'], ologits):.2e}")
+    assert rel_err(out["logits"], ologits) <= LOGIT_REL
+    want, _ = oracle.generate(prompt, 32)
+    assert tokens == list(want)
+    model.destroy()
+
+
+def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt):
+    """Config 4's model (int4-g128 layers, int8 output head, f16 cache) on a shorter
+    context: 64 prompt ids then 24 greedy tokens, plus the per-layer present K/V."""
+    cfg = hip.QWEN25_05B
+    model = hip.GpuModel.load(ctx, hip.device_tensors(full_ckpt, cfg, "int4", 128, "int8"), cfg,
+                              maxPositions=128)
+    prompt = hip.synth_tokens(4, "config4.prompt", cfg.vocab, 64)
+    cache = model.newCache(96)
+    out = model.forward_tokens(prompt, cache)
+    oracle = O.OracleModel(cfg, full_ckpt, scheme="int4", group=128, lm_head="int8", kv_f16=True)
+    ocache = oracle.new_cache(96)
+    ologits = oracle.forward(prompt, ocache)
+    print(f"config4 logits rel {rel_err(out['logits'], ologits):.2e}")
+    assert rel_err(out["logits"], ologits) <= LOGIT_REL
+    worst = 0.0
+    for L in range(cfg.layers):
+        for kind in ("key", "value"):
+            worst = max(worst, rel_err(cache.present(L)[kind], ocache.present(L)[kind]))
+    print(f"config4 worst per-layer present rel {worst:.2e}")
+    assert worst <= 5e-4      # PER_LAYER_REL, test/model.test.js:39
+    gen = model.decode(cache, out["argmax"], 23)
+    want, _ = oracle.generate(prompt, 24)
+    assert [out["argmax"]] + list(gen) == list(want)
+    model.destroy()
