@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Headline benchmark: batch-1 greedy decode tok/s of a Qwen2.5-0.5B-shaped model
+with int4-g128 layer weights and an int8 output head,
+on one MI355X through libqwen_hip.so.
+
+A step is one decode token: one replay of the hipGraph-captured decode step
+(gather -> 24 layers -> lm_head -> argmax -> next token, all on the device). The
+KV cache is first filled from a seeded 1024-token prompt (untimed); W warmup
+steps run and are rewound; then exactly K steps are timed with HIP events on the
+library's stream (and wall clock around them), inputs resident in HBM.
+
+Also reported on the same JSON line:
+  roofline       the dominant kernel of the step (by in-situ time), algorithmic
+                 bytes per launch over its average in-situ launch time, vs 8 TB/s
+  per_kernel_us  in-situ microseconds per token by kernel role (events around
+                 every launch, the reference's decode-profile split)
+  matvec_isolated  BASELINE config 2: int8 matvec with an f16 activation at the
+                 five layer shapes, one list-driven launch over >= 512 MiB of
+                 distinct matrices (larger than the 256 MB last-level cache)
+  cpu_baseline   the CPU oracle (a port of the reference's src/cpu path) timed on
+                 one host core over a bounded sample of the same workload
+
+Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "llm-inference-webgpu_amd"))
+
+import qwen_hip as H  # noqa: E402
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "batch-1 decode tok/s, Qwen2.5-0.5B int4/int8; matvec HBM GB/s vs peak"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def role_bytes(cfg, ctx_len, group=128):
+    """Algorithmic HBM bytes per launch of each decode role (int4-g128 layers, int8
+    head, f16 cache): weights + their scales/zeros once, plus the activations each
+    launch must read and write."""
+    d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
+
+    def int4(rows, cols):
+        return rows * cols // 2 + rows * (cols // group) * 8
+
+    f = 4
+    return {
+        "embed": d * 2 + d * f,
+        "qkv": int4(d + 2 * kv, d) + (d + 2 * kv) * f + 2 * d * f + (d + 2 * kv) * f,
+        "attention": 2 * ctx_len * kv * 2 + (d + 2 * kv) * f + 2 * kv * 2 + d * f,
+        "oproj": int4(d, d) + d * f + 2 * d * f,
+        "gateup": int4(2 * ffn, d) + 2 * d * f + ffn * f,
+        "down": int4(d, ffn) + ffn * f + 2 * d * f,
+        "head": V * d + V * f + 2 * d * f + V * f,
+    }
+
+
+def isolated_matvec(ctx, shapes, reps=5):
+    """Config 2: int8 weights, x ~ N(0,1) f16, rotation of distinct matrices >= 512 MiB."""
+    out = {}
+    rng = np.random.default_rng(2)
+    for name, rows, cols in shapes:
+        per = rows * cols + 4 * rows                   # codes + scales stored
+        count = int(np.ceil((512 << 20) / per))
+        algo = rows * cols + 4 * rows + 2 * cols + 4 * rows   # + x read + y written
+        q = rng.integers(-127, 128, size=(count, rows, cols), dtype=np.int8)
+        s = (rng.random((count, rows), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+        x = rng.standard_normal(cols).astype(np.float16).view(np.uint16)
+        dq, ds, dx, dy = ctx.upload(q), ctx.upload(s), ctx.upload(x), ctx.empty(count * rows * 4)
+        del q
+        W = ctx.weight(H.FMT_INT8, rows, cols, dq, ds)
+        ctx.matvec_xh_list(W, count, rows * cols, rows, dx, 0, dy)   # warm
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(reps):
+            ctx.matvec_xh_list(W, count, rows * cols, rows, dx, 0, dy)
+        ctx.record(e1)
+        ms = ctx.elapsed_ms(e0, e1) / reps
+        ctx.destroy_event(e0), ctx.destroy_event(e1)
+        gbs = count * algo / (ms * 1e-3) / 1e9
+        out[name] = {"shape": [rows, cols], "matrices": count, "bytes_per_launch": count * algo,
+                     "us_per_launch": round(ms * 1e3, 2), "us_per_matrix": round(ms * 1e3 / count, 4),
+                     "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"isolated int8 matvec {name} {rows}x{cols} x{count}: {gbs:.0f} GB/s")
+        for b in (dq, ds, dx, dy):
+            b.free()
+    return out
+
+
+def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
+    """The oracle (a C port of the reference CPU path, f64 accumulation) on one core:
+    its KV cache is loaded with the GPU cache's context (the same f16 values), then it
+    greedy-decodes `steps` tokens. Returns the baseline record and the token match."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    O.lib().or_set_threads(1)
+    oracle = O.OracleModel(cfg, ckpt, scheme="int4", group=128, lm_head="int8", kv_f16=True)
+    oc = oracle.new_cache(context + steps)
+    for L in range(cfg.layers):
+        p = cache.present(L)
+        k = np.ascontiguousarray(p["key"][:, :context].transpose(1, 0, 2).reshape(context, -1))
+        v = np.ascontiguousarray(p["value"][:, :context].transpose(1, 0, 2).reshape(context, -1))
+        oc.write(L, 0, k, v, context)
+    oc.length = context
+    toks, tok = [], first
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = O.argmax(oracle.forward([tok], oc))
+        toks.append(tok)
+    dt = time.perf_counter() - t0
+    match = sum(int(a == b) for a, b in zip(toks, gpu_tokens[:steps]))
+    cpu = {"value": round(steps / dt, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"{steps} greedy decode steps at context {context}..{context + steps - 1} "
+                     f"(KV cache loaded from the GPU run), oracle/liboracle.so, 1 thread, "
+                     f"{os.cpu_count()} host CPUs visible"}
+    return cpu, f"{match}/{steps}"
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--context", type=int, default=1024)
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--profile-steps", type=int, default=32)
+    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--isolated", choices=["all", "none"], default="all")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: every box in this pool has one, and batch-1 decode of a "
+              "0.5B model is not sharded (see DESIGN.md for how it would be). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = H.QWEN25_05B
+    ctx = H.GpuContext.create(0)
+    log(ctx.describe())
+    t0 = time.perf_counter()
+    ckpt = H.synthesize_checkpoint(cfg, seed=args.seed)
+    tensors = H.device_tensors(ckpt, cfg, "int4", 128, "int8")
+    extra = max(args.steps, args.warmup, args.profile_steps, args.cpu_steps) + 1
+    capacity = args.context + extra
+    model = H.GpuModel.load(ctx, tensors, cfg, maxPositions=capacity)
+    del tensors
+    log(f"model ready in {time.perf_counter() - t0:.1f}s, {model.device_bytes / 1e6:.1f} MB on device")
+
+    prompt = H.synth_tokens(args.seed, "config4.prompt", cfg.vocab, args.context)
+    cache = model.newCache(capacity)
+    t0 = time.perf_counter()
+    first = model.forward_tokens(prompt, cache)["argmax"]
+    prefill_s = time.perf_counter() - t0
+    log(f"prefilled {args.context} positions in {prefill_s:.2f}s (decode path, one position per step)")
+
+    if args.warmup:
+        model.decode(cache, first, args.warmup)
+        cache.length = args.context
+
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.done()
+    w0 = time.perf_counter()
+    ctx.record(e0)
+    model.decode_launch(cache, first, args.steps)
+    ctx.record(e1)
+    tokens = model.decode_collect(cache, args.steps)
+    wall = time.perf_counter() - w0
+    ms = ctx.elapsed_ms(e0, e1)
+    ctx.destroy_event(e0), ctx.destroy_event(e1)
+    tok_s = args.steps / (ms / 1e3)
+    log(f"decode: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms (wall): {tok_s:.0f} tok/s")
+
+    # In-situ per-kernel times over the same positions.
+    cache.length = args.context
+    psteps = min(args.profile_steps, args.steps)
+    ptoks, roles = model.decode_profile(cache, first, psteps)
+    deterministic = bool(np.array_equal(ptoks, tokens[:psteps]))
+    rb = role_bytes(cfg, args.context + psteps // 2)
+    per_kernel = {}
+    for r, (tot_ms, n) in roles.items():
+        if n == 0:
+            continue
+        per_kernel[r] = {"us_per_token": round(tot_ms * 1e3 / psteps, 2),
+                         "us_per_launch": round(tot_ms * 1e3 / n, 3),
+                         "launches_per_token": n // psteps,
+                         "GBps": round(rb[r] * n / (tot_ms * 1e-3) / 1e9, 1)}
+    dominant = max(per_kernel, key=lambda r: per_kernel[r]["us_per_token"])
+    dk = per_kernel[dominant]
+    achieved = rb[dominant] / (dk["us_per_launch"] * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": None, "bytes_per_launch": rb[dominant]}
+    log(f"per-kernel: {json.dumps(per_kernel)}")
+
+    iso = None
+    if args.isolated == "all":
+        d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
+        iso = isolated_matvec(ctx, [("q_o", d, d), ("k_v", kv, d), ("gate_up", ffn, d),
+                                    ("down", d, ffn), ("lm_head", V, d)])
+
+    cpu, match = (None, None)
+    if not args.no_cpu:
+        cpu, match = cpu_baseline(cfg, ckpt, cache, first, tokens, args.cpu_steps, args.context)
+        log(f"cpu baseline: {cpu['value']} tok/s, greedy match {match}")
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms / args.steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int4",
+        "data": "synthetic (seeded random-init weights, seeded prompt ids)",
+        "config": {"workload": "config4: Qwen2.5-0.5B-shape int4-g128 decode, int8 lm_head, "
+                               f"f16 KV cache, context {args.context}, batch 1, greedy",
+                   "global_batch": 1, "seq_len": args.context, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "per_kernel_us": per_kernel,
+        "profile_tokens_match_timed": deterministic,
+        "greedy_match_cpu_sample": match,
+        "matvec_isolated": iso,
+        "prefill_s": round(prefill_s, 3),
+    }
+    print(json.dumps(line), flush=True)
+    cache.destroy()
+    model.destroy()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

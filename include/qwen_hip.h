@@ -137,11 +137,20 @@ int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_ke
 
 /* ATTENTION (kernels.js:404-499): causal GQA over an f16 head-major cache. Query t (absolute
  * position past+t) attends to positions 0..past+t. Query head h reads kv head
- * h / (heads/kv_heads). Scale 1/sqrt(head_dim). q, out f32 [seq, heads*head_dim].
- * Split-K online softmax over fixed 64-position chunks. head_dim must be 64. */
+ * h / (heads/kv_heads). Scale 1/sqrt(head_dim). q (rotated), out f32 [seq, heads*head_dim].
+ * Evaluated in the order of groupedAttention (src/core/attention.js:32-66): f64 dots stored
+ * f32, softmax by the global max with an f64 sum, and a sequential f32 sum over positions, so
+ * the result is the CPU's to the bit up to f64 ordering. head_dim must be 64. */
 int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
                  const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
                  int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim);
+/* As qh_attention with a split-K online softmax over 64-position chunks: one pass over K/V
+ * shared by the query heads of a kv head, splits combined in order. Exact only to f32
+ * rounding; the fast form for long contexts. */
+int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                        const uint16_t* d_value_cache, int32_t capacity, float* d_out,
+                        int32_t seq, int32_t past, int32_t heads, int32_t kv_heads,
+                        int32_t head_dim);
 
 /* SWIGLU (kernels.js:502-515): gate = silu(gate) * up, in place. */
 int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n);
@@ -224,6 +233,25 @@ int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int3
 /* Enqueue the graph replays without waiting (for timing); qh_decode_collect waits and copies. */
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps);
 int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens);
+
+/* Kernel roles of one decode step, the grouping of the reference's in-situ profile
+ * ("GPU ms per token by role", web/decode-profile.html:88-192). */
+enum {
+  QH_ROLE_EMBED = 0,     /* embedding gather */
+  QH_ROLE_QKV = 1,       /* rmsnorm + q|k|v matvec + bias */
+  QH_ROLE_ATTENTION = 2, /* rope + f16 KV append + split-K GQA attention */
+  QH_ROLE_OPROJ = 3,     /* o projection + residual */
+  QH_ROLE_GATEUP = 4,    /* rmsnorm + gate|up matvec + swiglu */
+  QH_ROLE_DOWN = 5,      /* down projection + residual */
+  QH_ROLE_HEAD = 6,      /* final rmsnorm + lm_head + argmax */
+  QH_ROLE_COUNT = 7
+};
+/* As qh_decode, but with direct launches and a device event before every launch, so each
+ * kernel's in-situ time is measured (GpuContext.timed, src/gpu/device.js:301-338).
+ * h_role_ms[QH_ROLE_COUNT] receives the summed milliseconds per role over all steps and
+ * h_role_launches[QH_ROLE_COUNT] the launch counts. Tokens are identical to qh_decode's. */
+int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps,
+                      int32_t* h_tokens, float* h_role_ms, int32_t* h_role_launches);
 
 #ifdef __cplusplus
 }

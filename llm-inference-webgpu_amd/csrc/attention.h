@@ -1,42 +1,168 @@
-// Causal GQA attention over an f16 head-major KV cache, split-K over context
-// with an online softmax (device code, shared by the operator and the fused
-// decode step).
+// Causal GQA attention over an f16 head-major KV cache [kv_heads][capacity][64]
+// (device code, shared by the operators and the decode step). Replaces
+// ATTENTION (src/gpu/kernels.js:404-499). Query head h reads kv head
+// h / (heads/kv_heads), the blocked map of src/core/attention.js:74-76.
 //
-// Replaces ATTENTION (src/gpu/kernels.js:404-499). The reference gives each
-// (position, query head) a workgroup, writes every score to a global scratch
-// buffer and walks all positions with 64 of 256 threads for the PV sum. Here
-// one block owns (query position, kv head, split): the K/V chunk it stages
-// into LDS serves all `group` query heads that share the kv head (7 for
-// Qwen2.5), and the scores never leave LDS.
+// Two algorithms:
 //
-// Structure of one query at context ctx (= its position + 1):
-//   chunks of 64 positions; S = min(nchunks, kMaxSplits) splits of
-//   cps = ceil(nchunks / S) consecutive chunks; each split runs the online
-//   softmax over its chunks in order and writes (m, l, acc[64]) per head;
-//   the last split block to finish (atomic counter) combines the splits in
-//   split order. The structure depends only on ctx, so a query computed in a
-//   prefill and the same query computed in decode give the same bits.
+// Exact order (k_attn_scores + k_attn_pv), what the model path uses. It
+// evaluates groupedAttention (src/core/attention.js:32-66) step for step:
+// each score is a sequential f64 dot stored to f32, the softmax shifts by the
+// global max and normalizes with an f64 sum (src/core/ops.js:66-78), and the
+// output accumulates sequentially over positions in f32, as the reference's
+// Float32Array `out += weight * value` does. Scores and maxima are computed in
+// parallel over 64-position chunks; the sequential PV sum runs one lane per
+// output element. The result matches the CPU to the bit apart from f64-order
+// noise, so a device f16 cache and the CPU's same-f16 cache stay identical.
+//
+// Split-K online softmax (k_attention_splitk), for long contexts: one block
+// per (query, kv head, split of chunks) stages K/V once for all the query heads
+// that share it and keeps scores in LDS; the last split to finish combines.
+// Exact to f32 rounding, not to the CPU's order; checked within the kernel
+// tolerance.
 #pragma once
 
 #include "device_common.h"
 
 namespace qh {
 
-constexpr int kChunk = 64;        // positions per online-softmax step
-constexpr int kMaxSplits = 128;   // splits per (query, kv head)
+constexpr int kChunk = 64;        // positions per chunk
+constexpr int kMaxSplits = 128;   // split-K: splits per (query, kv head)
 constexpr int kHeadDim = 64;
 constexpr int kMaxGroup = 8;      // query heads per kv head
-constexpr int kPartialStride = kHeadDim + 2;  // m, l, acc[64]
+constexpr int kPartialStride = kHeadDim + 2;  // split-K partial: m, l, acc[64]
 
-struct AttnArgs {
-  const float* q;        // [seq][heads*64]; pre-rotation when rope_q
-  const float* k_new;    // fused append: this step's k [kv_heads*64], pre-rotation
-  const float* v_new;    // fused append: this step's v [kv_heads*64]
-  uint16_t* kc;          // [kv_heads][capacity][64] f16
-  uint16_t* vc;
-  const float* cos_t;    // rope tables [positions][32]
-  const float* sin_t;
-  const int* d_pos;      // decode: past read from the device
+__host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
+
+// ------------------------------------------------------------ exact order --
+
+struct ExactArgs {
+  const float* q;        // [seq][heads*64], rotated
+  const uint16_t* kc;    // [kv_heads][capacity][64] f16
+  const uint16_t* vc;
+  const int* d_pos;      // when set, past is read from the device (decode)
+  float* scores;         // [seq][heads][score_stride]; the PV pass overwrites them with p
+  float* maxes;          // [seq][heads][max_stride]: per-chunk maxima
+  float* out;            // [seq][heads*64]
+  int past, capacity, heads, kv_heads, score_stride, max_stride;
+};
+
+// grid (chunks, kv_heads, seq): scores of one 64-position chunk for the `group`
+// query heads of one kv head, and their per-chunk maxima.
+static __global__ __launch_bounds__(kBlock) void k_attn_scores(ExactArgs a) {
+  const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z;
+  const int past = a.d_pos ? *a.d_pos : a.past;
+  const int pos = past + t;
+  if (pos >= a.capacity) return;  // the host keeps positions inside the cache
+  const int ctx = pos + 1;
+  const int p0 = c * kChunk;
+  if (p0 >= ctx) return;
+  const int n = min(kChunk, ctx - p0);
+  const int group = a.heads / a.kv_heads;
+  const int tid = threadIdx.x;
+
+  __shared__ double qs[kMaxGroup][kHeadDim];
+  __shared__ __attribute__((aligned(16))) _Float16 ks[kChunk][kHeadDim + 2];
+  __shared__ float sc[kMaxGroup][kChunk];
+  const float* qrow = a.q + (size_t)t * a.heads * kHeadDim + (size_t)g * group * kHeadDim;
+  for (int i = tid; i < group * kHeadDim; i += kBlock) qs[i / kHeadDim][i % kHeadDim] = (double)qrow[i];
+  const uint16_t* kbase = a.kc + ((size_t)g * a.capacity + p0) * kHeadDim;
+  for (int e = tid; e < n * 8; e += kBlock) {
+    const int p = e >> 3, part = e & 7;
+    const v4u kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)p * kHeadDim)[part];
+#pragma unroll
+    for (int k = 0; k < 4; k++) *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kv4[k];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < group * kChunk; idx += kBlock) {
+    const int h = idx / kChunk, p = idx % kChunk;
+    float s = -INFINITY;
+    if (p < n) {
+      // dot += q[i] * k[i], i ascending, in f64 (each product is exact).
+      double dot = 0.0;
+#pragma unroll 8
+      for (int j = 0; j < kHeadDim; j += 2) {
+        const uint32_t kk = *reinterpret_cast<const uint32_t*>(&ks[p][j]);
+        dot = fma(qs[h][j], (double)f16_lo(kk), dot);
+        dot = fma(qs[h][j + 1], (double)f16_hi(kk), dot);
+      }
+      s = (float)(dot * 0.125);  // scale = 1/sqrt(64), exact
+      a.scores[((size_t)t * a.heads + g * group + h) * a.score_stride + p0 + p] = s;
+    }
+    sc[h][p] = s;
+  }
+  __syncthreads();
+  const int wave = tid / kWave, lane = tid & (kWave - 1);
+  for (int h = wave; h < group; h += kBlock / kWave) {
+    const float m = wave_max(sc[h][lane]);
+    if (lane == 0) a.maxes[((size_t)t * a.heads + g * group + h) * a.max_stride + c] = m;
+  }
+}
+
+// grid (heads, seq): softmax with the global max, then out[d] accumulated
+// sequentially over positions in f32 by lane d of wave 0.
+static __global__ __launch_bounds__(kBlock) void k_attn_pv(ExactArgs a) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int past = a.d_pos ? *a.d_pos : a.past;
+  const int pos = past + t;
+  if (pos >= a.capacity) return;
+  const int ctx = pos + 1;
+  const int g = h / (a.heads / a.kv_heads);
+  const int tid = threadIdx.x;
+  __shared__ double red[kBlock / kWave];
+  __shared__ float mx[kBlock / kWave];
+
+  const size_t row = (size_t)t * a.heads + h;
+  float* sc = a.scores + row * a.score_stride;
+  // The global max is the max of the chunk maxima (max is order-free).
+  const float* cm = a.maxes + row * a.max_stride;
+  float m = -INFINITY;
+  for (int c = tid; c < attn_chunks(ctx); c += kBlock) m = fmaxf(m, cm[c]);
+  m = wave_max(m);
+  if ((tid & (kWave - 1)) == 0) mx[tid / kWave] = m;
+  __syncthreads();
+  const double M = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+  // e = exp(s - max) stored f32; the sum over the unrounded e in f64; p = f32(e32 * (1/sum)).
+  double sum = 0.0;
+  for (int s = tid; s < ctx; s += kBlock) {
+    const double e = exp((double)sc[s] - M);
+    sc[s] = (float)e;
+    sum += e;
+  }
+  sum = block_sum_f64(sum, red);
+  const double inv = 1.0 / sum;
+  for (int s = tid; s < ctx; s += kBlock) sc[s] = (float)((double)sc[s] * inv);
+  __syncthreads();
+  if (tid >= kWave) return;
+
+  // out[d] += p[s] * v[s][d] for s ascending, rounding to f32 at every step. The
+  // product is exact in the fused form, so this is the CPU's f64-sum-then-f32
+  // except in double-rounding ties (probability ~2^-29 per step).
+  const uint16_t* vb = a.vc + (size_t)g * a.capacity * kHeadDim + tid;
+  float o = 0.f;
+  constexpr int U = 16;
+  int s = 0;
+  for (; s + U <= ctx; s += U) {
+    float pv[U];
+    _Float16 vv[U];
+#pragma unroll
+    for (int k = 0; k < U; k++) {
+      pv[k] = sc[s + k];
+      vv[k] = __builtin_bit_cast(_Float16, vb[(size_t)(s + k) * kHeadDim]);
+    }
+#pragma unroll
+    for (int k = 0; k < U; k++) o = fmaf(pv[k], (float)vv[k], o);
+  }
+  for (; s < ctx; s++) o = fmaf(sc[s], (float)__builtin_bit_cast(_Float16, vb[(size_t)s * kHeadDim]), o);
+  a.out[(size_t)t * a.heads * kHeadDim + (size_t)h * kHeadDim + tid] = o;
+}
+
+// -------------------------------------------------------------- split-K --
+
+struct SplitArgs {
+  const float* q;        // [seq][heads*64], rotated
+  const uint16_t* kc;    // [kv_heads][capacity][64] f16
+  const uint16_t* vc;
   float* partials;       // [seq][kv_heads][s_grid][group][66]
   int* counters;         // [seq][kv_heads], zero between launches
   float* out;            // [seq][heads*64]
@@ -44,7 +170,7 @@ struct AttnArgs {
 };
 
 __host__ __device__ inline void attn_splits(int ctx, int* nchunks, int* cps, int* splits) {
-  const int n = (ctx + kChunk - 1) / kChunk;
+  const int n = attn_chunks(ctx);
   const int s = n < kMaxSplits ? n : kMaxSplits;
   const int c = (n + s - 1) / s;
   *nchunks = n;
@@ -52,17 +178,23 @@ __host__ __device__ inline void attn_splits(int ctx, int* nchunks, int* cps, int
   *splits = (n + c - 1) / c;
 }
 
-template <bool ROPE_Q, bool FUSED_APPEND>
-__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
+// Grid width that covers every query with context <= max_ctx. The split count
+// is not monotone in ctx past kMaxSplits chunks (129 chunks need 65 splits, 128
+// need 128), so the bound is min(chunks, kMaxSplits), not splits(max_ctx).
+__host__ __device__ inline int attn_grid_splits(int max_ctx) {
+  const int n = attn_chunks(max_ctx);
+  return n < kMaxSplits ? n : kMaxSplits;
+}
+
+static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a) {
   const int split = blockIdx.x;
   const int g = blockIdx.y;
   const int t = blockIdx.z;
-  const int past = a.d_pos ? *a.d_pos : a.past;
-  const int pos = past + t;
+  const int pos = a.past + t;
   const int ctx = pos + 1;
   int nchunks, cps, nsplit;
   attn_splits(ctx, &nchunks, &cps, &nsplit);
-  if (split >= nsplit) return;
+  if (split >= nsplit || nsplit > a.s_grid) return;
   const int c0 = split * cps;
   const int c1 = min(c0 + cps, nchunks);
   const int group = a.heads / a.kv_heads;
@@ -73,49 +205,17 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 vs[kChunk][kHeadDim];
   __shared__ float sc[kMaxGroup][kChunk];
   __shared__ float mst[kMaxGroup], lst[kMaxGroup], alpha[kMaxGroup];
-  __shared__ __attribute__((aligned(16))) _Float16 knew[kHeadDim];
-  __shared__ __attribute__((aligned(16))) _Float16 vnew[kHeadDim];
   __shared__ int is_last;
 
   const size_t qrow = (size_t)t * a.heads * kHeadDim;
-  // Query heads g*group .. g*group+group-1 share kv head g (the blocked map of
-  // src/core/attention.js:74-76).
   for (int idx = tid; idx < group * kHeadDim; idx += kBlock) {
-    const int h = idx / kHeadDim, j = idx % kHeadDim;
-    const float* qh_ = a.q + qrow + (size_t)(g * group + h) * kHeadDim;
-    if constexpr (ROPE_Q) {
-      // Half-split rotation from the f32 tables, as ROPE (kernels.js:380-388).
-      const int jj = j & 31;
-      const float c = a.cos_t[(size_t)pos * 32 + jj], s = a.sin_t[(size_t)pos * 32 + jj];
-      const float lo = qh_[jj], hi = qh_[jj + 32];
-      qs[h][j] = j < 32 ? lo * c - hi * s : hi * c + lo * s;
-    } else {
-      qs[h][j] = qh_[j];
-    }
-  }
-  const bool owns_new = FUSED_APPEND && c1 == nchunks;
-  if constexpr (FUSED_APPEND) {
-    if (owns_new && tid < kHeadDim) {
-      const int j = tid, jj = j & 31;
-      const float* kh = a.k_new + (size_t)g * kHeadDim;
-      const float c = a.cos_t[(size_t)pos * 32 + jj], s = a.sin_t[(size_t)pos * 32 + jj];
-      const float lo = kh[jj], hi = kh[jj + 32];
-      const float kr = j < 32 ? lo * c - hi * s : hi * c + lo * s;
-      const _Float16 kh16 = (_Float16)kr;
-      const _Float16 vh16 = (_Float16)a.v_new[(size_t)g * kHeadDim + j];
-      knew[j] = kh16;
-      vnew[j] = vh16;
-      const size_t at = ((size_t)g * a.capacity + pos) * kHeadDim + j;
-      a.kc[at] = __builtin_bit_cast(uint16_t, kh16);
-      a.vc[at] = __builtin_bit_cast(uint16_t, vh16);
-    }
+    qs[idx / kHeadDim][idx % kHeadDim] = a.q[qrow + (size_t)g * group * kHeadDim + idx];
   }
   if (tid < kMaxGroup) {
     mst[tid] = -INFINITY;
     lst[tid] = 0.f;
   }
-  // Each thread owns outputs idx = tid and tid + 256 of [group][64].
-  float acc0 = 0.f, acc1 = 0.f;
+  float acc0 = 0.f, acc1 = 0.f;  // outputs tid and tid + 256 of [group][64]
   const int o0 = tid, o1 = tid + kBlock;
   __syncthreads();
 
@@ -124,28 +224,18 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   for (int c = c0; c < c1; c++) {
     const int p0 = c * kChunk;
     const int n = min(kChunk, ctx - p0);
-    // Stage K and V rows (128 B each) with 16-byte loads.
     for (int e = tid; e < kChunk * 8; e += kBlock) {
       const int p = e >> 3, part = e & 7;
-      uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
+      v4u kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
       if (p < n) {
-        if (FUSED_APPEND && owns_new && p0 + p == pos) {
-          kv4 = *reinterpret_cast<const uint4*>(&knew[part * 8]);
-          vv4 = *reinterpret_cast<const uint4*>(&vnew[part * 8]);
-        } else {
-          kv4 = reinterpret_cast<const uint4*>(kbase + (size_t)(p0 + p) * kHeadDim)[part];
-          vv4 = reinterpret_cast<const uint4*>(vbase + (size_t)(p0 + p) * kHeadDim)[part];
-        }
+        kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)(p0 + p) * kHeadDim)[part];
+        vv4 = reinterpret_cast<const v4u*>(vbase + (size_t)(p0 + p) * kHeadDim)[part];
       }
-      const uint32_t kw[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
 #pragma unroll
-      for (int k = 0; k < 4; k++) {
-        *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kw[k];
-      }
-      *reinterpret_cast<uint4*>(&vs[p][part * 8]) = vv4;
+      for (int k = 0; k < 4; k++) *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kv4[k];
+      *reinterpret_cast<v4u*>(&vs[p][part * 8]) = vv4;
     }
     __syncthreads();
-    // Scores, scaled by 1/sqrt(64) = 1/8 (exact in f32).
     for (int idx = tid; idx < group * kChunk; idx += kBlock) {
       const int h = idx / kChunk, p = idx % kChunk;
       float s = -INFINITY;
@@ -162,7 +252,6 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       sc[h][p] = s;
     }
     __syncthreads();
-    // Online softmax update, one wave per head.
     {
       const int wave = tid / kWave, lane = tid & (kWave - 1);
       for (int h = wave; h < group; h += kBlock / kWave) {
@@ -196,7 +285,6 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     __syncthreads();
   }
 
-  // Partial (m, l, acc) for this split.
   float* pbase = a.partials + (((size_t)t * a.kv_heads + g) * a.s_grid) * group * kPartialStride;
   {
     float* mine = pbase + (size_t)split * group * kPartialStride;
@@ -224,8 +312,6 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   __syncthreads();
   if (!is_last) return;
   __threadfence();
-
-  // Combine the splits in split order.
   for (int idx = tid; idx < group * kHeadDim; idx += kBlock) {
     const int h = idx / kHeadDim, d = idx % kHeadDim;
     float M = -INFINITY;

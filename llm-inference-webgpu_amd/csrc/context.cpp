@@ -261,8 +261,8 @@ int qh_matvec_xh_list(qh_ctx* ctx, const qh_weight* w, int32_t count, size_t dat
 int qh_rmsnorm(qh_ctx* ctx, const float* d_x, const float* d_gain, float* d_y, int32_t rows,
                int32_t cols, double eps) {
   QH_CHECK(ctx && d_x && d_gain && d_y, QH_ERR_INVALID, "rmsnorm needs x, gain and y");
-  QH_CHECK(rows >= 1 && cols >= 1 && cols <= 16384, QH_ERR_INVALID,
-           "rmsnorm shape [%d, %d] unsupported (cols up to 16384)", rows, cols);
+  QH_CHECK(rows >= 1 && cols >= 1 && cols <= 8192, QH_ERR_INVALID,
+           "rmsnorm shape [%d, %d] unsupported (cols up to 8192)", rows, cols);
   QH_HIP(qh::launch_rmsnorm(ctx->stream, d_x, d_gain, d_y, rows, cols, eps));
   return QH_OK;
 }
@@ -294,9 +294,10 @@ int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_ke
   return QH_OK;
 }
 
-int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
-                 const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
-                 int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+static int check_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                           const uint16_t* d_value_cache, int32_t capacity, float* d_out,
+                           int32_t seq, int32_t past, int32_t heads, int32_t kv_heads,
+                           int32_t head_dim) {
   QH_CHECK(ctx && d_q && d_key_cache && d_value_cache && d_out, QH_ERR_INVALID,
            "attention needs q, both caches and out");
   QH_CHECK(head_dim == 64, QH_ERR_INVALID, "attention supports head_dim 64 (got %d)", head_dim);
@@ -306,15 +307,54 @@ int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
   QH_CHECK(seq >= 1 && past >= 0, QH_ERR_INVALID, "attention needs seq >= 1 and past >= 0");
   QH_CHECK(past + seq <= capacity, QH_ERR_RANGE, "attention over %d positions exceeds capacity %d",
            past + seq, capacity);
+  return QH_OK;
+}
+
+int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                 const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                 int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
+                           kv_heads, head_dim);
+  if (rc) return rc;
+  // Scores and per-chunk maxima in the context scratch's partial region when they fit.
+  const size_t floats = qh::attention_exact_floats(seq, heads, past);
+  const size_t room = ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64;
+  const size_t n_scores = (size_t)seq * heads * (past + seq);
+  float* buf = nullptr;
+  if (floats * sizeof(float) <= room) {
+    buf = reinterpret_cast<float*>(static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes);
+    QH_HIP(qh::launch_attention_exact(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out,
+                                      seq, past, heads, kv_heads, buf, buf + n_scores));
+    return QH_OK;
+  }
+  QH_HIP(hipMallocAsync((void**)&buf, floats * sizeof(float), ctx->stream));
+  hipError_t e = qh::launch_attention_exact(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
+                                            d_out, seq, past, heads, kv_heads, buf, buf + n_scores);
+  QH_HIP(hipFreeAsync(buf, ctx->stream));
+  QH_HIP(e);
+  return QH_OK;
+}
+
+int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                        const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                        int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
+                           kv_heads, head_dim);
+  if (rc) return rc;
   const size_t pf = qh::attention_partials_floats(seq, heads, kv_heads, past + seq);
   const size_t need = pf * sizeof(float) + (size_t)seq * kv_heads * sizeof(int) + 256;
   void* parts = nullptr;
   int* counters = nullptr;
-  if (need <= ctx->scratch_bytes) {
-    counters = static_cast<int*>(ctx->d_scratch);
-    parts = static_cast<char*>(ctx->d_scratch) + (((size_t)seq * kv_heads * sizeof(int) + 255) & ~(size_t)255);
-    QH_HIP(qh::launch_attention(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out, seq,
-                                past, heads, kv_heads, static_cast<float*>(parts), counters));
+  // Counters live in the context scratch's counter region (after the argmax counter), which
+  // only ever holds zeroed counters; partials in the region after it.
+  const size_t n_counters = (size_t)seq * kv_heads;
+  const size_t part_room = ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64;
+  if ((n_counters + 16) * sizeof(int) <= qh_ctx::kScratchCounterBytes && pf * sizeof(float) <= part_room) {
+    counters = static_cast<int*>(ctx->d_scratch) + 16;
+    parts = static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes;
+    QH_HIP(qh::launch_attention_splitk(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
+                                       d_out, seq, past, heads, kv_heads,
+                                       static_cast<float*>(parts), counters));
     return QH_OK;
   }
   // Larger prefill shapes get a temporary buffer.
@@ -323,9 +363,9 @@ int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
   QH_HIP(hipMemsetAsync(tmp, 0, 256 + (size_t)seq * kv_heads * sizeof(int), ctx->stream));
   counters = static_cast<int*>(tmp);
   parts = static_cast<char*>(tmp) + (((size_t)seq * kv_heads * sizeof(int) + 255) & ~(size_t)255);
-  hipError_t e = qh::launch_attention(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out,
-                                      seq, past, heads, kv_heads, static_cast<float*>(parts),
-                                      counters);
+  hipError_t e = qh::launch_attention_splitk(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
+                                             d_out, seq, past, heads, kv_heads,
+                                             static_cast<float*>(parts), counters);
   QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
   return QH_OK;
@@ -345,10 +385,12 @@ int qh_add(qh_ctx* ctx, float* d_x, const float* d_delta, int32_t n) {
 
 int qh_argmax(qh_ctx* ctx, const float* d_v, int32_t n, int32_t* h_index) {
   QH_CHECK(ctx && d_v && h_index && n >= 1, QH_ERR_INVALID, "argmax needs v, n >= 1 and an output");
-  QH_CHECK(qh::argmax_scratch_bytes(n) + 64 <= ctx->scratch_bytes, QH_ERR_INVALID,
-           "argmax over %d values exceeds the context scratch", n);
-  int32_t* d_out = reinterpret_cast<int32_t*>(static_cast<char*>(ctx->d_scratch) + ctx->scratch_bytes - 64);
-  QH_HIP(qh::launch_argmax(ctx->stream, d_v, n, ctx->d_scratch, d_out));
+  QH_CHECK(qh::argmax_partials_bytes(n) + qh_ctx::kScratchCounterBytes + 64 <= ctx->scratch_bytes,
+           QH_ERR_INVALID, "argmax over %d values exceeds the context scratch", n);
+  char* base = static_cast<char*>(ctx->d_scratch);
+  int32_t* d_out = reinterpret_cast<int32_t*>(base + ctx->scratch_bytes - 64);
+  QH_HIP(qh::launch_argmax(ctx->stream, d_v, n, reinterpret_cast<int*>(base),
+                           base + qh_ctx::kScratchCounterBytes, d_out));
   QH_HIP(hipMemcpyAsync(ctx->h_pinned, d_out, 4, hipMemcpyDeviceToHost, ctx->stream));
   QH_HIP(hipStreamSynchronize(ctx->stream));
   *h_index = ctx->h_pinned[0];

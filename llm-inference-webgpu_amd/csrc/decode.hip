@@ -1,15 +1,16 @@
 // The fused decode step: the whole of GpuModel.#forward for one position
-// (src/gpu/model.js:240-402) as 5 launches per layer plus the gather and the
+// (src/gpu/model.js:240-402) as 6 launches per layer plus the gather and the
 // output head, instead of the reference's ~15 dispatches and 2 copies per
 // layer. Every launch reads its position from device memory, so the same
-// launches can be captured once in a hipGraph and replayed every token.
+// launches are captured once in a hipGraph and replayed every token.
 //
-// Per layer:
-//   1. rmsnorm(x) -> fused q|k|v matvec (+bias)               k_fused<RMSNORM, BIAS>
-//   2. rope(q,k) -> f16 KV append -> split-K GQA attention     k_attention<rope, append>
-//   3. o-proj matvec, residual add into x                      k_fused<COPY, RESIDUAL>
-//   4. rmsnorm(x) -> interleaved gate|up matvec -> swiglu      k_fused<RMSNORM, SWIGLU>
-//   5. down matvec, residual add into x                        k_fused<COPY, RESIDUAL>
+// Per layer (the order of src/cpu/model.js:89-143):
+//   1. rmsnorm(x) -> q|k|v matvec + bias -> rope (f64) -> q, f16 K/V append
+//   2. attention scores per 64-position chunk (f64 dots)
+//   3. softmax + sequential PV sum per head
+//   4. o-proj matvec, residual add into x
+//   5. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
+//   6. down matvec, residual add into x
 // then rmsnorm -> lm_head -> logits and argmax; the last block to finish
 // writes the token (the reference reads back 151,936 logits and scans them on
 // the host, src/gpu/model.js:372-382, web/bench.html:129-131) and advances
@@ -21,84 +22,148 @@
 namespace qh {
 
 enum { PRO_RMSNORM = 0, PRO_COPY = 1 };
-enum { EPI_BIAS = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
+enum { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 struct FusedArgs {
   DMat w;
   const float* in;      // rmsnorm input, or the vector to stage as-is
   const float* gain;    // rmsnorm gain
   double eps;
-  const float* bias;    // EPI_BIAS
-  float* out;           // EPI_BIAS / EPI_SWIGLU / EPI_LOGITS output; EPI_RESIDUAL target
-  int ntiles;           // row tiles; blocks loop over them
-  // EPI_LOGITS: argmax partials and the decode state it advances.
+  float* out;           // EPI_QKV: q [hidden]; EPI_SWIGLU: h; EPI_LOGITS: logits; EPI_RESIDUAL: x
+  int items;            // work items; blocks loop over them
+  // EPI_QKV
+  const float* bias;    // [hidden + 2*kv_dim]
+  const double* rope_cos;  // [positions][32] f64
+  const double* rope_sin;
+  uint16_t* kc;         // this layer's K cache [kv_heads][capacity][64]
+  uint16_t* vc;
+  int heads, kv_heads;
+  // EPI_QKV, EPI_LOGITS: the decode state
+  int* state;           // [0] position, [1] forced length
+  int capacity;
+  // EPI_LOGITS
   ArgPair* partials;
   int* counter;
-  int* state;           // [0] position, [1] forced length
   int* tokens;          // [capacity + 1]
   int* pred;            // [capacity]
-  int capacity;
 };
 
-template <int FMT, int R, int TL, int PRO, int EPI>
+// Rows of work item `it`. QKV: a rope pair (j, j+32) of a q or k head, or two
+// consecutive v rows. SWIGLU: gate row and up row (2j, 2j+1). Otherwise R
+// consecutive rows, clamped to the matrix.
+template <int EPI, int R>
+__device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows)[R]) {
+  if constexpr (EPI == EPI_QKV) {
+    static_assert(R == 2, "qkv items are row pairs");
+    const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
+    const int rope_pairs = (a.heads + a.kv_heads) * 32;
+    if (it < rope_pairs) {
+      const int head = it / 32, j = it % 32;  // heads 0..heads-1 are q, then k heads
+      const int base = head < a.heads ? head * kHeadDim : hidden + (head - a.heads) * kHeadDim;
+      rows[0] = base + j;
+      rows[1] = base + j + 32;
+    } else {
+      const int v = it - rope_pairs;
+      rows[0] = hidden + kvd + 2 * v;
+      rows[1] = hidden + kvd + 2 * v + 1;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; i++) rows[i] = min(it * R + i, a.w.rows - 1);
+  }
+}
+
+template <int FMT, int TL, int R, int PRO, int EPI>
 __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
-  extern __shared__ float smem[];
+  extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   __shared__ ArgPair tbest[kBlock / TL];
   __shared__ ArgPair wred[kBlock / kWave];
   __shared__ int is_last;
-  float* xs = smem;
-  float* xcs = smem + a.w.cols;
+  double* xs = smem;
   if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm(a.in, a.gain, a.eps, a.w.cols, xs, red);
   else stage_copy(a.in, a.w.cols, xs);
-  if constexpr (FMT == QH_FMT_INT4) stage_chunk_sums(xs, a.w.cols, xcs);
 
-  using TM = TeamMap<TL, R>;
-  const int lane = TM::lane();
+  using T = Teams<TL>;
+  const int lane = T::lane();
+  int pos = 0;
+  if constexpr (EPI == EPI_QKV) pos = a.state[0];
   float bv = NAN;
   int bi = 0x7fffffff;
-  for (int tile = blockIdx.x; tile < a.ntiles; tile += gridDim.x) {
-    const int row0 = TM::row0(tile);
-    if (row0 >= a.w.rows) continue;
-    float acc[1][R];
-    mv_team<FMT, R, 1, TL>(a.w, row0, xs, 0, xcs, 0, lane, acc);
+  for (int it = blockIdx.x * T::kTeams + T::team(); it < a.items; it += gridDim.x * T::kTeams) {
+    int rows[R];
+    item_rows<EPI, R>(a, it, rows);
+    double acc[1][R];
+    mv_team<FMT, R, 1, TL>(a.w, rows, xs, 0, lane, acc);
     if (lane != 0) continue;
-    float v[R];
+    if constexpr (EPI == EPI_QKV) {
+      // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts).
+      const float v0 = (float)(acc[0][0] + (double)a.bias[rows[0]]);
+      const float v1 = (float)(acc[0][1] + (double)a.bias[rows[1]]);
+      const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
+      const int rope_pairs = (a.heads + a.kv_heads) * 32;
+      if (pos >= a.capacity) continue;  // the host keeps positions inside the cache
+      if (it < rope_pairs) {
+        const int head = it / 32, j = it % 32;
+        float lo, hi;
+        rope_pair(v0, v1, a.rope_cos[(size_t)pos * 32 + j], a.rope_sin[(size_t)pos * 32 + j], &lo, &hi);
+        if (head < a.heads) {
+          a.out[head * kHeadDim + j] = lo;
+          a.out[head * kHeadDim + j + 32] = hi;
+        } else {
+          uint16_t* k = a.kc + ((size_t)(head - a.heads) * a.capacity + pos) * kHeadDim;
+          k[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
+          k[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
+        }
+      } else {
 #pragma unroll
-    for (int i = 0; i < R; i++) {
-      v[i] = acc[0][i];
-      if constexpr (FMT == QH_FMT_INT8) v[i] = v[i] * a.w.scales[min(row0 + i, a.w.rows - 1)];
-    }
-#pragma unroll
-    for (int i = 0; i < R; i++) {
-      const int r = row0 + i;
-      if (r >= a.w.rows) break;
-      if constexpr (EPI == EPI_BIAS) a.out[r] = v[i] + a.bias[r];
-      if constexpr (EPI == EPI_RESIDUAL) a.out[r] = a.out[r] + v[i];
-      if constexpr (EPI == EPI_LOGITS) {
-        a.out[r] = v[i];
-        if (argmax_better(v[i], r, bv, bi)) {
-          bv = v[i];
-          bi = r;
+        for (int i = 0; i < 2; i++) {
+          const int e = rows[i] - hidden - kvd;  // 0 .. kv_dim-1
+          uint16_t* v = a.vc + ((size_t)(e / kHeadDim) * a.capacity + pos) * kHeadDim + e % kHeadDim;
+          *v = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
         }
       }
-      if constexpr (EPI == EPI_SWIGLU) {
-        // Rows (2j, 2j+1) are gate row j and up row j: h[j] = silu(g) * u, evaluated
-        // in f64 like the CPU path (src/core/ops.js:81-91).
-        if ((i & 1) == 0 && r + 1 < a.w.rows) {
-          const double g = v[i];
-          a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * (double)v[i + 1]);
+    }
+    if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const int r = it * R + i;
+        if (r < a.w.rows) a.out[r] = a.out[r] + (float)acc[0][i];
+      }
+    }
+    if constexpr (EPI == EPI_SWIGLU) {
+      // h[j] = silu(g) * u over the f32 gate and up outputs, in f64 (src/core/ops.js:81-91).
+#pragma unroll
+      for (int i = 0; i < R; i += 2) {
+        const int r = it * R + i;
+        if (r + 1 < a.w.rows) {
+          const double g = (float)acc[0][i];
+          const double u = (float)acc[0][i + 1];
+          a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * u);
+        }
+      }
+    }
+    if constexpr (EPI == EPI_LOGITS) {
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const int r = it * R + i;
+        if (r >= a.w.rows) break;
+        const float v = (float)acc[0][i];
+        a.out[r] = v;
+        if (argmax_better(v, r, bv, bi)) {
+          bv = v;
+          bi = r;
         }
       }
     }
   }
   if constexpr (EPI == EPI_LOGITS) {
-    if (lane == 0) tbest[TM::team()] = {bv, bi};
+    if (lane == 0) tbest[T::team()] = {bv, bi};
     __syncthreads();
     if (threadIdx.x == 0) {
       float v = NAN;
       int i = 0x7fffffff;
-      for (int t = 0; t < TM::kTeams; t++) {
+      for (int t = 0; t < T::kTeams; t++) {
         if (argmax_better(tbest[t].v, tbest[t].i, v, i)) {
           v = tbest[t].v;
           i = tbest[t].i;
@@ -123,10 +188,10 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
     argmax_block(v, i, wred);
     if (threadIdx.x == 0) {
       const int tok = (a.out[0] != a.out[0]) ? 0 : i;
-      const int pos = a.state[0];
-      if (pos < a.capacity) a.pred[pos] = tok;
-      if (pos + 1 >= a.state[1] && pos + 1 <= a.capacity) a.tokens[pos + 1] = tok;
-      a.state[0] = pos + 1;
+      const int p = a.state[0];
+      if (p < a.capacity) a.pred[p] = tok;
+      if (p + 1 >= a.state[1] && p + 1 <= a.capacity) a.tokens[p + 1] = tok;
+      a.state[0] = p + 1;
       *a.counter = 0;
     }
   }
@@ -134,8 +199,11 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
 
 // x = the bf16 embedding row of the token at the current position, widened exactly.
 __global__ void k_embed(const uint16_t* __restrict__ embed, const int* __restrict__ tokens,
-                        const int* __restrict__ state, int hidden, int vocab, float* __restrict__ x) {
-  int tok = tokens[state[0]];
+                        const int* __restrict__ state, int capacity, int hidden, int vocab,
+                        float* __restrict__ x) {
+  const int pos = state[0];
+  if (pos < 0 || pos > capacity) return;  // the host keeps positions inside the cache
+  int tok = tokens[pos];
   tok = (tok < 0 || tok >= vocab) ? 0 : tok;  // ids are validated on the host
   const uint16_t* row = embed + (size_t)tok * hidden;
   for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
@@ -151,56 +219,65 @@ constexpr int kLmRows = 4;        // rows per team in the output head
 constexpr int kLmMaxBlocks = 1024;
 
 template <int FMT, int TL, int R, int PRO, int EPI>
-static hipError_t fused_t(hipStream_t s, FusedArgs a, int max_blocks) {
-  using TM = TeamMap<TL, R>;
-  a.ntiles = (a.w.rows + TM::kRowsPerBlock - 1) / TM::kRowsPerBlock;
-  const int blocks = a.ntiles < max_blocks ? a.ntiles : max_blocks;
-  const size_t lds = (size_t)(a.w.cols + a.w.cols / 32) * sizeof(float);
-  hipLaunchKernelGGL((k_fused<FMT, R, TL, PRO, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
+static hipError_t fused_t(hipStream_t s, FusedArgs a, int items, int max_blocks) {
+  using T = Teams<TL>;
+  a.items = items;
+  int blocks = (items + T::kTeams - 1) / T::kTeams;
+  if (blocks > max_blocks) blocks = max_blocks;
+  const size_t lds = (size_t)a.w.cols * sizeof(double);
+  hipLaunchKernelGGL((k_fused<FMT, TL, R, PRO, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
   return hipGetLastError();
 }
 
 template <int R, int PRO, int EPI>
-static hipError_t fused(hipStream_t s, const FusedArgs& a, int max_blocks = 1 << 30) {
+static hipError_t fused(hipStream_t s, const FusedArgs& a, int items, int max_blocks = 1 << 30) {
   const bool wide = team_width(a.w.nchunks) == 64;
   switch (a.w.format) {
     case QH_FMT_F16:
-      return wide ? fused_t<QH_FMT_F16, 64, R, PRO, EPI>(s, a, max_blocks)
-                  : fused_t<QH_FMT_F16, 32, R, PRO, EPI>(s, a, max_blocks);
+      return wide ? fused_t<QH_FMT_F16, 64, R, PRO, EPI>(s, a, items, max_blocks)
+                  : fused_t<QH_FMT_F16, 32, R, PRO, EPI>(s, a, items, max_blocks);
     case QH_FMT_INT8:
-      return wide ? fused_t<QH_FMT_INT8, 64, R, PRO, EPI>(s, a, max_blocks)
-                  : fused_t<QH_FMT_INT8, 32, R, PRO, EPI>(s, a, max_blocks);
+      return wide ? fused_t<QH_FMT_INT8, 64, R, PRO, EPI>(s, a, items, max_blocks)
+                  : fused_t<QH_FMT_INT8, 32, R, PRO, EPI>(s, a, items, max_blocks);
     default:
-      return wide ? fused_t<QH_FMT_INT4, 64, R, PRO, EPI>(s, a, max_blocks)
-                  : fused_t<QH_FMT_INT4, 32, R, PRO, EPI>(s, a, max_blocks);
+      return wide ? fused_t<QH_FMT_INT4, 64, R, PRO, EPI>(s, a, items, max_blocks)
+                  : fused_t<QH_FMT_INT4, 32, R, PRO, EPI>(s, a, items, max_blocks);
   }
 }
 
 int lm_head_blocks(const ModelDev& m) {
-  const int tl = team_width(m.lm_head.nchunks);
-  const int rows_per_block = (kBlock / tl) * kLmRows;
-  const int tiles = (m.vocab + rows_per_block - 1) / rows_per_block;
-  return tiles < kLmMaxBlocks ? tiles : kLmMaxBlocks;
+  const int teams = kBlock / team_width(m.lm_head.nchunks);
+  const int items = (m.vocab + kLmRows - 1) / kLmRows;
+  const int blocks = (items + teams - 1) / teams;
+  return blocks < kLmMaxBlocks ? blocks : kLmMaxBlocks;
 }
 
 size_t lm_partials_bytes(const ModelDev& m) { return (size_t)lm_head_blocks(m) * sizeof(ArgPair); }
 
-static int attention_grid(int capacity) {
-  int nchunks, cps, splits;
-  attn_splits(capacity, &nchunks, &cps, &splits);
-  return splits;
+int launches_per_step(const ModelDev& m, StepInput in) {
+  return (in == STEP_GATHER ? 1 : 0) + 6 * m.layers + 1;
+}
+
+// Records the event that opens a launch of `role` (see StepTimer).
+static hipError_t mark(hipStream_t s, StepTimer* t, int role) {
+  if (!t) return hipSuccess;
+  if (t->n >= t->capacity) return hipErrorInvalidValue;
+  t->roles[t->n] = role;
+  return hipEventRecord(t->events[t->n++], s);
 }
 
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
-                        bool logits) {
+                        bool logits, StepTimer* timer) {
   hipError_t e;
   if (in == STEP_GATHER) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, m.embed, c.tokens, c.state, m.hidden,
-                       m.vocab, c.x);
+    if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, m.embed, c.tokens, c.state,
+                       c.capacity, m.hidden, m.vocab, c.x);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const int kv_dim = m.kv_heads * m.head_dim;
   const size_t kv_layer = (size_t)m.kv_heads * c.capacity * m.head_dim;
+  const int chunks = attn_chunks(c.capacity);
   for (int L = 0; L < m.layers; L++) {
     const LayerDev& l = m.layers_host[L];
     uint16_t* kc = c.kv + (size_t)L * 2 * kv_layer;
@@ -212,35 +289,45 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     f.in = c.x;
     f.gain = l.in_norm;
     f.bias = l.qkv_bias;
-    f.out = c.qkv;
-    if ((e = fused<2, PRO_RMSNORM, EPI_BIAS>(s, f)) != hipSuccess) return e;
+    f.out = c.q;
+    f.rope_cos = m.rope_cos;
+    f.rope_sin = m.rope_sin;
+    f.kc = kc;
+    f.vc = vc;
+    f.heads = m.heads;
+    f.kv_heads = m.kv_heads;
+    f.state = c.state;
+    f.capacity = c.capacity;
+    if ((e = mark(s, timer, QH_ROLE_QKV)) != hipSuccess) return e;
+    if ((e = fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2)) != hipSuccess)
+      return e;
 
-    AttnArgs a{};
-    a.q = c.qkv;
-    a.k_new = c.qkv + m.hidden;
-    a.v_new = c.qkv + m.hidden + kv_dim;
+    ExactArgs a{};
+    a.q = c.q;
     a.kc = kc;
     a.vc = vc;
-    a.cos_t = m.rope_cos;
-    a.sin_t = m.rope_sin;
     a.d_pos = c.state;
-    a.partials = c.attn_partials;
-    a.counters = c.attn_counters;
+    a.scores = c.scores;
+    a.maxes = c.maxes;
     a.out = c.attn;
-    a.seq = 1;
     a.capacity = c.capacity;
     a.heads = m.heads;
     a.kv_heads = m.kv_heads;
-    a.s_grid = attention_grid(c.capacity);
-    hipLaunchKernelGGL((k_attention<true, true>), dim3(a.s_grid, m.kv_heads, 1), dim3(kBlock), 0,
-                       s, a);
+    a.score_stride = c.capacity;
+    a.max_stride = chunks;
+    if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_scores, dim3(chunks, m.kv_heads, 1), dim3(kBlock), 0, s, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_pv, dim3(m.heads, 1), dim3(kBlock), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
     f = FusedArgs{};
     f.w = l.o;
     f.in = c.attn;
     f.out = c.x;
-    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f)) != hipSuccess) return e;
+    if ((e = mark(s, timer, QH_ROLE_OPROJ)) != hipSuccess) return e;
+    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
 
     f = FusedArgs{};
     f.eps = m.eps;
@@ -248,31 +335,39 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     f.in = c.x;
     f.gain = l.post_norm;
     f.out = c.h;
-    if ((e = fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f)) != hipSuccess) return e;
+    if ((e = mark(s, timer, QH_ROLE_GATEUP)) != hipSuccess) return e;
+    if ((e = fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2)) != hipSuccess) return e;
 
     f = FusedArgs{};
     f.w = l.down;
     f.in = c.h;
     f.out = c.x;
-    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f)) != hipSuccess) return e;
+    if ((e = mark(s, timer, QH_ROLE_DOWN)) != hipSuccess) return e;
+    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.down.rows + 1) / 2)) != hipSuccess) return e;
   }
   if (!logits) {
+    if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, c.state);
-    return hipGetLastError();
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  } else {
+    FusedArgs f{};
+    f.eps = m.eps;
+    f.w = m.lm_head;
+    f.in = c.x;
+    f.gain = m.final_norm;
+    f.out = c.logits;
+    f.partials = static_cast<ArgPair*>(c.lm_partials);
+    f.counter = c.lm_counter;
+    f.state = c.state;
+    f.tokens = c.tokens;
+    f.pred = c.pred;
+    f.capacity = c.capacity;
+    if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
+    if ((e = fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows,
+                                                     kLmMaxBlocks)) != hipSuccess)
+      return e;
   }
-  FusedArgs f{};
-  f.eps = m.eps;
-  f.w = m.lm_head;
-  f.in = c.x;
-  f.gain = m.final_norm;
-  f.out = c.logits;
-  f.partials = static_cast<ArgPair*>(c.lm_partials);
-  f.counter = c.lm_counter;
-  f.state = c.state;
-  f.tokens = c.tokens;
-  f.pred = c.pred;
-  f.capacity = c.capacity;
-  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, kLmMaxBlocks);
+  return mark(s, timer, QH_ROLE_COUNT);
 }
 
 }  // namespace qh

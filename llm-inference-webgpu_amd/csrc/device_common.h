@@ -1,12 +1,19 @@
 // Device building blocks shared by every kernel: wave64 reductions on DPP and
-// ds_swizzle, the 16-byte weight-chunk dot products for the three weight
-// formats, the row-team matvec core, and block-level staging helpers.
+// ds_swizzle, the weight-chunk dot products for the three weight formats, the
+// row-team matvec core, and block-level staging helpers.
 //
-// The matvec core is what both decode and the batched prefill path use, so
-// every output row is summed in one order whatever the number of positions:
-// lane-sequential over that lane's chunks, then a fixed butterfly across the
-// team. That keeps prefill and decode bit-identical, the property the
-// reference's batchedMatvec was written to preserve (src/gpu/kernels.js:217-231).
+// Arithmetic follows the reference CPU path step for step (src/core/ops.js:
+// f32 storage, f64 accumulation). A weight is first dequantized to the f32 the
+// reference's loader would hold -- f32(q*scale), f32((level-zero)*scale), or the
+// f16 value -- and then multiplied into an f64 accumulator, so the only
+// difference from the CPU is the order of an f64 sum (~1e-16 relative), which
+// almost never survives the final rounding to f32.
+//
+// The matvec core is shared by decode and the batched prefill path, so each
+// output row is summed in one order whatever the number of positions: lane-
+// sequential over that lane's 16-byte chunks, then a fixed butterfly across the
+// team. Prefill and decode therefore agree bit for bit, the property the
+// reference's batchedMatvec was written to keep (src/gpu/kernels.js:217-231).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -24,32 +31,52 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 
 // ------------------------------------------------------------- reductions --
-// Butterfly sums inside a team of TL lanes (TL = 16, 32 or 64). Steps of 1, 2,
-// 4 and 8 lanes use DPP (quad_perm, row_half_mirror, row_mirror), 16 uses
-// ds_swizzle, 32 a bpermute. Every lane ends with the same bits.
-__device__ __forceinline__ float dpp_quad_xor1(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+// Butterflies inside a team of TL lanes (TL = 16, 32 or 64): steps of 1, 2, 4
+// and 8 lanes on DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror), 16 on ds_swizzle, 32 on a bpermute. Each step
+// adds a symmetric pair, so every lane ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float dpp_quad_xor2(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float dpp_half_mirror(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float dpp_mirror(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 __device__ __forceinline__ float swz_xor16(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
 }
+__device__ __forceinline__ double swz_xor16(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)u, 0x401F);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_swizzle((int)(uint32_t)(u >> 32), 0x401F);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
 
 template <int TL>
 __device__ __forceinline__ float team_sum(float v) {
   static_assert(TL == 16 || TL == 32 || TL == 64, "team width");
-  v += dpp_quad_xor1(v);
-  v += dpp_quad_xor2(v);
-  v += dpp_half_mirror(v);
-  v += dpp_mirror(v);
+  v += dpp32<kDppQuadXor1>(v);
+  v += dpp32<kDppQuadXor2>(v);
+  v += dpp32<kDppHalfMirror>(v);
+  v += dpp32<kDppMirror>(v);
+  if constexpr (TL >= 32) v += swz_xor16(v);
+  if constexpr (TL >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+
+template <int TL>
+__device__ __forceinline__ double team_sum(double v) {
+  static_assert(TL == 16 || TL == 32 || TL == 64, "team width");
+  v += dpp64<kDppQuadXor1>(v);
+  v += dpp64<kDppQuadXor2>(v);
+  v += dpp64<kDppHalfMirror>(v);
+  v += dpp64<kDppMirror>(v);
   if constexpr (TL >= 32) v += swz_xor16(v);
   if constexpr (TL >= 64) v += __shfl_xor(v, 32);
   return v;
@@ -59,15 +86,11 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
   return v;
 }
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
 
 // Sum over the block (blockDim.x == kBlock) in f64. `red` is LDS of kBlock/kWave doubles.
 // Every thread returns the same value.
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
-  v = wave_sum_f64(v);
+  v = team_sum<64>(v);
   const int wave = threadIdx.x / kWave;
   if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
   __syncthreads();
@@ -90,105 +113,94 @@ __device__ __forceinline__ float f16_lo(uint32_t u) {
 __device__ __forceinline__ float f16_hi(uint32_t u) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
 }
-__device__ __forceinline__ float s8(uint32_t u, int byte) {
-  return (float)(int8_t)(uint8_t)(u >> (8 * byte));
-}
-__device__ __forceinline__ float u8(uint32_t u, int byte) {
-  return (float)((u >> (8 * byte)) & 0xffu);
-}
 
-// acc += sum over the chunk of w[i] * x[i], sequentially in i.
-__device__ __forceinline__ float chunk_f16(const v4u w, const float* __restrict__ x, float acc) {
+// acc += sum over one chunk of w[i] * x[i] in f64, sequentially in i, where w[i]
+// is the f32 weight the reference loader holds:
+//   f16:  the f16 value (exact in f32);
+//   int8: f32(q * scale)          (src/core/quantize.js:60-68);
+//   int4: f32((level - zero) * scale), low nibble = even index (:134-151).
+// Each f32 product here is a single correctly rounded multiply of exact
+// operands, which is what the reference's f64 product stored to f32 is.
+__device__ __forceinline__ double chunk_f16(const v4u w, const double* __restrict__ x, double acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    acc = fmaf(f16_lo(u[j]), x[2 * j], acc);
-    acc = fmaf(f16_hi(u[j]), x[2 * j + 1], acc);
+    acc = fma((double)f16_lo(u[j]), x[2 * j], acc);
+    acc = fma((double)f16_hi(u[j]), x[2 * j + 1], acc);
   }
   return acc;
 }
-__device__ __forceinline__ float chunk_int8(const v4u w, const float* __restrict__ x, float acc) {
+__device__ __forceinline__ double chunk_int8(const v4u w, const double* __restrict__ x, float s,
+                                             double acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-#pragma unroll
-    for (int b = 0; b < 4; b++) acc = fmaf(s8(u[j], b), x[4 * j + b], acc);
-  }
-  return acc;
-}
-// Returns sum over the 32 nibbles of level[i] * x[i] (levels 0..15, low nibble = even index).
-__device__ __forceinline__ float chunk_int4(const v4u w, const float* __restrict__ x) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-  float d = 0.f;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint32_t lo = u[j] & 0x0F0F0F0Fu;
-    const uint32_t hi = (u[j] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-      d = fmaf(u8(lo, b), x[8 * j + 2 * b], d);
-      d = fmaf(u8(hi, b), x[8 * j + 2 * b + 1], d);
+      const float wf = (float)(int8_t)(uint8_t)(u[j] >> (8 * b)) * s;
+      acc = fma((double)wf, x[4 * j + b], acc);
     }
   }
-  return d;
+  return acc;
+}
+__device__ __forceinline__ double chunk_int4(const v4u w, const double* __restrict__ x, float s,
+                                             float z, double acc) {
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+#pragma unroll
+    for (int n = 0; n < 8; n++) {
+      const float wf = ((float)((u[j] >> (4 * n)) & 0xfu) - z) * s;
+      acc = fma((double)wf, x[8 * j + n], acc);
+    }
+  }
+  return acc;
 }
 
 // ------------------------------------------------------------ matvec core --
-// A team of TL lanes computes R consecutive rows starting at row0 for NB
-// positions. Lane `tl` handles chunks tl, tl+TL, ... of every row, so the x
-// chunk it reads is reused across the R rows. x for position b is at
-// xs + b*xstride (LDS or global), and for int4 the per-chunk sums of x at
-// xcs + b*cstride. Rows past the end are computed on a clamped row and must
-// not be stored. On return every lane of the team holds the R*NB sums; int8
-// sums still need the row scale.
+// A team of TL lanes computes R rows (row indices in `rows`, each < m.rows) for
+// NB positions. Lane `tl` handles chunks tl, tl+TL, ... of every row, so the x
+// chunk it reads is reused across the R rows. x for position b is f64 at
+// xs + b*xstride (LDS or global). On return every lane of the team holds the
+// R*NB f64 sums.
 template <int FMT, int R, int NB, int TL>
-__device__ __forceinline__ void mv_team(const DMat& m, int row0, const float* xs, int xstride,
-                                        const float* xcs, int cstride, int tl,
-                                        float (&acc)[NB][R]) {
+__device__ __forceinline__ void mv_team(const DMat& m, const int (&rows)[R], const double* xs,
+                                        int xstride, int tl, double (&acc)[NB][R]) {
   constexpr int W = Fmt<FMT>::kW;
 #pragma unroll
   for (int b = 0; b < NB; b++)
 #pragma unroll
-    for (int i = 0; i < R; i++) acc[b][i] = 0.f;
+    for (int i = 0; i < R; i++) acc[b][i] = 0.0;
 
-  int rr[R];
   const v4u* rp[R];
 #pragma unroll
-  for (int i = 0; i < R; i++) {
-    rr[i] = min(row0 + i, m.rows - 1);
-    rp[i] = reinterpret_cast<const v4u*>(m.data + (size_t)rr[i] * m.row_bytes);
+  for (int i = 0; i < R; i++) rp[i] = reinterpret_cast<const v4u*>(m.data + (size_t)rows[i] * m.row_bytes);
+  float srow[R];
+  if constexpr (FMT == QH_FMT_INT8) {
+#pragma unroll
+    for (int i = 0; i < R; i++) srow[i] = m.scales[rows[i]];
   }
   for (int c = tl; c < m.nchunks; c += TL) {
     v4u w[R];
 #pragma unroll
     for (int i = 0; i < R; i++) w[i] = __builtin_nontemporal_load(&rp[i][c]);
+    float s[R], z[R];
     if constexpr (FMT == QH_FMT_INT4) {
       const int g = c / m.cpg;
-      float s[R], z[R];
 #pragma unroll
       for (int i = 0; i < R; i++) {
-        s[i] = m.scales[(size_t)rr[i] * m.gpr + g];
-        z[i] = m.zeros[(size_t)rr[i] * m.gpr + g];
+        s[i] = m.scales[(size_t)rows[i] * m.gpr + g];
+        z[i] = m.zeros[(size_t)rows[i] * m.gpr + g];
       }
+    }
 #pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const float* xc = xs + (size_t)b * xstride + (size_t)c * W;
-        const float xsum = xcs[(size_t)b * cstride + c];
+    for (int b = 0; b < NB; b++) {
+      const double* xc = xs + (size_t)b * xstride + (size_t)c * W;
 #pragma unroll
-        for (int i = 0; i < R; i++) {
-          const float d = chunk_int4(w[i], xc);
-          acc[b][i] = fmaf(s[i], fmaf(-z[i], xsum, d), acc[b][i]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int b = 0; b < NB; b++) {
-        const float* xc = xs + (size_t)b * xstride + (size_t)c * W;
-#pragma unroll
-        for (int i = 0; i < R; i++) {
-          if constexpr (FMT == QH_FMT_F16) acc[b][i] = chunk_f16(w[i], xc, acc[b][i]);
-          else acc[b][i] = chunk_int8(w[i], xc, acc[b][i]);
-        }
+      for (int i = 0; i < R; i++) {
+        if constexpr (FMT == QH_FMT_F16) acc[b][i] = chunk_f16(w[i], xc, acc[b][i]);
+        else if constexpr (FMT == QH_FMT_INT8) acc[b][i] = chunk_int8(w[i], xc, srow[i], acc[b][i]);
+        else acc[b][i] = chunk_int4(w[i], xc, s[i], z[i], acc[b][i]);
       }
     }
   }
@@ -198,59 +210,45 @@ __device__ __forceinline__ void mv_team(const DMat& m, int row0, const float* xs
     for (int i = 0; i < R; i++) acc[b][i] = team_sum<TL>(acc[b][i]);
 }
 
-// Teams of TL lanes with R rows each, laid over a block of kBlock threads.
-template <int TL, int R>
-struct TeamMap {
-  static constexpr int kTeams = kBlock / TL;
-  static constexpr int kRowsPerBlock = kTeams * R;
-  __device__ static int team() { return threadIdx.x / TL; }
-  __device__ static int lane() { return threadIdx.x & (TL - 1); }
-  __device__ static int row0(int block) { return (block * kTeams + team()) * R; }
-};
-
-// --------------------------------------------------------- block staging --
-// y = x / sqrt(mean(x^2) + eps) * gain into LDS, with the statistic and the
-// products in f64 exactly as the reference CPU path evaluates them
-// (src/core/ops.js:17-24), so the normalized vector matches it to the bit
-// up to the order of the f64 sum.
-__device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
-                                              const float* __restrict__ gain, double eps, int cols,
-                                              float* xs, double* red) {
-  double ss = 0;
-  for (int i = threadIdx.x; i < cols; i += kBlock) {
-    const float v = x[i];
-    xs[i] = v;
-    ss += (double)v * (double)v;
-  }
-  ss = block_sum_f64(ss, red);
-  const double scale = 1.0 / sqrt(ss / cols + eps);
-  for (int i = threadIdx.x; i < cols; i += kBlock) {
-    xs[i] = (float)((double)xs[i] * scale * (double)gain[i]);
-  }
-  __syncthreads();
-}
-
-// Per-chunk sums of x (32 columns each), for the int4 zero-point term.
-__device__ __forceinline__ void stage_chunk_sums(const float* xs, int cols, float* xcs) {
-  const int n = cols / 32;
-  for (int c = threadIdx.x; c < n; c += kBlock) {
-    float s = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < 32; j++) s += xs[c * 32 + j];
-    xcs[c] = s;
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ void stage_copy(const float* __restrict__ x, int n, float* xs) {
-  for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = x[i];
-  __syncthreads();
-}
-
 // Team width of a matrix: 32 lanes when a row has at most 32 chunks, else 64.
 // It fixes which chunks a lane sums and the butterfly, so it is a function of
 // the shape alone and every path over a given matrix sums in one order.
 __host__ __device__ inline int team_width(int nchunks) { return nchunks <= 32 ? 32 : 64; }
+
+// Teams of TL lanes over a block of kBlock threads.
+template <int TL>
+struct Teams {
+  static constexpr int kTeams = kBlock / TL;
+  __device__ static int team() { return threadIdx.x / TL; }
+  __device__ static int lane() { return threadIdx.x & (TL - 1); }
+};
+
+// --------------------------------------------------------- block staging --
+// xs = x / sqrt(mean(x^2) + eps) * gain as f64 values of the f32 result, with
+// the statistic and the products in f64 as src/core/ops.js:17-24 evaluates
+// them, so the normalized vector is the CPU's up to the order of the f64 sum.
+__device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
+                                              const float* __restrict__ gain, double eps, int cols,
+                                              double* xs, double* red) {
+  double ss = 0;
+  for (int i = threadIdx.x; i < cols; i += kBlock) {
+    const double v = x[i];
+    xs[i] = v;
+    ss = fma(v, v, ss);  // v*v is exact in f64, so the fused form rounds once like the CPU's
+  }
+  ss = block_sum_f64(ss, red);
+  const double scale = 1.0 / sqrt(ss / cols + eps);
+  for (int i = threadIdx.x; i < cols; i += kBlock) {
+    xs[i] = (double)(float)(xs[i] * scale * (double)gain[i]);
+  }
+  __syncthreads();
+}
+
+// xs = (double)x for an f32 vector.
+__device__ __forceinline__ void stage_copy(const float* __restrict__ x, int n, double* xs) {
+  for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = (double)x[i];
+  __syncthreads();
+}
 
 struct ArgPair {
   float v;
@@ -292,6 +290,17 @@ __device__ __forceinline__ void argmax_block(float& v, int& i, ArgPair* red) {
       }
     }
   }
+}
+
+// The reference's rotation (src/core/ops.js:147-159) of the pair (lo, hi) by
+// f64 cos/sin, without contracting the products into a fused multiply-add, so
+// each product and the difference round separately as they do in JavaScript.
+__device__ __forceinline__ void rope_pair(float lo, float hi, double c, double s, float* out_lo,
+                                          float* out_hi) {
+#pragma clang fp contract(off)
+  const double l = lo, h = hi;
+  *out_lo = (float)(l * c - h * s);
+  *out_hi = (float)(h * c + l * s);
 }
 
 }  // namespace qh

@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 
 #include "qh_internal.h"
 
@@ -68,6 +69,25 @@ uint16_t f32_to_bf16(float x) {
 }
 
 }  // namespace
+
+namespace qh {
+
+// src/core/ops.js:99-136: inv_freq = theta^(-2j/headDim); angle = p * inv_freq in f64.
+void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t) {
+  const int half = head_dim / 2;
+  double inv[4096];
+  for (int j = 0; j < half && j < 4096; j++) inv[j] = std::pow(theta, (-2.0 * j) / head_dim);
+#pragma omp parallel for schedule(static)
+  for (int p = 0; p < positions; p++) {
+    for (int j = 0; j < half; j++) {
+      const double angle = p * inv[j];
+      cos_t[(size_t)p * half + j] = std::cos(angle);
+      sin_t[(size_t)p * half + j] = std::sin(angle);
+    }
+  }
+}
+
+}  // namespace qh
 
 using qh::fail;
 
@@ -150,16 +170,12 @@ int qh_rope_tables(int32_t head_dim, double theta, int32_t positions, float* h_c
   QH_CHECK(h_cos && h_sin && head_dim >= 2 && head_dim % 2 == 0 && positions >= 1, QH_ERR_INVALID,
            "rope_tables needs an even head_dim, positions >= 1 and outputs");
   const int half = head_dim / 2;
-  double inv[4096];
   QH_CHECK(half <= 4096, QH_ERR_INVALID, "head_dim %d too large", head_dim);
-  for (int j = 0; j < half; j++) inv[j] = std::pow(theta, (-2.0 * j) / head_dim);
-#pragma omp parallel for schedule(static)
-  for (int p = 0; p < positions; p++) {
-    for (int j = 0; j < half; j++) {
-      const double angle = p * inv[j];
-      h_cos[(size_t)p * half + j] = (float)std::cos(angle);
-      h_sin[(size_t)p * half + j] = (float)std::sin(angle);
-    }
+  std::vector<double> c((size_t)positions * half), s((size_t)positions * half);
+  qh::rope_tables_f64(head_dim, theta, positions, c.data(), s.data());
+  for (size_t i = 0; i < c.size(); i++) {
+    h_cos[i] = (float)c[i];
+    h_sin[i] = (float)s[i];
   }
   return QH_OK;
 }

@@ -391,13 +391,14 @@ int qh_model_finalize(qh_model* m) {
   for (auto& n : consumed) free_staged(m->staged[n]);
   m->staged.clear();
 
-  // Rope tables from host f64 (src/core/ops.js:123-136, src/gpu/model.js:201-205).
-  std::vector<float> cs((size_t)c.max_positions * 32), sn((size_t)c.max_positions * 32);
-  if ((rc = qh_rope_tables(c.head_dim, c.rope_theta, c.max_positions, cs.data(), sn.data()))) return rc;
-  float *dcos = nullptr, *dsin = nullptr;
-  if ((rc = m->alloc(cs.size() * 4, (void**)&dcos)) || (rc = m->alloc(sn.size() * 4, (void**)&dsin))) return rc;
-  QH_HIP(hipMemcpy(dcos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
-  QH_HIP(hipMemcpy(dsin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  // Rope cos/sin in f64 from the host's libm: the values src/core/ops.js:147-159 rotates
+  // by (ropeInPlace evaluates them per call; here they are tabulated once).
+  std::vector<double> cs((size_t)c.max_positions * 32), sn((size_t)c.max_positions * 32);
+  qh::rope_tables_f64(c.head_dim, c.rope_theta, c.max_positions, cs.data(), sn.data());
+  double *dcos = nullptr, *dsin = nullptr;
+  if ((rc = m->alloc(cs.size() * 8, (void**)&dcos)) || (rc = m->alloc(sn.size() * 8, (void**)&dsin))) return rc;
+  QH_HIP(hipMemcpy(dcos, cs.data(), cs.size() * 8, hipMemcpyHostToDevice));
+  QH_HIP(hipMemcpy(dsin, sn.data(), sn.size() * 8, hipMemcpyHostToDevice));
 
   qh::ModelDev& d = m->dev;
   d.hidden = c.hidden;
@@ -444,9 +445,7 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   c->m = m;
   qh::CacheDev& d = c->dev;
   d.capacity = capacity;
-  const int kv_dim = md.kv_heads * md.head_dim;
-  int nchunks, cps, splits;
-  qh::attn_splits_host(capacity, &nchunks, &cps, &splits);
+  const int chunks = (capacity + 63) / 64;
   const size_t kv_bytes = (size_t)md.layers * 2 * md.kv_heads * capacity * md.head_dim * 2;
   int rc = QH_OK;
   auto A = [&](size_t n, void** p) {
@@ -457,12 +456,12 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   A((size_t)(capacity + 1) * 4, (void**)&d.tokens);
   A((size_t)capacity * 4, (void**)&d.pred);
   A((size_t)md.hidden * 4, (void**)&d.x);
-  A((size_t)(md.hidden + 2 * kv_dim) * 4, (void**)&d.qkv);
+  A((size_t)md.hidden * 4, (void**)&d.q);
   A((size_t)md.hidden * 4, (void**)&d.attn);
   A((size_t)md.intermediate * 4, (void**)&d.h);
   A((size_t)md.vocab * 4, (void**)&d.logits);
-  A((size_t)splits * md.kv_heads * (md.heads / md.kv_heads) * (md.head_dim + 2) * 4, (void**)&d.attn_partials);
-  A(256, (void**)&d.attn_counters);
+  A((size_t)md.heads * capacity * 4, (void**)&d.scores);
+  A((size_t)md.heads * chunks * 4, (void**)&d.maxes);
   A(qh::lm_partials_bytes(md), &d.lm_partials);
   A(256, (void**)&d.lm_counter);
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
@@ -471,7 +470,6 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   if (!rc && (hipMemset(d.kv, 0, kv_bytes) != hipSuccess || hipMemset(d.state, 0, 256) != hipSuccess ||
               hipMemset(d.tokens, 0, (size_t)(capacity + 1) * 4) != hipSuccess ||
               hipMemset(d.pred, 0, (size_t)capacity * 4) != hipSuccess ||
-              hipMemset(d.attn_counters, 0, 256) != hipSuccess ||
               hipMemset(d.lm_counter, 0, 256) != hipSuccess)) {
     rc = fail(QH_ERR_DEVICE, "clearing the cache failed");
   }
@@ -689,6 +687,49 @@ int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int3
   int rc = qh_decode_launch(m, c, first_token, steps);
   if (rc) return rc;
   return qh_decode_collect(m, c, steps, h_tokens);
+}
+
+int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps,
+                      int32_t* h_tokens, float* h_role_ms, int32_t* h_role_launches) {
+  QH_CHECK(m && c && c->m == m && h_role_ms && h_role_launches, QH_ERR_INVALID,
+           "decode_profile needs a model, its cache and role outputs");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(steps >= 1, QH_ERR_INVALID, "decode needs steps >= 1");
+  QH_CHECK(first_token >= 0 && first_token < m->dev.vocab, QH_ERR_RANGE,
+           "token %d is outside the vocabulary", first_token);
+  int rc = check_room(c, steps);
+  if (rc) return rc;
+  BusyGuard guard(c);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  const int n_ev = qh::launches_per_step(m->dev, qh::STEP_GATHER) + 1;
+  std::vector<hipEvent_t> ev(n_ev, nullptr);
+  std::vector<int> roles(n_ev, 0);
+  for (auto& e : ev) QH_HIP(hipEventCreate(&e));
+  for (int r = 0; r < QH_ROLE_COUNT; r++) h_role_ms[r] = 0.f, h_role_launches[r] = 0;
+  const int start = c->length;
+  c->h_pinned[3] = first_token;
+  hipError_t err = hipMemcpyAsync(c->dev.tokens + start, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s);
+  if (err == hipSuccess && (rc = set_state(c, start, start + 1))) err = hipErrorUnknown;
+  for (int i = 0; i < steps && err == hipSuccess; i++) {
+    qh::StepTimer t{ev.data(), roles.data(), n_ev, 0};
+    err = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, true, &t);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+    for (int k = 0; err == hipSuccess && k + 1 < t.n; k++) {
+      float ms = 0.f;
+      err = hipEventElapsedTime(&ms, ev[k], ev[k + 1]);
+      h_role_ms[roles[k]] += ms;
+      h_role_launches[roles[k]] += 1;
+    }
+  }
+  if (err == hipSuccess && h_tokens) {
+    err = hipMemcpy(h_tokens, c->dev.pred + start, (size_t)steps * 4, hipMemcpyDeviceToHost);
+  }
+  for (auto& e : ev) hipEventDestroy(e);
+  if (rc) return rc;
+  QH_HIP(err);
+  c->length += steps;
+  return QH_OK;
 }
 
 }  // extern "C"

@@ -26,8 +26,8 @@ struct ModelDev {
   DMat lm_head;                 // [vocab, hidden]
   const float* final_norm;
   const uint16_t* embed;        // [vocab, hidden] bf16
-  const float* rope_cos;        // [max_positions, 32]
-  const float* rope_sin;
+  const double* rope_cos;       // [max_positions, 32], f64 as the CPU path rotates
+  const double* rope_sin;
 };
 
 struct CacheDev {
@@ -37,12 +37,12 @@ struct CacheDev {
   int* tokens;         // [capacity + 1] token consumed at each position
   int* pred;           // [capacity] argmax after each position
   float* x;            // [hidden] residual stream
-  float* qkv;          // [hidden + 2*kv_dim]
+  float* q;            // [hidden] rotated queries
   float* attn;         // [hidden]
   float* h;            // [intermediate]
   float* logits;       // [vocab]
-  float* attn_partials;
-  int* attn_counters;  // [kv_heads]
+  float* scores;       // [heads][capacity]: scores, then softmax weights
+  float* maxes;        // [heads][chunks(capacity)]: per-chunk score maxima
   void* lm_partials;   // argmax block partials
   int* lm_counter;
   int lm_blocks;
@@ -51,11 +51,22 @@ struct CacheDev {
 // How a step obtains its input row.
 enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1 };
 
+// Optional per-launch timing: an event is recorded before every launch (tagged with
+// its QH_ROLE_*) and one after the last, so launch i took events[i+1] - events[i].
+struct StepTimer {
+  hipEvent_t* events;
+  int* roles;
+  int capacity;  // events available
+  int n;         // events recorded
+};
+
 // Launches one decode position: [gather] -> layers -> (lm_head + argmax, or a
 // position advance when `logits` is false). With STEP_HIDDEN the caller has
 // already written the input row into cache.x.
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
-                        bool logits);
+                        bool logits, StepTimer* timer = nullptr);
+// Launches in one step (the events a StepTimer needs, minus the final one).
+int launches_per_step(const ModelDev& m, StepInput in);
 // Blocks the lm_head launch uses (sizes lm_partials).
 int lm_head_blocks(const ModelDev& m);
 size_t lm_partials_bytes(const ModelDev& m);

@@ -1,126 +1,152 @@
 // Kernels and launchers for the standalone operator surface: matvec (f32 and
 // f16 activations, single and list-driven), rmsnorm, rope, KV append,
-// attention, swiglu, residual add and argmax. Each replaces one WGSL kernel of
-// src/gpu/kernels.js; the fused decode step (decode.hip) reuses the same
-// device building blocks.
+// attention (exact order and split-K), swiglu, residual add and argmax. Each
+// replaces one WGSL kernel of src/gpu/kernels.js; the decode step
+// (decode.hip) is built from the same device building blocks.
 #include "attention.h"
 #include "device_common.h"
 
 namespace qh {
 
 // ------------------------------------------------------------------ matvec --
-// y[b, r] = sum_c W[r, c] x[b, c] (+ bias[r]) for NB positions per block row.
-// x (and the int4 chunk sums) staged in LDS when they fit, else x read from
-// global memory through the caches.
+// y[b, r] = f32(sum_c W[r, c] x[b, c] + bias[r]) for NB positions per block,
+// positions b_base + blockIdx.y*NB .. +NB-1 (launches cover whole tiles only).
+// x is staged in LDS as f64 when NB*cols doubles fit, else read as an f64 copy
+// from global memory. Teams of TL lanes compute R consecutive rows.
 template <int FMT, int R, int NB, int TL, bool X_LDS>
 __global__ __launch_bounds__(kBlock) void k_matvec(DMat m, const float* __restrict__ x,
+                                                   const double* __restrict__ x64,
                                                    const float* __restrict__ bias,
-                                                   float* __restrict__ y, int seq) {
-  extern __shared__ float smem[];
-  const int b0 = blockIdx.y * NB;
-  const int nb = min(NB, seq - b0);
-  float* xs = smem;                                     // [NB][cols] when X_LDS
-  float* xcs = smem + (X_LDS ? NB * m.cols : 0);        // [NB][nchunks] for int4
-  const float* xsrc = x + (size_t)b0 * m.cols;
+                                                   float* __restrict__ y, int b_base) {
+  extern __shared__ double smem[];
+  const int b0 = b_base + blockIdx.y * NB;
+  const double* xuse;
   if constexpr (X_LDS) {
-    for (int i = threadIdx.x; i < NB * m.cols; i += kBlock) {
-      xs[i] = i < nb * m.cols ? xsrc[i] : 0.f;
-    }
+    const float* xsrc = x + (size_t)b0 * m.cols;
+    for (int i = threadIdx.x; i < NB * m.cols; i += kBlock) smem[i] = (double)xsrc[i];
     __syncthreads();
-  }
-  const float* xuse = X_LDS ? xs : xsrc;
-  if constexpr (FMT == QH_FMT_INT4) {
-    for (int e = threadIdx.x; e < NB * m.nchunks; e += kBlock) {
-      const int b = e / m.nchunks, c = e % m.nchunks;
-      float s = 0.f;
-      if (b < nb) {
-        const float* xc = xuse + (size_t)b * m.cols + (size_t)c * 32;
-#pragma unroll 8
-        for (int j = 0; j < 32; j++) s += xc[j];
-      }
-      xcs[e] = s;
-    }
-    __syncthreads();
-  }
-  // Positions past the end read position 0's x (never stored).
-  using TM = TeamMap<TL, R>;
-  const int row0 = TM::row0(blockIdx.x);
-  if (row0 >= m.rows) return;
-  float acc[NB][R];
-  if (X_LDS || nb == NB) {
-    mv_team<FMT, R, NB, TL>(m, row0, xuse, m.cols, xcs, m.nchunks, TM::lane(), acc);
+    xuse = smem;
   } else {
-    // Tail tile reading x from global: clamp positions to stay in bounds.
-    mv_team<FMT, R, NB, TL>(m, row0, xuse, 0, xcs, 0, TM::lane(), acc);
+    xuse = x64 + (size_t)b0 * m.cols;
   }
-  if (TM::lane() == 0) {
+  using T = Teams<TL>;
+  const int row0 = (blockIdx.x * T::kTeams + T::team()) * R;
+  if (row0 >= m.rows) return;
+  int rows[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) rows[i] = min(row0 + i, m.rows - 1);
+  double acc[NB][R];
+  mv_team<FMT, R, NB, TL>(m, rows, xuse, m.cols, T::lane(), acc);
+  if (T::lane() == 0) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-      if (b >= nb) break;
 #pragma unroll
       for (int i = 0; i < R; i++) {
         const int r = row0 + i;
         if (r >= m.rows) break;
-        float v = acc[b][i];
-        if constexpr (FMT == QH_FMT_INT8) v = v * m.scales[r];
-        if (bias) v = v + bias[r];
-        y[(size_t)(b0 + b) * m.rows + r] = v;
+        // The CPU's sum starts from the bias (src/core/ops.js:36); the f64 order only.
+        const double v = bias ? acc[b][i] + (double)bias[r] : acc[b][i];
+        y[(size_t)(b0 + b) * m.rows + r] = (float)v;
       }
     }
   }
 }
 
+__global__ void k_widen(const float* __restrict__ x, double* __restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (double)x[i];
+}
+
+constexpr size_t kMatvecLdsBytes = 64 * 1024;
+
+template <int NB>
+static bool x_in_lds(const DMat& m) { return (size_t)NB * m.cols * sizeof(double) <= kMatvecLdsBytes; }
+
+// `tiles` whole tiles of NB positions starting at position b_base.
 template <int FMT, int NB, int TL>
-static hipError_t matvec_tl(hipStream_t s, const DMat& m, const float* x, const float* bias,
-                            float* y, int seq) {
+static hipError_t matvec_tl(hipStream_t s, const DMat& m, const float* x, const double* x64,
+                            const float* bias, float* y, int b_base, int tiles) {
   constexpr int R = 2;
-  using TM = TeamMap<TL, R>;
-  const size_t x_bytes = (size_t)NB * m.cols * sizeof(float);
-  const size_t c_bytes = FMT == QH_FMT_INT4 ? (size_t)NB * m.nchunks * sizeof(float) : 0;
-  const dim3 grid((m.rows + TM::kRowsPerBlock - 1) / TM::kRowsPerBlock, (seq + NB - 1) / NB);
-  if (x_bytes + c_bytes <= 48 * 1024) {
-    hipLaunchKernelGGL((k_matvec<FMT, R, NB, TL, true>), grid, dim3(kBlock), x_bytes + c_bytes, s,
-                       m, x, bias, y, seq);
+  const int rows_per_block = (kBlock / TL) * R;
+  const dim3 grid((m.rows + rows_per_block - 1) / rows_per_block, tiles);
+  if (x_in_lds<NB>(m)) {
+    hipLaunchKernelGGL((k_matvec<FMT, R, NB, TL, true>), grid, dim3(kBlock),
+                       (size_t)NB * m.cols * sizeof(double), s, m, x, x64, bias, y, b_base);
   } else {
-    hipLaunchKernelGGL((k_matvec<FMT, R, NB, TL, false>), grid, dim3(kBlock), c_bytes, s, m, x,
-                       bias, y, seq);
+    hipLaunchKernelGGL((k_matvec<FMT, R, NB, TL, false>), grid, dim3(kBlock), 0, s, m, x, x64,
+                       bias, y, b_base);
   }
   return hipGetLastError();
 }
 
 template <int FMT, int NB>
-static hipError_t matvec_nb(hipStream_t s, const DMat& m, const float* x, const float* bias,
-                            float* y, int seq) {
-  if (team_width(m.nchunks) == 32) return matvec_tl<FMT, NB, 32>(s, m, x, bias, y, seq);
-  return matvec_tl<FMT, NB, 64>(s, m, x, bias, y, seq);
+static hipError_t matvec_nb(hipStream_t s, const DMat& m, const float* x, const double* x64,
+                            const float* bias, float* y, int b_base, int tiles) {
+  if (team_width(m.nchunks) == 32) return matvec_tl<FMT, NB, 32>(s, m, x, x64, bias, y, b_base, tiles);
+  return matvec_tl<FMT, NB, 64>(s, m, x, x64, bias, y, b_base, tiles);
 }
 
 template <int FMT>
-static hipError_t matvec_fmt(hipStream_t s, const DMat& m, const float* x, const float* bias,
-                             float* y, int seq) {
-  // The position tile of src/gpu/model.js:133-138. It decides only how many
-  // positions share a weight read, never how an output is summed.
-  if (seq >= 8) return matvec_nb<FMT, 8>(s, m, x, bias, y, seq);
-  if (seq >= 4) return matvec_nb<FMT, 4>(s, m, x, bias, y, seq);
-  if (seq >= 2) return matvec_nb<FMT, 2>(s, m, x, bias, y, seq);
-  return matvec_nb<FMT, 1>(s, m, x, bias, y, seq);
+static hipError_t matvec_fmt(hipStream_t s, const DMat& m, const float* x, const double* x64,
+                             const float* bias, float* y, int seq) {
+  // Tiles of 8 positions (src/gpu/model.js:133-138 batchTileFor), then 4, 2 and 1 for the
+  // remainder. The tile decides only how many positions share a weight read, never how an
+  // output is summed.
+  hipError_t e = hipSuccess;
+  int done = 0;
+  if (seq >= 8) {
+    if ((e = matvec_nb<FMT, 8>(s, m, x, x64, bias, y, 0, seq / 8)) != hipSuccess) return e;
+    done = seq / 8 * 8;
+  }
+  if (seq - done >= 4) {
+    if ((e = matvec_nb<FMT, 4>(s, m, x, x64, bias, y, done, 1)) != hipSuccess) return e;
+    done += 4;
+  }
+  if (seq - done >= 2) {
+    if ((e = matvec_nb<FMT, 2>(s, m, x, x64, bias, y, done, 1)) != hipSuccess) return e;
+    done += 2;
+  }
+  if (seq - done >= 1) e = matvec_nb<FMT, 1>(s, m, x, x64, bias, y, done, 1);
+  return e;
+}
+
+size_t matvec_x64_bytes(const DMat& m, int seq) {
+  // Tiles whose x does not fit in LDS read an f64 copy of all positions.
+  const bool any_global = !x_in_lds<1>(m) || (seq >= 2 && !x_in_lds<2>(m)) ||
+                          (seq >= 4 && !x_in_lds<4>(m)) || (seq >= 8 && !x_in_lds<8>(m));
+  return any_global ? (size_t)seq * m.cols * sizeof(double) : 0;
 }
 
 hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
-                         int seq) {
-  switch (m.format) {
-    case QH_FMT_F16: return matvec_fmt<QH_FMT_F16>(s, m, x, bias, y, seq);
-    case QH_FMT_INT8: return matvec_fmt<QH_FMT_INT8>(s, m, x, bias, y, seq);
-    default: return matvec_fmt<QH_FMT_INT4>(s, m, x, bias, y, seq);
+                         int seq, double* x64_scratch) {
+  const size_t need = matvec_x64_bytes(m, seq);
+  double* x64 = nullptr;
+  hipError_t e = hipSuccess;
+  if (need) {
+    x64 = x64_scratch;
+    if (!x64 && (e = hipMallocAsync((void**)&x64, need, s)) != hipSuccess) return e;
+    const size_t n = (size_t)seq * m.cols;
+    hipLaunchKernelGGL(k_widen, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, x64, n);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
+  switch (m.format) {
+    case QH_FMT_F16: e = matvec_fmt<QH_FMT_F16>(s, m, x, x64, bias, y, seq); break;
+    case QH_FMT_INT8: e = matvec_fmt<QH_FMT_INT8>(s, m, x, x64, bias, y, seq); break;
+    default: e = matvec_fmt<QH_FMT_INT4>(s, m, x, x64, bias, y, seq); break;
+  }
+  if (need && !x64_scratch) {
+    const hipError_t f = hipFreeAsync(x64, s);
+    if (e == hipSuccess) e = f;
+  }
+  return e;
 }
 
 // ------------------------------------------- matvec with an f16 activation --
-// The isolated-matvec shape: x f16, one output vector per matrix in a list.
-// Weights are widened to exact f16 pairs and multiplied with v_dot2_f32_f16:
-// int8 code q becomes the f16 1152+q by a byte permute against 0x64 (1024 + the
-// biased byte q+128) and a packed subtract of 1152, which is exact; int4 levels
-// likewise from 1024+level minus (1024+zero). Accumulation is f32.
+// The isolated-matvec shape: x f16, int8 weights, one output
+// vector per matrix of a list. Codes are widened to exact f16 pairs and
+// multiplied with v_dot2_f32_f16: code q becomes the f16 1152+q by a byte
+// permute against 0x64 (1024 + the biased byte q+128) and a packed subtract of
+// 1152, both exact; accumulation is f32 and the row scale multiplies the sum.
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
@@ -135,22 +161,23 @@ __device__ __forceinline__ float dot8_int8_h(uint32_t u, const half2_t* xp, floa
   return acc;
 }
 
-template <int FMT, int R, int TL>
+template <int R, int TL>
 __global__ __launch_bounds__(kBlock) void k_matvec_xh_list(DMat m, int count, size_t data_stride,
                                                            size_t scale_stride,
                                                            const uint16_t* __restrict__ x,
                                                            size_t x_stride, float* __restrict__ y) {
-  using TM = TeamMap<TL, R>;
-  const int blocks_per_mat = (m.rows + TM::kRowsPerBlock - 1) / TM::kRowsPerBlock;
+  using T = Teams<TL>;
+  constexpr int kRowsPerBlock = T::kTeams * R;
+  const int blocks_per_mat = (m.rows + kRowsPerBlock - 1) / kRowsPerBlock;
   const int mat = blockIdx.x / blocks_per_mat;
   const int rb = blockIdx.x % blocks_per_mat;
   if (mat >= count) return;
-  const int row0 = TM::row0(rb);
+  const int row0 = (rb * T::kTeams + T::team()) * R;
   if (row0 >= m.rows) return;
   const uint8_t* data = m.data + (size_t)mat * data_stride;
   const float* scales = m.scales + (size_t)mat * scale_stride;
   const half2_t* xh = reinterpret_cast<const half2_t*>(x + (size_t)mat * x_stride);
-  const int tl = TM::lane();
+  const int tl = T::lane();
 
   float acc[R];
   const v4u* rp[R];
@@ -163,7 +190,6 @@ __global__ __launch_bounds__(kBlock) void k_matvec_xh_list(DMat m, int count, si
     v4u w[R];
 #pragma unroll
     for (int i = 0; i < R; i++) w[i] = __builtin_nontemporal_load(&rp[i][c]);
-    static_assert(FMT == QH_FMT_INT8, "f16-activation list matvec is int8");
     // 16 weights per chunk: x halves 16c .. 16c+15 as 8 pairs.
     half2_t xp[8];
     const v4u xa = reinterpret_cast<const v4u*>(xh)[2 * c];
@@ -193,16 +219,15 @@ hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t
                                  size_t scale_stride, const uint16_t* x, size_t x_stride,
                                  float* y) {
   constexpr int R = 4;
-  if (team_width(m.nchunks) == 32) {
-    using TM = TeamMap<32, R>;
-    const size_t bpm = (m.rows + TM::kRowsPerBlock - 1) / TM::kRowsPerBlock;
-    hipLaunchKernelGGL((k_matvec_xh_list<QH_FMT_INT8, R, 32>), dim3(bpm * count), dim3(kBlock), 0,
-                       s, m, count, data_stride, scale_stride, x, x_stride, y);
+  const int tl = team_width(m.nchunks);
+  const size_t rows_per_block = (size_t)(kBlock / tl) * R;
+  const size_t bpm = (m.rows + rows_per_block - 1) / rows_per_block;
+  if (tl == 32) {
+    hipLaunchKernelGGL((k_matvec_xh_list<R, 32>), dim3(bpm * count), dim3(kBlock), 0, s, m, count,
+                       data_stride, scale_stride, x, x_stride, y);
   } else {
-    using TM = TeamMap<64, R>;
-    const size_t bpm = (m.rows + TM::kRowsPerBlock - 1) / TM::kRowsPerBlock;
-    hipLaunchKernelGGL((k_matvec_xh_list<QH_FMT_INT8, R, 64>), dim3(bpm * count), dim3(kBlock), 0,
-                       s, m, count, data_stride, scale_stride, x, x_stride, y);
+    hipLaunchKernelGGL((k_matvec_xh_list<R, 64>), dim3(bpm * count), dim3(kBlock), 0, s, m, count,
+                       data_stride, scale_stride, x, x_stride, y);
   }
   return hipGetLastError();
 }
@@ -211,22 +236,22 @@ hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t
 __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float* __restrict__ x,
                                                     const float* __restrict__ gain,
                                                     float* __restrict__ y, int cols, double eps) {
-  extern __shared__ float smem[];
+  extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   const size_t base = (size_t)blockIdx.x * cols;
   stage_rmsnorm(x + base, gain, eps, cols, smem, red);
-  for (int i = threadIdx.x; i < cols; i += kBlock) y[base + i] = smem[i];
+  for (int i = threadIdx.x; i < cols; i += kBlock) y[base + i] = (float)smem[i];
 }
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
                           int cols, double eps) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), cols * sizeof(float), s, x, gain, y,
+  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), cols * sizeof(double), s, x, gain, y,
                      cols, eps);
   return hipGetLastError();
 }
 
 // -------------------------------------------------------------------- rope --
-// One thread per (row, head, pair), as ROPE (kernels.js:368-389).
+// One thread per (row, head, pair), from f32 tables, as ROPE (kernels.js:368-389).
 __global__ void k_rope(float* __restrict__ v, const float* __restrict__ cos_t,
                        const float* __restrict__ sin_t, int rows, int heads, int head_dim,
                        int base_pos) {
@@ -276,28 +301,45 @@ hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint1
 }
 
 // --------------------------------------------------------------- attention --
-static int attention_grid_splits(int max_ctx) {
-  int nchunks, cps, splits;
-  attn_splits(max_ctx, &nchunks, &cps, &splits);
-  return splits;
+size_t attention_exact_floats(int seq, int heads, int past) {
+  const size_t total = (size_t)past + seq;
+  return (size_t)seq * heads * (total + attn_chunks((int)total));
 }
 
-void attn_splits_host(int ctx, int* nchunks, int* cps, int* splits) {
-  attn_splits(ctx, nchunks, cps, splits);
-}
-
-size_t attention_partials_floats(int seq, int heads, int kv_heads, int capacity) {
-  const int s_grid = attention_grid_splits(capacity);
-  return (size_t)seq * kv_heads * s_grid * (heads / kv_heads) * kPartialStride;
-}
-
-hipError_t launch_attention(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc,
-                            int capacity, float* out, int seq, int past, int heads, int kv_heads,
-                            float* partials, int* counters) {
-  AttnArgs a{};
+hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t* kc,
+                                  const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                  int heads, int kv_heads, float* scores, float* maxes) {
+  ExactArgs a{};
   a.q = q;
-  a.kc = const_cast<uint16_t*>(kc);
-  a.vc = const_cast<uint16_t*>(vc);
+  a.kc = kc;
+  a.vc = vc;
+  a.scores = scores;
+  a.maxes = maxes;
+  a.out = out;
+  a.past = past;
+  a.capacity = capacity;
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.score_stride = past + seq;
+  a.max_stride = attn_chunks(past + seq);
+  hipLaunchKernelGGL(k_attn_scores, dim3(a.max_stride, kv_heads, seq), dim3(kBlock), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_pv, dim3(heads, seq), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx) {
+  return (size_t)seq * kv_heads * attn_grid_splits(max_ctx) * (heads / kv_heads) * kPartialStride;
+}
+
+hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
+                                   const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                   int heads, int kv_heads, float* partials, int* counters) {
+  SplitArgs a{};
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
   a.partials = partials;
   a.counters = counters;
   a.out = out;
@@ -306,9 +348,8 @@ hipError_t launch_attention(hipStream_t s, const float* q, const uint16_t* kc, c
   a.capacity = capacity;
   a.heads = heads;
   a.kv_heads = kv_heads;
-  a.s_grid = attention_grid_splits(past + seq);
-  hipLaunchKernelGGL((k_attention<false, false>), dim3(a.s_grid, kv_heads, seq), dim3(kBlock), 0,
-                     s, a);
+  a.s_grid = attn_grid_splits(past + seq);
+  hipLaunchKernelGGL(k_attention_splitk, dim3(a.s_grid, kv_heads, seq), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
@@ -337,8 +378,7 @@ hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n) {
 }
 
 // ------------------------------------------------------------------ argmax --
-// Block partials then the last block's reduction (atomic counter). Scratch:
-// [counter, pad to 64 B][partials: nblocks x {float value, int index}].
+// Block partials, then the last block's reduction (atomic counter).
 constexpr int kArgmaxPerThread = 16;
 constexpr int kArgmaxPerBlock = kBlock * kArgmaxPerThread;
 
@@ -385,16 +425,16 @@ __global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ x, 
   }
 }
 
-size_t argmax_scratch_bytes(int n) {
+size_t argmax_partials_bytes(int n) {
   const int blocks = (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
-  return 64 + (size_t)blocks * sizeof(ArgPair);
+  return (size_t)blocks * sizeof(ArgPair);
 }
 
-hipError_t launch_argmax(hipStream_t s, const float* v, int n, void* scratch, int32_t* d_out) {
+hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, void* partials,
+                         int32_t* d_out) {
   const int blocks = (n + kArgmaxPerBlock - 1) / kArgmaxPerBlock;
-  int* counter = static_cast<int*>(scratch);
-  ArgPair* partials = reinterpret_cast<ArgPair*>(static_cast<char*>(scratch) + 64);
-  hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(kBlock), 0, s, v, n, counter, partials, d_out);
+  hipLaunchKernelGGL(k_argmax, dim3(blocks), dim3(kBlock), 0, s, v, n, counter,
+                     static_cast<ArgPair*>(partials), d_out);
   return hipGetLastError();
 }
 

@@ -55,9 +55,12 @@ struct qh_ctx {
   int cus = 0;
   size_t hbm_bytes = 0;
   size_t lds_per_block = 0;
-  // Small reusable scratch for operators that reduce across blocks (argmax).
+  // Reusable scratch for operators that reduce across blocks (argmax, attention):
+  // [0, kScratchCounterBytes) holds only counters, which every kernel leaves at
+  // zero; block partials go after it; the argmax result sits in the last 64 bytes.
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;
+  static constexpr size_t kScratchCounterBytes = 16384;
   int32_t* h_pinned = nullptr;  // 4-byte pinned readback slots
 };
 
@@ -67,8 +70,11 @@ struct qh_event {
 
 // Kernel launchers (defined in the .hip files). They assume validated arguments.
 namespace qh {
+// x f32 [seq, cols]. When NB*cols doubles do not fit in LDS the kernel reads an f64 copy
+// of x from `x64_scratch` (seq*cols doubles; NULL means the launcher allocates one).
 hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
-                         int seq);
+                         int seq, double* x64_scratch = nullptr);
+size_t matvec_x64_bytes(const DMat& m, int seq);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
@@ -78,17 +84,25 @@ hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float*
 hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint16_t* kc,
                             uint16_t* vc, int capacity, int kv_heads, int head_dim, int past,
                             int seq);
-// Attention over an f16 head-major cache. `partials` must hold attention_partials_floats(...)
-// floats and `counters` seq*kv_heads ints, zeroed before first use (kernels leave them zeroed).
-hipError_t launch_attention(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc,
-                            int capacity, float* out, int seq, int past, int heads, int kv_heads,
-                            float* partials, int* counters);
-size_t attention_partials_floats(int seq, int heads, int kv_heads, int capacity);
-// Split structure of one query at context ctx (see attention.h).
-void attn_splits_host(int ctx, int* nchunks, int* cps, int* splits);
+// Exact-order attention over an f16 head-major cache. `scores` holds
+// seq*heads*(past+seq) floats and `maxes` seq*heads*chunks(past+seq) floats.
+hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t* kc,
+                                  const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                  int heads, int kv_heads, float* scores, float* maxes);
+size_t attention_exact_floats(int seq, int heads, int past);
+// Split-K attention. `partials` holds attention_partials_floats(...) floats and `counters`
+// seq*kv_heads ints, zeroed before first use (the kernel leaves them zeroed).
+hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
+                                   const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                   int heads, int kv_heads, float* partials, int* counters);
+size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx);
+// f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).
+void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
 hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n);
-// Argmax into d_out[0]; `scratch` holds argmax_scratch_bytes(n) bytes, counter zeroed.
-hipError_t launch_argmax(hipStream_t s, const float* v, int n, void* scratch, int32_t* d_out);
-size_t argmax_scratch_bytes(int n);
+// Argmax into d_out[0]; `partials` holds argmax_partials_bytes(n) bytes; *counter is zero
+// before the launch and left zero after it.
+hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, void* partials,
+                         int32_t* d_out);
+size_t argmax_partials_bytes(int n);
 }  // namespace qh

@@ -26,6 +26,8 @@ LIB_PATH = os.path.join(HERE, "libqwen_hip.so")
 QH_OK, QH_ERR_INVALID, QH_ERR_RANGE, QH_ERR_BUSY, QH_ERR_DEVICE, QH_ERR_NOMEM, QH_ERR_STATE = range(7)
 FMT_F32, FMT_F16, FMT_INT8, FMT_INT4, FMT_BF16 = range(5)
 FORMAT_OF = {"f32": FMT_F32, "f16": FMT_F16, "int8": FMT_INT8, "int4": FMT_INT4, "bf16": FMT_BF16}
+# Kernel roles of a decode step, in QH_ROLE_* order.
+ROLES = ("embed", "qkv", "attention", "oproj", "gateup", "down", "head")
 
 
 class QwenHipError(RuntimeError):
@@ -134,6 +136,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_rope_tables": [i32, f64, i32, vp, vp],
         "qh_kv_append": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32],
         "qh_attention": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
+        "qh_attention_splitk": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
@@ -149,6 +152,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_forward": [vp, vp, vp, i32, vp, vp], "qh_forward_tokens": [vp, vp, vp, i32, vp, vp],
         "qh_decode": [vp, vp, i32, i32, vp], "qh_decode_launch": [vp, vp, i32, i32],
         "qh_decode_collect": [vp, vp, i32, vp],
+        "qh_decode_profile": [vp, vp, i32, i32, vp, vp, vp],
     }
     for name, args in sigs.items():
         f = getattr(lib, name)
@@ -409,9 +413,11 @@ class GpuContext:
         _check(self.lib.qh_kv_append(self.handle, k.ptr, v.ptr, kc.ptr, vc.ptr, capacity, kv_heads,
                                      head_dim, past, seq))
 
-    def attention(self, q, kc, vc, capacity, out, seq, past, heads, kv_heads, head_dim=64) -> None:
-        _check(self.lib.qh_attention(self.handle, q.ptr, kc.ptr, vc.ptr, capacity, out.ptr, seq,
-                                     past, heads, kv_heads, head_dim))
+    def attention(self, q, kc, vc, capacity, out, seq, past, heads, kv_heads, head_dim=64,
+                  splitk=False) -> None:
+        fn = self.lib.qh_attention_splitk if splitk else self.lib.qh_attention
+        _check(fn(self.handle, q.ptr, kc.ptr, vc.ptr, capacity, out.ptr, seq, past, heads, kv_heads,
+                  head_dim))
 
     def swiglu(self, gate, up, n) -> None:
         _check(self.lib.qh_swiglu(self.handle, gate.ptr, up.ptr, n))
@@ -542,6 +548,16 @@ class GpuModel:
         out = np.empty(steps, np.int32)
         _check(self.lib.qh_decode_collect(self.handle, cache.handle, steps, _ptr(out)))
         return out
+
+    def decode_profile(self, cache: GpuKVCache, first_token: int, steps: int):
+        """Greedy decode with a device event around every launch; returns
+        (tokens, {role: (total ms, launches)}) over the steps."""
+        out = np.empty(steps, np.int32)
+        ms = np.zeros(len(ROLES), np.float32)
+        n = np.zeros(len(ROLES), np.int32)
+        _check(self.lib.qh_decode_profile(self.handle, cache.handle, first_token, steps, _ptr(out),
+                                          _ptr(ms), _ptr(n)))
+        return out, {r: (float(ms[i]), int(n[i])) for i, r in enumerate(ROLES)}
 
     def destroy(self) -> None:
         if self.handle:
