@@ -129,13 +129,19 @@ int qh_rope(qh_ctx* ctx, float* d_v, const float* d_cos, const float* d_sin,
 int qh_rope_tables(int32_t head_dim, double theta, int32_t positions, float* h_cos,
                    float* h_sin);
 
-/* The KV append (model.js:336-338): k, v f32 [seq, kv_heads*head_dim] written as f16 into a
- * head-major cache [kv_heads, capacity, head_dim] at positions past .. past+seq-1. */
+/* The KV append (model.js:336-338): k, v f32 [seq, kv_heads*head_dim] written as f16 at
+ * positions past .. past+seq-1. The key cache is position-major per head
+ * [kv_heads, capacity, head_dim]; the value cache is dimension-major per head
+ * [kv_heads, head_dim, vstride] with vstride = capacity rounded up to a multiple of 8
+ * (qh_value_cache_bytes gives its size), the layout the attention kernels stream. */
 int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_key_cache,
                  uint16_t* d_value_cache, int32_t capacity, int32_t kv_heads, int32_t head_dim,
                  int32_t past, int32_t seq);
+/* Bytes of a value cache for `capacity` positions (no counterpart in the reference, whose
+ * cache layout is internal to src/gpu/model.js). */
+size_t qh_value_cache_bytes(int32_t capacity, int32_t kv_heads, int32_t head_dim);
 
-/* ATTENTION (kernels.js:404-499): causal GQA over an f16 head-major cache. Query t (absolute
+/* ATTENTION (kernels.js:404-499): causal GQA over the f16 caches of qh_kv_append. Query t (absolute
  * position past+t) attends to positions 0..past+t. Query head h reads kv head
  * h / (heads/kv_heads). Scale 1/sqrt(head_dim). q (rotated), out f32 [seq, heads*head_dim].
  * Evaluated in the order of groupedAttention (src/core/attention.js:32-66): f64 dots stored

@@ -1,19 +1,26 @@
-// Causal GQA attention over an f16 head-major KV cache [kv_heads][capacity][64]
-// (device code, shared by the operators and the decode step). Replaces
-// ATTENTION (src/gpu/kernels.js:404-499). Query head h reads kv head
-// h / (heads/kv_heads), the blocked map of src/core/attention.js:74-76.
+// Causal GQA attention over an f16 KV cache (device code, shared by the
+// operators and the decode step). Replaces ATTENTION (src/gpu/kernels.js:
+// 404-499). Query head h reads kv head h / (heads/kv_heads), the blocked map of
+// src/core/attention.js:74-76.
+//
+// Cache layout, per kv head: keys position-major [capacity][64] (a position's
+// key is one 128-byte row, read whole by the lane that scores it) and values
+// dimension-major [64][vstride] with vstride = capacity rounded up to 8 (one
+// dimension's values over positions are contiguous, so the lane that owns
+// output dimension d reads 8 positions in one 16-byte load).
 //
 // Two algorithms:
 //
-// Exact order (k_attn_scores + k_attn_pv), what the model path uses. It
-// evaluates groupedAttention (src/core/attention.js:32-66) step for step:
-// each score is a sequential f64 dot stored to f32, the softmax shifts by the
-// global max and normalizes with an f64 sum (src/core/ops.js:66-78), and the
-// output accumulates sequentially over positions in f32, as the reference's
-// Float32Array `out += weight * value` does. Scores and maxima are computed in
-// parallel over 64-position chunks; the sequential PV sum runs one lane per
-// output element. The result matches the CPU to the bit apart from f64-order
-// noise, so a device f16 cache and the CPU's same-f16 cache stay identical.
+// Exact order (k_attn_exact), what the model path uses. It evaluates
+// groupedAttention (src/core/attention.js:32-66) step for step: each score is a
+// sequential f64 dot stored to f32, the softmax shifts by the global max and
+// normalizes with an f64 sum (src/core/ops.js:66-78), and the output
+// accumulates sequentially over positions in f32, as the reference's
+// Float32Array `out += weight * value` does. Blocks score 256 positions each;
+// the last block of a (query, head) to finish does the softmax and the
+// sequential PV sum, one lane per output dimension. The result matches the CPU
+// to the bit apart from f64-order noise, so a device f16 cache and the CPU's
+// same-f16 cache stay identical.
 //
 // Split-K online softmax (k_attention_splitk), for long contexts: one block
 // per (query, kv head, split of chunks) stages K/V once for all the query heads
@@ -26,11 +33,13 @@
 
 namespace qh {
 
-constexpr int kChunk = 64;        // positions per chunk
+constexpr int kChunk = 64;        // split-K: positions per chunk
 constexpr int kMaxSplits = 128;   // split-K: splits per (query, kv head)
 constexpr int kHeadDim = 64;
 constexpr int kMaxGroup = 8;      // query heads per kv head
 constexpr int kPartialStride = kHeadDim + 2;  // split-K partial: m, l, acc[64]
+constexpr int kPLds = 8192;       // exact: probabilities kept in LDS up to this context
+static_assert(kSpan == kBlock, "exact attention scores one position per thread");
 
 __host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
 
@@ -39,122 +48,141 @@ __host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) 
 struct ExactArgs {
   const float* q;        // [seq][heads*64], rotated
   const uint16_t* kc;    // [kv_heads][capacity][64] f16
-  const uint16_t* vc;
+  const uint16_t* vt;    // [kv_heads][64][vstride] f16
   const int* d_pos;      // when set, past is read from the device (decode)
-  float* scores;         // [seq][heads][score_stride]; the PV pass overwrites them with p
-  float* maxes;          // [seq][heads][max_stride]: per-chunk maxima
+  float* scores;         // [seq][heads][score_stride], score_stride % 4 == 0
+  float* maxes;          // [seq][heads][max_stride]: per-span maxima
+  int* counters;         // [seq][heads]: zero between launches; the last block resets its own
   float* out;            // [seq][heads*64]
-  int past, capacity, heads, kv_heads, score_stride, max_stride;
+  int past, capacity, vstride, heads, kv_heads, score_stride, max_stride;
 };
 
-// grid (chunks, kv_heads, seq): scores of one 64-position chunk for the `group`
-// query heads of one kv head, and their per-chunk maxima.
-static __global__ __launch_bounds__(kBlock) void k_attn_scores(ExactArgs a) {
-  const int c = blockIdx.x, g = blockIdx.y, t = blockIdx.z;
+// out[d] = sum over s < ctx of p[s] * v[s][d], s ascending, rounding to f32 at
+// every step, by the 64 lanes of one wave (lane d). The product is exact in the
+// fused form, so each step is the CPU's f64 sum stored to f32 except in
+// double-rounding ties (probability ~2^-29 per step). Values come 8 positions
+// per 16-byte load, 64 positions in flight ahead of the arithmetic.
+__device__ __forceinline__ float pv_chain(const float* __restrict__ p, const uint16_t* __restrict__ vrow,
+                                          int ctx) {
+  constexpr int G = 8;  // 16-byte groups per batch
+  const int full = ctx & ~7;
+  const v4u* vg = reinterpret_cast<const v4u*>(vrow);
+  const v4f* pg = reinterpret_cast<const v4f*>(p);
+  float o = 0.f;
+  v4u cur[G], nxt[G];
+#pragma unroll
+  for (int k = 0; k < G; k++)
+    if (8 * k < full) cur[k] = vg[k];
+  for (int s = 0; s < full; s += 8 * G) {
+#pragma unroll
+    for (int k = 0; k < G; k++)
+      if (s + 8 * G + 8 * k < full) nxt[k] = vg[(s + 8 * G) / 8 + k];
+#pragma unroll
+    for (int k = 0; k < G; k++) {
+      if (s + 8 * k < full) {
+        const v4f pa = pg[(s + 8 * k) / 4], pb = pg[(s + 8 * k) / 4 + 1];
+        o = fmaf(pa.x, f16_lo(cur[k].x), o);
+        o = fmaf(pa.y, f16_hi(cur[k].x), o);
+        o = fmaf(pa.z, f16_lo(cur[k].y), o);
+        o = fmaf(pa.w, f16_hi(cur[k].y), o);
+        o = fmaf(pb.x, f16_lo(cur[k].z), o);
+        o = fmaf(pb.y, f16_hi(cur[k].z), o);
+        o = fmaf(pb.z, f16_lo(cur[k].w), o);
+        o = fmaf(pb.w, f16_hi(cur[k].w), o);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < G; k++) cur[k] = nxt[k];
+  }
+  for (int s = full; s < ctx; s++) o = fmaf(p[s], (float)__builtin_bit_cast(_Float16, vrow[s]), o);
+  return o;
+}
+
+// grid (spans, heads, seq). Block (span, h, t) scores positions span*256 ..
+// +255 of query t against head h and records the span's maximum; the last span
+// block of (t, h) to finish computes the probabilities and the output.
+static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
+  const int sp = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
   const int past = a.d_pos ? *a.d_pos : a.past;
   const int pos = past + t;
   if (pos >= a.capacity) return;  // the host keeps positions inside the cache
   const int ctx = pos + 1;
-  const int p0 = c * kChunk;
-  if (p0 >= ctx) return;
-  const int n = min(kChunk, ctx - p0);
-  const int group = a.heads / a.kv_heads;
-  const int tid = threadIdx.x;
-
-  __shared__ double qs[kMaxGroup][kHeadDim];
-  __shared__ __attribute__((aligned(16))) _Float16 ks[kChunk][kHeadDim + 2];
-  __shared__ float sc[kMaxGroup][kChunk];
-  const float* qrow = a.q + (size_t)t * a.heads * kHeadDim + (size_t)g * group * kHeadDim;
-  for (int i = tid; i < group * kHeadDim; i += kBlock) qs[i / kHeadDim][i % kHeadDim] = (double)qrow[i];
-  const uint16_t* kbase = a.kc + ((size_t)g * a.capacity + p0) * kHeadDim;
-  for (int e = tid; e < n * 8; e += kBlock) {
-    const int p = e >> 3, part = e & 7;
-    const v4u kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)p * kHeadDim)[part];
-#pragma unroll
-    for (int k = 0; k < 4; k++) *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kv4[k];
-  }
-  __syncthreads();
-  for (int idx = tid; idx < group * kChunk; idx += kBlock) {
-    const int h = idx / kChunk, p = idx % kChunk;
-    float s = -INFINITY;
-    if (p < n) {
-      // dot += q[i] * k[i], i ascending, in f64 (each product is exact).
-      double dot = 0.0;
-#pragma unroll 8
-      for (int j = 0; j < kHeadDim; j += 2) {
-        const uint32_t kk = *reinterpret_cast<const uint32_t*>(&ks[p][j]);
-        dot = fma(qs[h][j], (double)f16_lo(kk), dot);
-        dot = fma(qs[h][j + 1], (double)f16_hi(kk), dot);
-      }
-      s = (float)(dot * 0.125);  // scale = 1/sqrt(64), exact
-      a.scores[((size_t)t * a.heads + g * group + h) * a.score_stride + p0 + p] = s;
-    }
-    sc[h][p] = s;
-  }
-  __syncthreads();
-  const int wave = tid / kWave, lane = tid & (kWave - 1);
-  for (int h = wave; h < group; h += kBlock / kWave) {
-    const float m = wave_max(sc[h][lane]);
-    if (lane == 0) a.maxes[((size_t)t * a.heads + g * group + h) * a.max_stride + c] = m;
-  }
-}
-
-// grid (heads, seq): softmax with the global max, then out[d] accumulated
-// sequentially over positions in f32 by lane d of wave 0.
-static __global__ __launch_bounds__(kBlock) void k_attn_pv(ExactArgs a) {
-  const int h = blockIdx.x, t = blockIdx.y;
-  const int past = a.d_pos ? *a.d_pos : a.past;
-  const int pos = past + t;
-  if (pos >= a.capacity) return;
-  const int ctx = pos + 1;
+  const int nspan = attn_spans(ctx);
+  if (sp >= nspan) return;
   const int g = h / (a.heads / a.kv_heads);
   const int tid = threadIdx.x;
+  const int p = sp * kSpan + tid;
+
+  __shared__ double qs[kHeadDim];
+  __shared__ float wmax[kBlock / kWave];
   __shared__ double red[kBlock / kWave];
-  __shared__ float mx[kBlock / kWave];
+  __shared__ int is_last;
+  __shared__ __attribute__((aligned(16))) float pl[kPLds];
+
+  v4u kr[8];
+  if (p < ctx) {
+    const v4u* kp = reinterpret_cast<const v4u*>(a.kc + ((size_t)g * a.capacity + p) * kHeadDim);
+#pragma unroll
+    for (int j = 0; j < 8; j++) kr[j] = kp[j];
+  }
+  if (tid < kHeadDim) qs[tid] = (double)a.q[((size_t)t * a.heads + h) * kHeadDim + tid];
+  __syncthreads();
 
   const size_t row = (size_t)t * a.heads + h;
   float* sc = a.scores + row * a.score_stride;
-  // The global max is the max of the chunk maxima (max is order-free).
-  const float* cm = a.maxes + row * a.max_stride;
-  float m = -INFINITY;
-  for (int c = tid; c < attn_chunks(ctx); c += kBlock) m = fmaxf(m, cm[c]);
-  m = wave_max(m);
-  if ((tid & (kWave - 1)) == 0) mx[tid / kWave] = m;
+  float s = -INFINITY;
+  if (p < ctx) {
+    // dot += q[i] * k[i], i ascending, in f64 (each product is exact).
+    double dot = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t u[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        dot = fma(qs[8 * j + 2 * e], (double)f16_lo(u[e]), dot);
+        dot = fma(qs[8 * j + 2 * e + 1], (double)f16_hi(u[e]), dot);
+      }
+    }
+    s = (float)(dot * 0.125);  // scale = 1/sqrt(64), exact
+    sc[p] = s;
+  }
+  const float wm = wave_max(s);
+  if ((tid & (kWave - 1)) == 0) wmax[tid / kWave] = wm;
   __syncthreads();
-  const double M = fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3]));
+  if (tid == 0) {
+    a.maxes[row * a.max_stride + sp] = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    __threadfence();
+    is_last = atomicAdd(a.counters + row, 1) == nspan - 1;
+  }
+  __syncthreads();
+  if (!is_last) return;
+  __threadfence();
+
+  // The global max is the max of the span maxima (max is order-free).
+  float m = -INFINITY;
+  for (int c = tid; c < nspan; c += kBlock) m = fmaxf(m, a.maxes[row * a.max_stride + c]);
+  m = wave_max(m);
+  __syncthreads();
+  if ((tid & (kWave - 1)) == 0) wmax[tid / kWave] = m;
+  __syncthreads();
+  const double M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   // e = exp(s - max) stored f32; the sum over the unrounded e in f64; p = f32(e32 * (1/sum)).
+  float* pb = ctx <= kPLds ? pl : sc;
   double sum = 0.0;
-  for (int s = tid; s < ctx; s += kBlock) {
-    const double e = exp((double)sc[s] - M);
-    sc[s] = (float)e;
+  for (int i = tid; i < ctx; i += kBlock) {
+    const double e = exp((double)sc[i] - M);
+    pb[i] = (float)e;
     sum += e;
   }
   sum = block_sum_f64(sum, red);
   const double inv = 1.0 / sum;
-  for (int s = tid; s < ctx; s += kBlock) sc[s] = (float)((double)sc[s] * inv);
+  for (int i = tid; i < ctx; i += kBlock) pb[i] = (float)((double)pb[i] * inv);
   __syncthreads();
-  if (tid >= kWave) return;
-
-  // out[d] += p[s] * v[s][d] for s ascending, rounding to f32 at every step. The
-  // product is exact in the fused form, so this is the CPU's f64-sum-then-f32
-  // except in double-rounding ties (probability ~2^-29 per step).
-  const uint16_t* vb = a.vc + (size_t)g * a.capacity * kHeadDim + tid;
-  float o = 0.f;
-  constexpr int U = 16;
-  int s = 0;
-  for (; s + U <= ctx; s += U) {
-    float pv[U];
-    _Float16 vv[U];
-#pragma unroll
-    for (int k = 0; k < U; k++) {
-      pv[k] = sc[s + k];
-      vv[k] = __builtin_bit_cast(_Float16, vb[(size_t)(s + k) * kHeadDim]);
-    }
-#pragma unroll
-    for (int k = 0; k < U; k++) o = fmaf(pv[k], (float)vv[k], o);
+  if (tid < kHeadDim) {
+    const uint16_t* vrow = a.vt + ((size_t)g * kHeadDim + tid) * a.vstride;
+    a.out[row * kHeadDim + tid] = pv_chain(pb, vrow, ctx);
   }
-  for (; s < ctx; s++) o = fmaf(sc[s], (float)__builtin_bit_cast(_Float16, vb[(size_t)s * kHeadDim]), o);
-  a.out[(size_t)t * a.heads * kHeadDim + (size_t)h * kHeadDim + tid] = o;
+  if (tid == 0) a.counters[row] = 0;
 }
 
 // -------------------------------------------------------------- split-K --
@@ -162,11 +190,11 @@ static __global__ __launch_bounds__(kBlock) void k_attn_pv(ExactArgs a) {
 struct SplitArgs {
   const float* q;        // [seq][heads*64], rotated
   const uint16_t* kc;    // [kv_heads][capacity][64] f16
-  const uint16_t* vc;
+  const uint16_t* vt;    // [kv_heads][64][vstride] f16
   float* partials;       // [seq][kv_heads][s_grid][group][66]
   int* counters;         // [seq][kv_heads], zero between launches
   float* out;            // [seq][heads*64]
-  int past, seq, capacity, heads, kv_heads, s_grid;
+  int past, seq, capacity, vstride, heads, kv_heads, s_grid;
 };
 
 __host__ __device__ inline void attn_splits(int ctx, int* nchunks, int* cps, int* splits) {
@@ -186,7 +214,7 @@ __host__ __device__ inline int attn_grid_splits(int max_ctx) {
   return n < kMaxSplits ? n : kMaxSplits;
 }
 
-static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a) {
+[[maybe_unused]] static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a) {
   const int split = blockIdx.x;
   const int g = blockIdx.y;
   const int t = blockIdx.z;
@@ -202,7 +230,7 @@ static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a)
 
   __shared__ float qs[kMaxGroup][kHeadDim];
   __shared__ __attribute__((aligned(16))) _Float16 ks[kChunk][kHeadDim + 2];
-  __shared__ __attribute__((aligned(16))) _Float16 vs[kChunk][kHeadDim];
+  __shared__ _Float16 vs[kChunk][kHeadDim + 2];
   __shared__ float sc[kMaxGroup][kChunk];
   __shared__ float mst[kMaxGroup], lst[kMaxGroup], alpha[kMaxGroup];
   __shared__ int is_last;
@@ -220,20 +248,26 @@ static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a)
   __syncthreads();
 
   const uint16_t* kbase = a.kc + (size_t)g * a.capacity * kHeadDim;
-  const uint16_t* vbase = a.vc + (size_t)g * a.capacity * kHeadDim;
+  const uint16_t* vbase = a.vt + (size_t)g * kHeadDim * a.vstride;
   for (int c = c0; c < c1; c++) {
     const int p0 = c * kChunk;
     const int n = min(kChunk, ctx - p0);
     for (int e = tid; e < kChunk * 8; e += kBlock) {
+      // keys: position p, 16-byte part; values: dimension d, 8 positions from p8
       const int p = e >> 3, part = e & 7;
       v4u kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
-      if (p < n) {
-        kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)(p0 + p) * kHeadDim)[part];
-        vv4 = reinterpret_cast<const v4u*>(vbase + (size_t)(p0 + p) * kHeadDim)[part];
-      }
+      if (p < n) kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)(p0 + p) * kHeadDim)[part];
+      const int d = e >> 3, p8 = (e & 7) * 8;
+      if (p8 < n) vv4 = *reinterpret_cast<const v4u*>(vbase + (size_t)d * a.vstride + p0 + p8);
 #pragma unroll
       for (int k = 0; k < 4; k++) *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kv4[k];
-      *reinterpret_cast<v4u*>(&vs[p][part * 8]) = vv4;
+      const uint32_t vu[4] = {vv4.x, vv4.y, vv4.z, vv4.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const uint16_t bits = (uint16_t)(vu[k >> 1] >> (16 * (k & 1)));
+        // positions past the context hold no value yet: stage zeros, as their weights are
+        vs[p8 + k][d] = p8 + k < n ? __builtin_bit_cast(_Float16, bits) : (_Float16)0.f;
+      }
     }
     __syncthreads();
     for (int idx = tid; idx < group * kChunk; idx += kBlock) {

@@ -280,6 +280,11 @@ int qh_rope(qh_ctx* ctx, float* d_v, const float* d_cos, const float* d_sin,
   return QH_OK;
 }
 
+size_t qh_value_cache_bytes(int32_t capacity, int32_t kv_heads, int32_t head_dim) {
+  if (capacity < 1 || kv_heads < 1 || head_dim < 1) return 0;
+  return (size_t)kv_heads * head_dim * qh::value_stride(capacity) * sizeof(uint16_t);
+}
+
 int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_key_cache,
                  uint16_t* d_value_cache, int32_t capacity, int32_t kv_heads, int32_t head_dim,
                  int32_t past, int32_t seq) {
@@ -316,21 +321,26 @@ int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
   int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
                            kv_heads, head_dim);
   if (rc) return rc;
-  // Scores and per-chunk maxima in the context scratch's partial region when they fit.
+  // Scores and span maxima in the context scratch's partial region, counters in its counter
+  // region (after the argmax counter), when they fit; else a temporary buffer.
   const size_t floats = qh::attention_exact_floats(seq, heads, past);
   const size_t room = ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64;
-  const size_t n_scores = (size_t)seq * heads * (past + seq);
-  float* buf = nullptr;
-  if (floats * sizeof(float) <= room) {
-    buf = reinterpret_cast<float*>(static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes);
+  const size_t n_counters = (size_t)seq * heads;
+  if ((n_counters + 16) * sizeof(int) <= qh_ctx::kScratchCounterBytes && floats * sizeof(float) <= room) {
+    float* buf = reinterpret_cast<float*>(static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes);
+    int* counters = static_cast<int*>(ctx->d_scratch) + 16;
     QH_HIP(qh::launch_attention_exact(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out,
-                                      seq, past, heads, kv_heads, buf, buf + n_scores));
+                                      seq, past, heads, kv_heads, buf, counters));
     return QH_OK;
   }
-  QH_HIP(hipMallocAsync((void**)&buf, floats * sizeof(float), ctx->stream));
-  hipError_t e = qh::launch_attention_exact(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
-                                            d_out, seq, past, heads, kv_heads, buf, buf + n_scores);
-  QH_HIP(hipFreeAsync(buf, ctx->stream));
+  const size_t counter_bytes = (n_counters * sizeof(int) + 255) & ~(size_t)255;
+  void* tmp = nullptr;
+  QH_HIP(hipMallocAsync(&tmp, counter_bytes + floats * sizeof(float), ctx->stream));
+  QH_HIP(hipMemsetAsync(tmp, 0, counter_bytes, ctx->stream));
+  hipError_t e = qh::launch_attention_exact(
+      ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads, kv_heads,
+      reinterpret_cast<float*>(static_cast<char*>(tmp) + counter_bytes), static_cast<int*>(tmp));
+  QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
   return QH_OK;
 }

@@ -1,20 +1,26 @@
 // The fused decode step: the whole of GpuModel.#forward for one position
-// (src/gpu/model.js:240-402) as 6 launches per layer plus the gather and the
+// (src/gpu/model.js:240-402) as 5 launches per layer plus the gather and the
 // output head, instead of the reference's ~15 dispatches and 2 copies per
 // layer. Every launch reads its position from device memory, so the same
 // launches are captured once in a hipGraph and replayed every token.
 //
 // Per layer (the order of src/cpu/model.js:89-143):
 //   1. rmsnorm(x) -> q|k|v matvec + bias -> rope (f64) -> q, f16 K/V append
-//   2. attention scores per 64-position chunk (f64 dots)
-//   3. softmax + sequential PV sum per head
-//   4. o-proj matvec, residual add into x
-//   5. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
-//   6. down matvec, residual add into x
+//   2. attention: scores per 256-position span (f64 dots); the last span block
+//      of each head does the softmax and the sequential PV sum
+//   3. o-proj matvec, residual add into x
+//   4. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
+//   5. down matvec, residual add into x
 // then rmsnorm -> lm_head -> logits and argmax; the last block to finish
 // writes the token (the reference reads back 151,936 logits and scans them on
 // the host, src/gpu/model.js:372-382, web/bench.html:129-131) and advances
 // the position.
+//
+// A matvec launch is latency-bound at these sizes (a layer's int4 weights are
+// 7.5 MB), so each team issues the loads of its whole share of the weights
+// (WTile) before the block stages its activation vector, and a team with more
+// than one work item loads the next item's weights before the current item's
+// arithmetic.
 #include "attention.h"
 #include "device_common.h"
 #include "model_dev.h"
@@ -30,13 +36,14 @@ struct FusedArgs {
   const float* gain;    // rmsnorm gain
   double eps;
   float* out;           // EPI_QKV: q [hidden]; EPI_SWIGLU: h; EPI_LOGITS: logits; EPI_RESIDUAL: x
-  int items;            // work items; blocks loop over them
+  int items;            // work items; teams stride over them
   // EPI_QKV
   const float* bias;    // [hidden + 2*kv_dim]
   const double* rope_cos;  // [positions][32] f64
   const double* rope_sin;
-  uint16_t* kc;         // this layer's K cache [kv_heads][capacity][64]
-  uint16_t* vc;
+  uint16_t* kc;         // this layer's keys [kv_heads][capacity][64]
+  uint16_t* vt;         // this layer's values [kv_heads][64][vstride]
+  int vstride;
   int heads, kv_heads;
   // EPI_QKV, EPI_LOGITS: the decode state
   int* state;           // [0] position, [1] forced length
@@ -73,7 +80,72 @@ __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows
   }
 }
 
-template <int FMT, int TL, int R, int PRO, int EPI>
+// Lane 0 of the team that summed item `it` (acc = the R row sums) stores it.
+template <int R, int EPI>
+__device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, const int (&rows)[R],
+                                         const double (&acc)[R], float& bv, int& bi) {
+  if constexpr (EPI == EPI_QKV) {
+    // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts).
+    const float v0 = (float)(acc[0] + (double)a.bias[rows[0]]);
+    const float v1 = (float)(acc[1] + (double)a.bias[rows[1]]);
+    const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
+    const int rope_pairs = (a.heads + a.kv_heads) * 32;
+    if (pos >= a.capacity) return;  // the host keeps positions inside the cache
+    if (it < rope_pairs) {
+      const int head = it / 32, j = it % 32;
+      float lo, hi;
+      rope_pair(v0, v1, a.rope_cos[(size_t)pos * 32 + j], a.rope_sin[(size_t)pos * 32 + j], &lo, &hi);
+      if (head < a.heads) {
+        a.out[head * kHeadDim + j] = lo;
+        a.out[head * kHeadDim + j + 32] = hi;
+      } else {
+        uint16_t* k = a.kc + ((size_t)(head - a.heads) * a.capacity + pos) * kHeadDim;
+        k[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
+        k[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int e = rows[i] - hidden - kvd;  // kv head e/64, dimension e%64
+        a.vt[(size_t)e * a.vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
+      }
+    }
+  }
+  if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int r = it * R + i;
+      if (r < a.w.rows) a.out[r] = a.out[r] + (float)acc[i];
+    }
+  }
+  if constexpr (EPI == EPI_SWIGLU) {
+    // h[j] = silu(g) * u over the f32 gate and up outputs, in f64 (src/core/ops.js:81-91).
+#pragma unroll
+    for (int i = 0; i < R; i += 2) {
+      const int r = it * R + i;
+      if (r + 1 < a.w.rows) {
+        const double g = (float)acc[i];
+        const double u = (float)acc[i + 1];
+        a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * u);
+      }
+    }
+  }
+  if constexpr (EPI == EPI_LOGITS) {
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const int r = it * R + i;
+      if (r >= a.w.rows) break;
+      const float v = (float)acc[i];
+      a.out[r] = v;
+      if (argmax_better(v, r, bv, bi)) {
+        bv = v;
+        bi = r;
+      }
+    }
+  }
+}
+
+template <int FMT, int TL, int R, int KC, int PRO, int EPI>
 __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
@@ -81,81 +153,41 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   __shared__ ArgPair wred[kBlock / kWave];
   __shared__ int is_last;
   double* xs = smem;
-  if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm(a.in, a.gain, a.eps, a.w.cols, xs, red);
-  else stage_copy(a.in, a.w.cols, xs);
-
   using T = Teams<TL>;
   const int lane = T::lane();
+  const int stride = gridDim.x * T::kTeams;
+  int it = blockIdx.x * T::kTeams + T::team();
+
+  // This team's first item: weight loads in flight before the staging below.
+  int rows[R];
+  WTile<FMT, R, KC> cur;
+  if (it < a.items) {
+    item_rows<EPI, R>(a, it, rows);
+    wtile_load<FMT, R, KC, TL>(a.w, rows, lane, cur);
+  }
+  const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
+  if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm(a.in, a.gain, a.eps, a.w.cols, xs, red, lay);
+  else stage_copy(a.in, a.w.cols, xs, lay);
+
   int pos = 0;
   if constexpr (EPI == EPI_QKV) pos = a.state[0];
   float bv = NAN;
   int bi = 0x7fffffff;
-  for (int it = blockIdx.x * T::kTeams + T::team(); it < a.items; it += gridDim.x * T::kTeams) {
-    int rows[R];
-    item_rows<EPI, R>(a, it, rows);
-    double acc[1][R];
-    mv_team<FMT, R, 1, TL>(a.w, rows, xs, 0, lane, acc);
-    if (lane != 0) continue;
-    if constexpr (EPI == EPI_QKV) {
-      // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts).
-      const float v0 = (float)(acc[0][0] + (double)a.bias[rows[0]]);
-      const float v1 = (float)(acc[0][1] + (double)a.bias[rows[1]]);
-      const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
-      const int rope_pairs = (a.heads + a.kv_heads) * 32;
-      if (pos >= a.capacity) continue;  // the host keeps positions inside the cache
-      if (it < rope_pairs) {
-        const int head = it / 32, j = it % 32;
-        float lo, hi;
-        rope_pair(v0, v1, a.rope_cos[(size_t)pos * 32 + j], a.rope_sin[(size_t)pos * 32 + j], &lo, &hi);
-        if (head < a.heads) {
-          a.out[head * kHeadDim + j] = lo;
-          a.out[head * kHeadDim + j + 32] = hi;
-        } else {
-          uint16_t* k = a.kc + ((size_t)(head - a.heads) * a.capacity + pos) * kHeadDim;
-          k[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
-          k[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-          const int e = rows[i] - hidden - kvd;  // 0 .. kv_dim-1
-          uint16_t* v = a.vc + ((size_t)(e / kHeadDim) * a.capacity + pos) * kHeadDim + e % kHeadDim;
-          *v = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
-        }
-      }
+  while (it < a.items) {
+    const int nx = it + stride;
+    int nrows[R];
+    WTile<FMT, R, KC> nxt;
+    if (nx < a.items) {
+      item_rows<EPI, R>(a, nx, nrows);
+      wtile_load<FMT, R, KC, TL>(a.w, nrows, lane, nxt);
     }
-    if constexpr (EPI == EPI_RESIDUAL) {
+    double acc[R];
+    wtile_dot<FMT, R, KC, TL>(a.w, cur, xs, lane, acc);
+    if (lane == 0) epilogue<R, EPI>(a, it, pos, rows, acc, bv, bi);
+    it = nx;
 #pragma unroll
-      for (int i = 0; i < R; i++) {
-        const int r = it * R + i;
-        if (r < a.w.rows) a.out[r] = a.out[r] + (float)acc[0][i];
-      }
-    }
-    if constexpr (EPI == EPI_SWIGLU) {
-      // h[j] = silu(g) * u over the f32 gate and up outputs, in f64 (src/core/ops.js:81-91).
-#pragma unroll
-      for (int i = 0; i < R; i += 2) {
-        const int r = it * R + i;
-        if (r + 1 < a.w.rows) {
-          const double g = (float)acc[0][i];
-          const double u = (float)acc[0][i + 1];
-          a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * u);
-        }
-      }
-    }
-    if constexpr (EPI == EPI_LOGITS) {
-#pragma unroll
-      for (int i = 0; i < R; i++) {
-        const int r = it * R + i;
-        if (r >= a.w.rows) break;
-        const float v = (float)acc[0][i];
-        a.out[r] = v;
-        if (argmax_better(v, r, bv, bi)) {
-          bv = v;
-          bi = r;
-        }
-      }
-    }
+    for (int i = 0; i < R; i++) rows[i] = nrows[i];
+    cur = nxt;
   }
   if constexpr (EPI == EPI_LOGITS) {
     if (lane == 0) tbest[T::team()] = {bv, bi};
@@ -215,47 +247,70 @@ __global__ void k_advance(int* state) {
   if (threadIdx.x == 0) state[0] = state[0] + 1;
 }
 
-constexpr int kLmRows = 4;        // rows per team in the output head
-constexpr int kLmMaxBlocks = 1024;
+constexpr int kLmRows = 4;          // rows per team in the output head
+constexpr int kLmMaxBlocks = 2048;  // the head's teams take ceil(items / (teams * blocks)) items each
 
-template <int FMT, int TL, int R, int PRO, int EPI>
+// Chunks per lane a kernel is built for: the smallest instantiated count that
+// covers ceil(nchunks / TL).
+static int kc_for(int nchunks) {
+  const int tl = team_width(nchunks);
+  const int need = (nchunks + tl - 1) / tl;
+  for (int kc : {1, 2, 3, 5, 8, 16})
+    if (need <= kc) return kc;
+  return 0;
+}
+
+static int fused_blocks(int items, int teams, int max_blocks) {
+  int blocks = (items + teams - 1) / teams;
+  if (blocks > max_blocks) {
+    const int per_team = (items + teams * max_blocks - 1) / (teams * max_blocks);
+    blocks = (items + teams * per_team - 1) / (teams * per_team);
+  }
+  return blocks;
+}
+
+template <int FMT, int TL, int R, int KC, int PRO, int EPI>
 static hipError_t fused_t(hipStream_t s, FusedArgs a, int items, int max_blocks) {
   using T = Teams<TL>;
   a.items = items;
-  int blocks = (items + T::kTeams - 1) / T::kTeams;
-  if (blocks > max_blocks) blocks = max_blocks;
+  const int blocks = fused_blocks(items, T::kTeams, max_blocks);
   const size_t lds = (size_t)a.w.cols * sizeof(double);
-  hipLaunchKernelGGL((k_fused<FMT, TL, R, PRO, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
+  hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
   return hipGetLastError();
+}
+
+template <int FMT, int R, int PRO, int EPI>
+static hipError_t fused_f(hipStream_t s, const FusedArgs& a, int items, int max_blocks) {
+  if (team_width(a.w.nchunks) == 32) return fused_t<FMT, 32, R, 1, PRO, EPI>(s, a, items, max_blocks);
+  switch (kc_for(a.w.nchunks)) {
+    case 1: return fused_t<FMT, 64, R, 1, PRO, EPI>(s, a, items, max_blocks);
+    case 2: return fused_t<FMT, 64, R, 2, PRO, EPI>(s, a, items, max_blocks);
+    case 3: return fused_t<FMT, 64, R, 3, PRO, EPI>(s, a, items, max_blocks);
+    case 5: return fused_t<FMT, 64, R, 5, PRO, EPI>(s, a, items, max_blocks);
+    case 8: return fused_t<FMT, 64, R, 8, PRO, EPI>(s, a, items, max_blocks);
+    case 16: return fused_t<FMT, 64, R, 16, PRO, EPI>(s, a, items, max_blocks);
+    default: return hipErrorInvalidValue;  // rows longer than the model limits allow
+  }
 }
 
 template <int R, int PRO, int EPI>
 static hipError_t fused(hipStream_t s, const FusedArgs& a, int items, int max_blocks = 1 << 30) {
-  const bool wide = team_width(a.w.nchunks) == 64;
   switch (a.w.format) {
-    case QH_FMT_F16:
-      return wide ? fused_t<QH_FMT_F16, 64, R, PRO, EPI>(s, a, items, max_blocks)
-                  : fused_t<QH_FMT_F16, 32, R, PRO, EPI>(s, a, items, max_blocks);
-    case QH_FMT_INT8:
-      return wide ? fused_t<QH_FMT_INT8, 64, R, PRO, EPI>(s, a, items, max_blocks)
-                  : fused_t<QH_FMT_INT8, 32, R, PRO, EPI>(s, a, items, max_blocks);
-    default:
-      return wide ? fused_t<QH_FMT_INT4, 64, R, PRO, EPI>(s, a, items, max_blocks)
-                  : fused_t<QH_FMT_INT4, 32, R, PRO, EPI>(s, a, items, max_blocks);
+    case QH_FMT_F16: return fused_f<QH_FMT_F16, R, PRO, EPI>(s, a, items, max_blocks);
+    case QH_FMT_INT8: return fused_f<QH_FMT_INT8, R, PRO, EPI>(s, a, items, max_blocks);
+    default: return fused_f<QH_FMT_INT4, R, PRO, EPI>(s, a, items, max_blocks);
   }
 }
 
 int lm_head_blocks(const ModelDev& m) {
   const int teams = kBlock / team_width(m.lm_head.nchunks);
-  const int items = (m.vocab + kLmRows - 1) / kLmRows;
-  const int blocks = (items + teams - 1) / teams;
-  return blocks < kLmMaxBlocks ? blocks : kLmMaxBlocks;
+  return fused_blocks((m.vocab + kLmRows - 1) / kLmRows, teams, kLmMaxBlocks);
 }
 
 size_t lm_partials_bytes(const ModelDev& m) { return (size_t)lm_head_blocks(m) * sizeof(ArgPair); }
 
 int launches_per_step(const ModelDev& m, StepInput in) {
-  return (in == STEP_GATHER ? 1 : 0) + 6 * m.layers + 1;
+  return (in == STEP_GATHER ? 1 : 0) + 5 * m.layers + 1;
 }
 
 // Records the event that opens a launch of `role` (see StepTimer).
@@ -276,12 +331,10 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   const int kv_dim = m.kv_heads * m.head_dim;
-  const size_t kv_layer = (size_t)m.kv_heads * c.capacity * m.head_dim;
-  const int chunks = attn_chunks(c.capacity);
   for (int L = 0; L < m.layers; L++) {
     const LayerDev& l = m.layers_host[L];
-    uint16_t* kc = c.kv + (size_t)L * 2 * kv_layer;
-    uint16_t* vc = kc + kv_layer;
+    uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
+    uint16_t* vt = kc + c.key_elems;
 
     FusedArgs f{};
     f.eps = m.eps;
@@ -293,7 +346,8 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     f.rope_cos = m.rope_cos;
     f.rope_sin = m.rope_sin;
     f.kc = kc;
-    f.vc = vc;
+    f.vt = vt;
+    f.vstride = c.vstride;
     f.heads = m.heads;
     f.kv_heads = m.kv_heads;
     f.state = c.state;
@@ -305,21 +359,20 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     ExactArgs a{};
     a.q = c.q;
     a.kc = kc;
-    a.vc = vc;
+    a.vt = vt;
     a.d_pos = c.state;
     a.scores = c.scores;
     a.maxes = c.maxes;
+    a.counters = c.attn_counters;
     a.out = c.attn;
     a.capacity = c.capacity;
+    a.vstride = c.vstride;
     a.heads = m.heads;
     a.kv_heads = m.kv_heads;
-    a.score_stride = c.capacity;
-    a.max_stride = chunks;
+    a.score_stride = c.score_stride;
+    a.max_stride = attn_spans(c.capacity);
     if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_scores, dim3(chunks, m.kv_heads, 1), dim3(kBlock), 0, s, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_pv, dim3(m.heads, 1), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
     f = FusedArgs{};
@@ -343,7 +396,7 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     f.in = c.h;
     f.out = c.x;
     if ((e = mark(s, timer, QH_ROLE_DOWN)) != hipSuccess) return e;
-    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.down.rows + 1) / 2)) != hipSuccess) return e;
+    if ((e = fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows)) != hipSuccess) return e;
   }
   if (!logits) {
     if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;

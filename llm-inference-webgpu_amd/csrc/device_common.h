@@ -1,6 +1,7 @@
 // Device building blocks shared by every kernel: wave64 reductions on DPP and
 // ds_swizzle, the weight-chunk dot products for the three weight formats, the
-// row-team matvec core, and block-level staging helpers.
+// row-team matvec core (streamed and register-prefetched forms), and
+// block-level staging helpers.
 //
 // Arithmetic follows the reference CPU path step for step (src/core/ops.js:
 // f32 storage, f64 accumulation). A weight is first dequantized to the f32 the
@@ -26,6 +27,7 @@ namespace qh {
 
 // 16 bytes of one weight row, loaded with one global_load_dwordx4.
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;
@@ -113,15 +115,42 @@ __device__ __forceinline__ float f16_lo(uint32_t u) {
 __device__ __forceinline__ float f16_hi(uint32_t u) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(u >> 16));
 }
+// Byte b of u as f32 (one v_cvt_f32_ubyte).
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t u) {
+  return (float)((u >> (8 * B)) & 0xffu);
+}
 
 // acc += sum over one chunk of w[i] * x[i] in f64, sequentially in i, where w[i]
 // is the f32 weight the reference loader holds:
 //   f16:  the f16 value (exact in f32);
-//   int8: f32(q * scale)          (src/core/quantize.js:60-68);
-//   int4: f32((level - zero) * scale), low nibble = even index (:134-151).
-// Each f32 product here is a single correctly rounded multiply of exact
-// operands, which is what the reference's f64 product stored to f32 is.
-__device__ __forceinline__ double chunk_f16(const v4u w, const double* __restrict__ x, double acc) {
+//   int8: f32(q * scale)                       (src/core/quantize.js:60-68);
+//   int4: f32(f64(level - zero) * scale), low nibble = even index (:134-151).
+//
+// Quantized chunks take a biased-byte form when the group allows it: the codes
+// are offset so every byte is a non-negative integer m, converted with one
+// v_cvt_f32_ubyte, and w = fma(m, scale, -bias*scale). The bias is a power of
+// two, so -bias*scale is exact and the fused multiply-add rounds the exact value
+// (m - bias) * scale = (level - zero) * scale once -- the reference's weight.
+// The form needs scale > 0 and finite below 2^100 (no overflow in bias*scale,
+// and the sign of a zero weight is +0 as the reference's is), and for int4 an
+// integer zero point in [0, 15] (what the quantizer writes, quantize.js:115),
+// so (level - zero + 16) is a byte in [1, 31] and four of them take one add.
+// Other groups use the reference's arithmetic directly.
+//
+// x is the chunk's slice of the f64 activation vector, element e at
+// b[(e/2)*ps + e%2]: pairs of consecutive elements are adjacent, and pair
+// strides are either 2 (plain layout) or 2*nchunks (the chunk-transposed LDS
+// layout of stage_*, where the 64 lanes of a team, each on its own chunk, read
+// 64 consecutive 16-byte pairs -- no LDS bank conflicts, where the plain layout
+// would put a whole wave on one bank).
+struct XV {
+  const double* b;
+  int ps;
+  __device__ __forceinline__ double operator[](int e) const { return b[(e >> 1) * ps + (e & 1)]; }
+};
+
+__device__ __forceinline__ double chunk_f16(const v4u w, const XV x, double acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -130,40 +159,94 @@ __device__ __forceinline__ double chunk_f16(const v4u w, const double* __restric
   }
   return acc;
 }
-__device__ __forceinline__ double chunk_int8(const v4u w, const double* __restrict__ x, float s,
+
+__device__ __forceinline__ bool scale_biasable(float s) { return s > 0.f && s <= 0x1p100f; }
+
+__device__ __forceinline__ double chunk_int8(const v4u w, const XV x, float s,
                                              double acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+  if (scale_biasable(s)) {
+    const float c = -128.f * s;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 4; j++) {
+      const uint32_t m = u[j] ^ 0x80808080u;  // q + 128 in every byte
+      acc = fma((double)fmaf(ubyte<0>(m), s, c), x[4 * j + 0], acc);
+      acc = fma((double)fmaf(ubyte<1>(m), s, c), x[4 * j + 1], acc);
+      acc = fma((double)fmaf(ubyte<2>(m), s, c), x[4 * j + 2], acc);
+      acc = fma((double)fmaf(ubyte<3>(m), s, c), x[4 * j + 3], acc);
+    }
+  } else {
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const float wf = (float)(int8_t)(uint8_t)(u[j] >> (8 * b)) * s;
-      acc = fma((double)wf, x[4 * j + b], acc);
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const float wf = (float)(int8_t)(uint8_t)(u[j] >> (8 * b)) * s;  // q*s is exact before rounding
+        acc = fma((double)wf, x[4 * j + b], acc);
+      }
     }
   }
   return acc;
 }
-__device__ __forceinline__ double chunk_int4(const v4u w, const double* __restrict__ x, float s,
+
+__device__ __forceinline__ double chunk_int4(const v4u w, const XV x, float s,
                                              float z, double acc) {
   const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+  const int zi = (int)z;
+  if (scale_biasable(s) && (float)zi == z && (unsigned)zi <= 15u) {
+    const float c = -16.f * s;
+    const uint32_t bias = (uint32_t)(16 - zi) * 0x01010101u;
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
+    for (int j = 0; j < 4; j++) {
+      const uint32_t ev = (u[j] & 0x0F0F0F0Fu) + bias;         // elements 8j, 8j+2, 8j+4, 8j+6
+      const uint32_t od = ((u[j] >> 4) & 0x0F0F0F0Fu) + bias;  // elements 8j+1, +3, +5, +7
+      acc = fma((double)fmaf(ubyte<0>(ev), s, c), x[8 * j + 0], acc);
+      acc = fma((double)fmaf(ubyte<0>(od), s, c), x[8 * j + 1], acc);
+      acc = fma((double)fmaf(ubyte<1>(ev), s, c), x[8 * j + 2], acc);
+      acc = fma((double)fmaf(ubyte<1>(od), s, c), x[8 * j + 3], acc);
+      acc = fma((double)fmaf(ubyte<2>(ev), s, c), x[8 * j + 4], acc);
+      acc = fma((double)fmaf(ubyte<2>(od), s, c), x[8 * j + 5], acc);
+      acc = fma((double)fmaf(ubyte<3>(ev), s, c), x[8 * j + 6], acc);
+      acc = fma((double)fmaf(ubyte<3>(od), s, c), x[8 * j + 7], acc);
+    }
+  } else {
+    const double zd = z, sd = s;
 #pragma unroll
-    for (int n = 0; n < 8; n++) {
-      const float wf = ((float)((u[j] >> (4 * n)) & 0xfu) - z) * s;
-      acc = fma((double)wf, x[8 * j + n], acc);
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int n = 0; n < 8; n++) {
+        const float wf = (float)(((double)((u[j] >> (4 * n)) & 0xfu) - zd) * sd);
+        acc = fma((double)wf, x[8 * j + n], acc);
+      }
     }
   }
   return acc;
 }
 
 // ------------------------------------------------------------ matvec core --
+// Where element i of an f64 activation vector sits in a staged copy:
+// chunk-transposed (XT) for a matrix with W = 1 << lw weights per chunk and nc
+// chunks per row -- pair (i%W)/2 of every chunk together, chunk-minor -- else
+// plain. XV over either layout reads the same elements in the same order.
+struct XLayout {
+  int lw, nc;  // plain: lw = 13 (W >= any staged length), nc = 1
+  __device__ __forceinline__ int pos(int i) const {
+    const int e = i & ((1 << lw) - 1);
+    return (((e >> 1) * nc + (i >> lw)) << 1) | (i & 1);
+  }
+};
+constexpr XLayout kPlain = {13, 1};
+template <int FMT>
+__host__ __device__ inline XLayout chunk_layout(int nchunks) {
+  constexpr int lw = FMT == QH_FMT_F16 ? 3 : FMT == QH_FMT_INT8 ? 4 : 5;
+  return XLayout{lw, nchunks};
+}
+
 // A team of TL lanes computes R rows (row indices in `rows`, each < m.rows) for
 // NB positions. Lane `tl` handles chunks tl, tl+TL, ... of every row, so the x
 // chunk it reads is reused across the R rows. x for position b is f64 at
-// xs + b*xstride (LDS or global). On return every lane of the team holds the
-// R*NB f64 sums.
-template <int FMT, int R, int NB, int TL>
+// xs + b*xstride (LDS or global), chunk-transposed when XT. On return every
+// lane of the team holds the R*NB f64 sums.
+template <int FMT, int R, int NB, int TL, bool XT>
 __device__ __forceinline__ void mv_team(const DMat& m, const int (&rows)[R], const double* xs,
                                         int xstride, int tl, double (&acc)[NB][R]) {
   constexpr int W = Fmt<FMT>::kW;
@@ -195,7 +278,8 @@ __device__ __forceinline__ void mv_team(const DMat& m, const int (&rows)[R], con
     }
 #pragma unroll
     for (int b = 0; b < NB; b++) {
-      const double* xc = xs + (size_t)b * xstride + (size_t)c * W;
+      const XV xc = XT ? XV{xs + (size_t)b * xstride + 2 * c, 2 * m.nchunks}
+                       : XV{xs + (size_t)b * xstride + (size_t)c * W, 2};
 #pragma unroll
       for (int i = 0; i < R; i++) {
         if constexpr (FMT == QH_FMT_F16) acc[b][i] = chunk_f16(w[i], xc, acc[b][i]);
@@ -208,6 +292,67 @@ __device__ __forceinline__ void mv_team(const DMat& m, const int (&rows)[R], con
   for (int b = 0; b < NB; b++)
 #pragma unroll
     for (int i = 0; i < R; i++) acc[b][i] = team_sum<TL>(acc[b][i]);
+}
+
+// The same sums with a lane's whole share of R rows -- at most KC chunks per
+// row -- loaded into registers first (WTile), so the loads of a work item are in
+// flight together, ahead of the activation staging and of the previous item's
+// arithmetic. Chunks are summed in the order mv_team sums them.
+template <int FMT, int R, int KC>
+struct WTile {
+  v4u w[KC][R];
+  float s[KC][R];  // int4: group scale of each chunk; int8: row scale in s[0]
+  float z[KC][R];  // int4: group zero point
+};
+
+template <int FMT, int R, int KC, int TL>
+__device__ __forceinline__ void wtile_load(const DMat& m, const int (&rows)[R], int tl,
+                                           WTile<FMT, R, KC>& t) {
+#pragma unroll
+  for (int k = 0; k < KC; k++) {
+    const int c = tl + k * TL;
+    const bool in = c < m.nchunks;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      const v4u* rp = reinterpret_cast<const v4u*>(m.data + (size_t)rows[i] * m.row_bytes);
+      t.w[k][i] = in ? __builtin_nontemporal_load(&rp[c]) : v4u{0, 0, 0, 0};
+    }
+    if constexpr (FMT == QH_FMT_INT4) {
+      const int g = (in ? c : 0) / m.cpg;
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        t.s[k][i] = m.scales[(size_t)rows[i] * m.gpr + g];
+        t.z[k][i] = m.zeros[(size_t)rows[i] * m.gpr + g];
+      }
+    }
+  }
+  if constexpr (FMT == QH_FMT_INT8) {
+#pragma unroll
+    for (int i = 0; i < R; i++) t.s[0][i] = m.scales[rows[i]];
+  }
+}
+
+// xs is chunk-transposed (chunk_layout<FMT>(m.nchunks)).
+template <int FMT, int R, int KC, int TL>
+__device__ __forceinline__ void wtile_dot(const DMat& m, const WTile<FMT, R, KC>& t, const double* xs,
+                                          int tl, double (&acc)[R]) {
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = 0.0;
+#pragma unroll
+  for (int k = 0; k < KC; k++) {
+    const int c = tl + k * TL;
+    if (c < m.nchunks) {
+      const XV xc{xs + 2 * c, 2 * m.nchunks};
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        if constexpr (FMT == QH_FMT_F16) acc[i] = chunk_f16(t.w[k][i], xc, acc[i]);
+        else if constexpr (FMT == QH_FMT_INT8) acc[i] = chunk_int8(t.w[k][i], xc, t.s[0][i], acc[i]);
+        else acc[i] = chunk_int4(t.w[k][i], xc, t.s[k][i], t.z[k][i], acc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = team_sum<TL>(acc[i]);
 }
 
 // Team width of a matrix: 32 lanes when a row has at most 32 chunks, else 64.
@@ -224,29 +369,83 @@ struct Teams {
 };
 
 // --------------------------------------------------------- block staging --
+// Vectors of up to kStageMax f32 values are staged with every load of a thread
+// issued before any is used: thread t owns the float4 groups t, t+kBlock, ...
+constexpr int kStageVec = 8;                           // float4 groups per thread
+constexpr int kStageMax = kStageVec * 4 * kBlock;      // 8192 values
+
 // xs = x / sqrt(mean(x^2) + eps) * gain as f64 values of the f32 result, with
 // the statistic and the products in f64 as src/core/ops.js:17-24 evaluates
 // them, so the normalized vector is the CPU's up to the order of the f64 sum.
+// cols is a multiple of 4 and at most kStageMax; x and gain are 16-byte aligned.
+// Element i goes to xs[lay.pos(i)].
 __device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
                                               const float* __restrict__ gain, double eps, int cols,
-                                              double* xs, double* red) {
+                                              double* xs, double* red, XLayout lay) {
+  const int n4 = cols >> 2;
+  v4f v[kStageVec], g[kStageVec];
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    const int i = threadIdx.x + j * kBlock;
+    if (i < n4) {
+      v[j] = reinterpret_cast<const v4f*>(x)[i];
+      g[j] = reinterpret_cast<const v4f*>(gain)[i];
+    }
+  }
   double ss = 0;
-  for (int i = threadIdx.x; i < cols; i += kBlock) {
-    const double v = x[i];
-    xs[i] = v;
-    ss = fma(v, v, ss);  // v*v is exact in f64, so the fused form rounds once like the CPU's
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    if (threadIdx.x + j * kBlock < n4) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) ss = fma((double)v[j][e], (double)v[j][e], ss);  // v*v exact in f64
+    }
   }
   ss = block_sum_f64(ss, red);
   const double scale = 1.0 / sqrt(ss / cols + eps);
-  for (int i = threadIdx.x; i < cols; i += kBlock) {
-    xs[i] = (double)(float)(xs[i] * scale * (double)gain[i]);
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    const int i = threadIdx.x + j * kBlock;
+    if (i < n4) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) xs[lay.pos(4 * i + e)] = (double)(float)((double)v[j][e] * scale * (double)g[j][e]);
+    }
   }
   __syncthreads();
 }
 
-// xs = (double)x for an f32 vector.
-__device__ __forceinline__ void stage_copy(const float* __restrict__ x, int n, double* xs) {
-  for (int i = threadIdx.x; i < n; i += kBlock) xs[i] = (double)x[i];
+// stage_rmsnorm for any cols and alignment, one element per thread and step.
+__device__ __forceinline__ void stage_rmsnorm_scalar(const float* __restrict__ x,
+                                                     const float* __restrict__ gain, double eps,
+                                                     int cols, double* xs, double* red) {
+  double ss = 0;
+  for (int i = threadIdx.x; i < cols; i += kBlock) {
+    const double v = x[i];
+    xs[i] = v;
+    ss = fma(v, v, ss);
+  }
+  ss = block_sum_f64(ss, red);
+  const double scale = 1.0 / sqrt(ss / cols + eps);
+  for (int i = threadIdx.x; i < cols; i += kBlock) xs[i] = (double)(float)(xs[i] * scale * (double)gain[i]);
+  __syncthreads();
+}
+
+// xs = (double)x for an f32 vector (same bounds and layout as stage_rmsnorm).
+__device__ __forceinline__ void stage_copy(const float* __restrict__ x, int n, double* xs, XLayout lay) {
+  const int n4 = n >> 2;
+  v4f v[kStageVec];
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    const int i = threadIdx.x + j * kBlock;
+    if (i < n4) v[j] = reinterpret_cast<const v4f*>(x)[i];
+  }
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    const int i = threadIdx.x + j * kBlock;
+    if (i < n4) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) xs[lay.pos(4 * i + e)] = (double)v[j][e];
+    }
+  }
   __syncthreads();
 }
 

@@ -142,9 +142,11 @@ int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out) {
   QH_CHECK(c.heads % c.kv_heads == 0 && c.heads / c.kv_heads <= 8, QH_ERR_INVALID,
            "num_attention_heads %d is not divisible by num_key_value_heads %d (or groups > 8)",
            c.heads, c.kv_heads);
-  QH_CHECK(c.hidden % 32 == 0 && c.intermediate % 32 == 0 && c.hidden <= 16384 &&
-               c.intermediate <= 16384,
-           QH_ERR_INVALID, "hidden and intermediate must be multiples of 32 up to 16384");
+  // The decode kernels stage a whole activation vector in LDS as f64 (8192 values) and keep a
+  // lane's share of a row in registers (at most 16 chunks of a 64-lane team).
+  QH_CHECK(c.hidden % 32 == 0 && c.intermediate % 32 == 0 && c.hidden <= 8192 &&
+               c.intermediate <= 8192,
+           QH_ERR_INVALID, "hidden and intermediate must be multiples of 32 up to 8192");
   qh_model* m = new qh_model();
   m->ctx = ctx;
   m->cfg = c;
@@ -445,8 +447,12 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   c->m = m;
   qh::CacheDev& d = c->dev;
   d.capacity = capacity;
-  const int chunks = (capacity + 63) / 64;
-  const size_t kv_bytes = (size_t)md.layers * 2 * md.kv_heads * capacity * md.head_dim * 2;
+  d.vstride = qh::value_stride(capacity);
+  d.key_elems = (size_t)md.kv_heads * capacity * md.head_dim;
+  d.layer_elems = d.key_elems + (size_t)md.kv_heads * md.head_dim * d.vstride;
+  d.score_stride = (capacity + 3) & ~3;
+  const int spans = qh::attn_spans(capacity);
+  const size_t kv_bytes = (size_t)md.layers * d.layer_elems * 2;
   int rc = QH_OK;
   auto A = [&](size_t n, void** p) {
     if (!rc) rc = c->alloc(n, p);
@@ -460,8 +466,9 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   A((size_t)md.hidden * 4, (void**)&d.attn);
   A((size_t)md.intermediate * 4, (void**)&d.h);
   A((size_t)md.vocab * 4, (void**)&d.logits);
-  A((size_t)md.heads * capacity * 4, (void**)&d.scores);
-  A((size_t)md.heads * chunks * 4, (void**)&d.maxes);
+  A((size_t)md.heads * d.score_stride * 4, (void**)&d.scores);
+  A((size_t)md.heads * spans * 4, (void**)&d.maxes);
+  A(256, (void**)&d.attn_counters);
   A(qh::lm_partials_bytes(md), &d.lm_partials);
   A(256, (void**)&d.lm_counter);
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
@@ -470,7 +477,8 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   if (!rc && (hipMemset(d.kv, 0, kv_bytes) != hipSuccess || hipMemset(d.state, 0, 256) != hipSuccess ||
               hipMemset(d.tokens, 0, (size_t)(capacity + 1) * 4) != hipSuccess ||
               hipMemset(d.pred, 0, (size_t)capacity * 4) != hipSuccess ||
-              hipMemset(d.lm_counter, 0, 256) != hipSuccess)) {
+              hipMemset(d.lm_counter, 0, 256) != hipSuccess ||
+              hipMemset(d.attn_counters, 0, 256) != hipSuccess)) {
     rc = fail(QH_ERR_DEVICE, "clearing the cache failed");
   }
   d.lm_blocks = qh::lm_head_blocks(md);
@@ -520,18 +528,18 @@ int qh_cache_present(qh_cache* c, int32_t layer, float* h_key, float* h_value) {
   const qh::ModelDev& md = c->m->dev;
   QH_CHECK(layer >= 0 && layer < md.layers, QH_ERR_RANGE, "layer %d out of range", layer);
   QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight");
-  const size_t kv_layer = (size_t)md.kv_heads * c->dev.capacity * md.head_dim;
-  std::vector<uint16_t> buf(2 * kv_layer);
+  const qh::CacheDev& d = c->dev;
+  std::vector<uint16_t> buf(d.layer_elems);
   QH_HIP(hipStreamSynchronize(c->m->ctx->stream));
-  QH_HIP(hipMemcpy(buf.data(), c->dev.kv + (size_t)layer * 2 * kv_layer, buf.size() * 2, hipMemcpyDeviceToHost));
+  QH_HIP(hipMemcpy(buf.data(), d.kv + (size_t)layer * d.layer_elems, buf.size() * 2, hipMemcpyDeviceToHost));
   const int n = c->length, hd = md.head_dim;
+  const uint16_t* vt = buf.data() + d.key_elems;
   for (int h = 0; h < md.kv_heads; h++) {
     for (int t = 0; t < n; t++) {
       for (int i = 0; i < hd; i++) {
-        const size_t from = ((size_t)h * c->dev.capacity + t) * hd + i;
         const size_t to = ((size_t)h * n + t) * hd + i;
-        h_key[to] = f16_to_f32(buf[from]);
-        h_value[to] = f16_to_f32(buf[kv_layer + from]);
+        h_key[to] = f16_to_f32(buf[((size_t)h * d.capacity + t) * hd + i]);
+        h_value[to] = f16_to_f32(vt[((size_t)h * hd + i) * d.vstride + t]);
       }
     }
   }

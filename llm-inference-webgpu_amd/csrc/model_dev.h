@@ -32,7 +32,11 @@ struct ModelDev {
 
 struct CacheDev {
   int capacity;
-  uint16_t* kv;        // [layers][2][kv_heads][capacity][64] f16
+  int vstride;         // value row length: capacity rounded up to 8
+  // Per layer: keys [kv_heads][capacity][64], then values [kv_heads][64][vstride], f16.
+  uint16_t* kv;
+  size_t layer_elems;  // f16 elements per layer (keys + values)
+  size_t key_elems;    // f16 elements of a layer's keys
   int* state;          // [0] position, [1] forced length (tokens below it are the caller's)
   int* tokens;         // [capacity + 1] token consumed at each position
   int* pred;           // [capacity] argmax after each position
@@ -41,8 +45,10 @@ struct CacheDev {
   float* attn;         // [hidden]
   float* h;            // [intermediate]
   float* logits;       // [vocab]
-  float* scores;       // [heads][capacity]: scores, then softmax weights
-  float* maxes;        // [heads][chunks(capacity)]: per-chunk score maxima
+  float* scores;       // [heads][score_stride]: scores, then softmax weights
+  float* maxes;        // [heads][spans(capacity)]: per-span score maxima
+  int score_stride;    // capacity rounded up to 4
+  int* attn_counters;  // [heads], zero between launches
   void* lm_partials;   // argmax block partials
   int* lm_counter;
   int lm_blocks;

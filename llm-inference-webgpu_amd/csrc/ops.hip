@@ -22,8 +22,13 @@ __global__ __launch_bounds__(kBlock) void k_matvec(DMat m, const float* __restri
   const int b0 = b_base + blockIdx.y * NB;
   const double* xuse;
   if constexpr (X_LDS) {
+    // chunk-transposed per position, so the team's lanes read distinct LDS banks
     const float* xsrc = x + (size_t)b0 * m.cols;
-    for (int i = threadIdx.x; i < NB * m.cols; i += kBlock) smem[i] = (double)xsrc[i];
+    const XLayout lay = chunk_layout<FMT>(m.nchunks);
+    for (int i = threadIdx.x; i < NB * m.cols; i += kBlock) {
+      const int b = i / m.cols, j = i - b * m.cols;
+      smem[b * m.cols + lay.pos(j)] = (double)xsrc[i];
+    }
     __syncthreads();
     xuse = smem;
   } else {
@@ -36,7 +41,7 @@ __global__ __launch_bounds__(kBlock) void k_matvec(DMat m, const float* __restri
 #pragma unroll
   for (int i = 0; i < R; i++) rows[i] = min(row0 + i, m.rows - 1);
   double acc[NB][R];
-  mv_team<FMT, R, NB, TL>(m, rows, xuse, m.cols, T::lane(), acc);
+  mv_team<FMT, R, NB, TL, X_LDS>(m, rows, xuse, m.cols, T::lane(), acc);
   if (T::lane() == 0) {
 #pragma unroll
     for (int b = 0; b < NB; b++) {
@@ -235,18 +240,23 @@ hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t
 // ----------------------------------------------------------------- rmsnorm --
 __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float* __restrict__ x,
                                                     const float* __restrict__ gain,
-                                                    float* __restrict__ y, int cols, double eps) {
+                                                    float* __restrict__ y, int cols, double eps,
+                                                    int vec) {
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   const size_t base = (size_t)blockIdx.x * cols;
-  stage_rmsnorm(x + base, gain, eps, cols, smem, red);
+  if (vec) stage_rmsnorm(x + base, gain, eps, cols, smem, red, kPlain);
+  else stage_rmsnorm_scalar(x + base, gain, eps, cols, smem, red);
   for (int i = threadIdx.x; i < cols; i += kBlock) y[base + i] = (float)smem[i];
 }
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
                           int cols, double eps) {
+  // The vector staging reads float4 groups: every row start and the gain 16-byte aligned.
+  const int vec = (cols % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)gain % 16 == 0) &&
+                  cols <= kStageMax;
   hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), cols * sizeof(double), s, x, gain, y,
-                     cols, eps);
+                     cols, eps, vec);
   return hipGetLastError();
 }
 
@@ -278,54 +288,58 @@ hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float*
 }
 
 // --------------------------------------------------------------- KV append --
+// Keys position-major [kv_heads][capacity][64], values dimension-major
+// [kv_heads][64][vstride] (the layout attention.h reads).
 __global__ void k_kv_append(const float* __restrict__ k, const float* __restrict__ v,
-                            uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int capacity,
+                            uint16_t* __restrict__ kc, uint16_t* __restrict__ vt, int capacity,
                             int kv_heads, int head_dim, int past, int seq) {
   const int kv_dim = kv_heads * head_dim;
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= seq * kv_dim) return;
   const int t = idx / kv_dim, e = idx % kv_dim;
   const int h = e / head_dim, d = e % head_dim;
-  const size_t at = ((size_t)h * capacity + past + t) * head_dim + d;
-  kc[at] = __builtin_bit_cast(uint16_t, (_Float16)k[idx]);
-  vc[at] = __builtin_bit_cast(uint16_t, (_Float16)v[idx]);
+  kc[((size_t)h * capacity + past + t) * head_dim + d] = __builtin_bit_cast(uint16_t, (_Float16)k[idx]);
+  vt[((size_t)h * head_dim + d) * value_stride(capacity) + past + t] =
+      __builtin_bit_cast(uint16_t, (_Float16)v[idx]);
 }
 
 hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint16_t* kc,
-                            uint16_t* vc, int capacity, int kv_heads, int head_dim, int past,
+                            uint16_t* vt, int capacity, int kv_heads, int head_dim, int past,
                             int seq) {
   const int n = seq * kv_heads * head_dim;
-  hipLaunchKernelGGL(k_kv_append, dim3((n + 255) / 256), dim3(256), 0, s, k, v, kc, vc, capacity,
+  hipLaunchKernelGGL(k_kv_append, dim3((n + 255) / 256), dim3(256), 0, s, k, v, kc, vt, capacity,
                      kv_heads, head_dim, past, seq);
   return hipGetLastError();
 }
 
 // --------------------------------------------------------------- attention --
+static int score_stride(int total) { return (total + 3) & ~3; }
+
 size_t attention_exact_floats(int seq, int heads, int past) {
-  const size_t total = (size_t)past + seq;
-  return (size_t)seq * heads * (total + attn_chunks((int)total));
+  const int total = past + seq;
+  return (size_t)seq * heads * (score_stride(total) + attn_spans(total));
 }
 
 hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t* kc,
-                                  const uint16_t* vc, int capacity, float* out, int seq, int past,
-                                  int heads, int kv_heads, float* scores, float* maxes) {
+                                  const uint16_t* vt, int capacity, float* out, int seq, int past,
+                                  int heads, int kv_heads, float* scores, int* counters) {
   ExactArgs a{};
+  const int total = past + seq;
   a.q = q;
   a.kc = kc;
-  a.vc = vc;
+  a.vt = vt;
   a.scores = scores;
-  a.maxes = maxes;
+  a.score_stride = score_stride(total);
+  a.max_stride = attn_spans(total);
+  a.maxes = scores + (size_t)seq * heads * a.score_stride;
+  a.counters = counters;
   a.out = out;
   a.past = past;
   a.capacity = capacity;
+  a.vstride = value_stride(capacity);
   a.heads = heads;
   a.kv_heads = kv_heads;
-  a.score_stride = past + seq;
-  a.max_stride = attn_chunks(past + seq);
-  hipLaunchKernelGGL(k_attn_scores, dim3(a.max_stride, kv_heads, seq), dim3(kBlock), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_pv, dim3(heads, seq), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL(k_attn_exact, dim3(a.max_stride, heads, seq), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
@@ -334,18 +348,19 @@ size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx) 
 }
 
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
-                                   const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                   const uint16_t* vt, int capacity, float* out, int seq, int past,
                                    int heads, int kv_heads, float* partials, int* counters) {
   SplitArgs a{};
   a.q = q;
   a.kc = kc;
-  a.vc = vc;
+  a.vt = vt;
   a.partials = partials;
   a.counters = counters;
   a.out = out;
   a.past = past;
   a.seq = seq;
   a.capacity = capacity;
+  a.vstride = value_stride(capacity);
   a.heads = heads;
   a.kv_heads = kv_heads;
   a.s_grid = attn_grid_splits(past + seq);

@@ -46,6 +46,13 @@ struct DMat {
 int make_dmat(const qh_weight* w, DMat* out);
 int weights_per_chunk(int format);
 
+// Row length of the dimension-major value cache [kv_heads][head_dim][vstride]: capacity
+// rounded up to 8, so every row starts 16-byte aligned.
+__host__ __device__ inline int value_stride(int capacity) { return (capacity + 7) & ~7; }
+// Exact attention scores 256 positions per block ("span").
+constexpr int kSpan = 256;
+__host__ __device__ inline int attn_spans(int ctx) { return (ctx + kSpan - 1) / kSpan; }
+
 }  // namespace qh
 
 struct qh_ctx {
@@ -81,19 +88,22 @@ hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, floa
                           int cols, double eps);
 hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float* sin_t, int rows,
                        int heads, int head_dim, int base_pos);
+// Keys [kv_heads][capacity][head_dim]; values dimension-major [kv_heads][head_dim][vstride],
+// vstride = capacity rounded up to a multiple of 8.
 hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint16_t* kc,
-                            uint16_t* vc, int capacity, int kv_heads, int head_dim, int past,
+                            uint16_t* vt, int capacity, int kv_heads, int head_dim, int past,
                             int seq);
-// Exact-order attention over an f16 head-major cache. `scores` holds
-// seq*heads*(past+seq) floats and `maxes` seq*heads*chunks(past+seq) floats.
+// Exact-order attention. `scores` holds attention_exact_floats(seq, heads, past) floats
+// (scores, then per-span maxima) and `counters` seq*heads ints, zero before the launch and
+// left zero after it.
 hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t* kc,
-                                  const uint16_t* vc, int capacity, float* out, int seq, int past,
-                                  int heads, int kv_heads, float* scores, float* maxes);
+                                  const uint16_t* vt, int capacity, float* out, int seq, int past,
+                                  int heads, int kv_heads, float* scores, int* counters);
 size_t attention_exact_floats(int seq, int heads, int past);
 // Split-K attention. `partials` holds attention_partials_floats(...) floats and `counters`
 // seq*kv_heads ints, zeroed before first use (the kernel leaves them zeroed).
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
-                                   const uint16_t* vc, int capacity, float* out, int seq, int past,
+                                   const uint16_t* vt, int capacity, float* out, int seq, int past,
                                    int heads, int kv_heads, float* partials, int* counters);
 size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx);
 // f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).

@@ -160,6 +160,13 @@ def _declare(lib: ctypes.CDLL) -> None:
         f.restype = ctypes.c_int
     lib.qh_stream.argtypes = [vp]
     lib.qh_stream.restype = vp
+    lib.qh_value_cache_bytes.argtypes = [i32, i32, i32]
+    lib.qh_value_cache_bytes.restype = ctypes.c_size_t
+
+
+def value_cache_bytes(capacity: int, kv_heads: int, head_dim: int = 64) -> int:
+    """Bytes of a dimension-major value cache (rows of capacity rounded up to 8)."""
+    return int(load_library().qh_value_cache_bytes(capacity, kv_heads, head_dim))
 
 
 def _check(rc: int) -> None:

@@ -71,6 +71,45 @@ def test_matvec_matches_oracle(ctx, hip, fmt, rows, cols):
     free(wb, dx, db, dy)
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_matvec_irregular_quant_params(ctx, hip, fmt):
+    # Scales and zero points the quantizer never writes (zero, negative, non-integer or
+    # out-of-range zero points, huge scales) take the reference's dequant arithmetic
+    # rather than the biased-byte form; either way each weight is the loader's f32.
+    rows, cols, group = 64, 896, 128
+    rng = np.random.default_rng(11)
+    w32 = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    x = rng.standard_normal(cols).astype(np.float32)
+    if fmt == "int8":
+        q, s = hip.quantize_int8(w32)
+        s[::5] = 0.0
+        s[1::5] *= -1.0
+        s[2::5] = np.float32(2.0 ** 110)
+        bufs = [ctx.upload(q), ctx.upload(s)]
+        W = ctx.weight(hip.FMT_INT8, rows, cols, bufs[0], bufs[1])
+        deq = O.dequantize_int8(q, s)
+    else:
+        q, s, z = hip.quantize_int4(w32, group)
+        s, z = s.reshape(rows, -1), z.reshape(rows, -1)
+        z[::4, 0] = 2.5
+        z[1::4, 1] = 17.0
+        z[2::4, 2] = -3.0
+        s[3::4, 3] *= -1.0
+        s[::6, 4] = 0.0
+        s, z = s.reshape(-1), z.reshape(-1)
+        bufs = [ctx.upload(q), ctx.upload(s), ctx.upload(z)]
+        W = ctx.weight(hip.FMT_INT4, rows, cols, bufs[0], bufs[1], bufs[2], group)
+        deq = O.dequantize_int4(q, s, z, cols, group)
+    dx, dy = ctx.upload(x), ctx.empty(rows * 4)
+    ctx.matvec(W, dx, None, dy, 1)
+    got = dy.read(count=rows)
+    ref = O.matvec(deq, x, rows, cols)
+    finite = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), finite)
+    assert ulps(got[finite], ref[finite]) <= 1
+    free(bufs, dx, dy)
+
+
 def test_matvec_lm_head_shape_int8(ctx, hip):
     rows, cols = 151936, 896
     rng = np.random.default_rng(1)
@@ -181,25 +220,34 @@ def test_rope_beyond_table_is_range_error(ctx, hip):
 
 
 def kv_setup(ctx, hip, capacity, ctx_len, seed, kv_heads=2):
-    """An f16 head-major cache holding ctx_len positions of K, V ~ N(0,1), written by
-    qh_kv_append; returns device caches and the oracle's [pos, kv_dim] f32 views."""
+    """f16 caches holding ctx_len positions of K, V ~ N(0,1), written by qh_kv_append;
+    returns device caches and the oracle's [pos, kv_dim] f32 views."""
     rng = np.random.default_rng(seed)
     k = rng.standard_normal((ctx_len, kv_heads * 64)).astype(np.float32)
     v = rng.standard_normal((ctx_len, kv_heads * 64)).astype(np.float32)
-    kc, vc = ctx.empty(kv_heads * capacity * 64 * 2), ctx.empty(kv_heads * capacity * 64 * 2)
+    kc = ctx.empty(kv_heads * capacity * 64 * 2)
+    vc = ctx.empty(hip.value_cache_bytes(capacity, kv_heads))
     dk, dv = ctx.upload(k), ctx.upload(v)
     ctx.kv_append(dk, dv, kc, vc, capacity, kv_heads, 64, 0, ctx_len)
     free(dk, dv)
     return kc, vc, O.through_f16(k), O.through_f16(v)
 
 
-def test_kv_append_rounds_to_f16_exactly(ctx, hip):
-    kc, vc, kr, vr = kv_setup(ctx, hip, 8, 5, 0)
-    got = kc.read(np.uint16, 2 * 8 * 64).reshape(2, 8, 64)[:, :5]
+@pytest.mark.parametrize("capacity", [8, 13])
+def test_kv_append_rounds_to_f16_exactly(ctx, hip, capacity):
+    # keys position-major [kv_heads, capacity, 64]; values dimension-major
+    # [kv_heads, 64, vstride] with vstride = capacity rounded up to 8
+    kc, vc, kr, vr = kv_setup(ctx, hip, capacity, 5, 0)
+    got = kc.read(np.uint16, 2 * capacity * 64).reshape(2, capacity, 64)[:, :5]
     want = O.f32_to_f16(kr).reshape(5, 2, 64).transpose(1, 0, 2)
     np.testing.assert_array_equal(got, want)
+    vstride = (capacity + 7) // 8 * 8
+    assert hip.value_cache_bytes(capacity, 2) == 2 * 64 * vstride * 2
+    got_v = vc.read(np.uint16, 2 * 64 * vstride).reshape(2, 64, vstride)[:, :, :5]
+    want_v = O.f32_to_f16(vr).reshape(5, 2, 64).transpose(1, 2, 0)
+    np.testing.assert_array_equal(got_v, want_v)
     with pytest.raises(hip.RangeError):
-        ctx.kv_append(kc, vc, kc, vc, 8, 2, 64, 6, 3)
+        ctx.kv_append(kc, vc, kc, vc, capacity, 2, 64, capacity - 2, 3)
     free(kc, vc)
 
 
