@@ -11,16 +11,17 @@
 //
 // Two algorithms:
 //
-// Exact order (k_attn_exact), what the model path uses. It evaluates
-// groupedAttention (src/core/attention.js:32-66) step for step: each score is a
-// sequential f64 dot stored to f32, the softmax shifts by the global max and
-// normalizes with an f64 sum (src/core/ops.js:66-78), and the output
-// accumulates sequentially over positions in f32, as the reference's
-// Float32Array `out += weight * value` does. Blocks score 256 positions each;
-// the last block of a (query, head) to finish does the softmax and the
-// sequential PV sum, one lane per output dimension. The result matches the CPU
-// to the bit apart from f64-order noise, so a device f16 cache and the CPU's
-// same-f16 cache stay identical.
+// Exact order (k_attn_block up to kPLds positions, k_attn_exact beyond), what
+// the model path uses. It evaluates groupedAttention (src/core/attention.js:
+// 32-66) step for step: each score is a sequential f64 dot stored to f32, the
+// softmax shifts by the global max and normalizes with an f64 sum
+// (src/core/ops.js:66-78), and the output accumulates sequentially over
+// positions in f32, as the reference's Float32Array `out += weight * value`
+// does, one lane per output dimension. k_attn_block does a (query, head) in one
+// 1024-thread block; k_attn_exact scores 256 positions per block and the last
+// block of a (query, head) to finish does the softmax and the PV sum. The
+// result matches the CPU to the bit apart from f64-order noise, so a device f16
+// cache and the CPU's same-f16 cache stay identical.
 //
 // Split-K online softmax (k_attention_splitk), for long contexts: one block
 // per (query, kv head, split of chunks) stages K/V once for all the query heads
@@ -38,7 +39,7 @@ constexpr int kMaxSplits = 128;   // split-K: splits per (query, kv head)
 constexpr int kHeadDim = 64;
 constexpr int kMaxGroup = 8;      // query heads per kv head
 constexpr int kPartialStride = kHeadDim + 2;  // split-K partial: m, l, acc[64]
-constexpr int kPLds = 8192;       // exact: probabilities kept in LDS up to this context
+constexpr int kPLds = 4096;       // exact: probabilities kept in LDS up to this context
 static_assert(kSpan == kBlock, "exact attention scores one position per thread");
 
 __host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
@@ -57,45 +58,217 @@ struct ExactArgs {
   int past, capacity, vstride, heads, kv_heads, score_stride, max_stride;
 };
 
-// out[d] = sum over s < ctx of p[s] * v[s][d], s ascending, rounding to f32 at
-// every step, by the 64 lanes of one wave (lane d). The product is exact in the
-// fused form, so each step is the CPU's f64 sum stored to f32 except in
-// double-rounding ties (probability ~2^-29 per step). Values come 8 positions
-// per 16-byte load, 64 positions in flight ahead of the arithmetic.
-__device__ __forceinline__ float pv_chain(const float* __restrict__ p, const uint16_t* __restrict__ vrow,
-                                          int ctx) {
-  constexpr int G = 8;  // 16-byte groups per batch
-  const int full = ctx & ~7;
-  const v4u* vg = reinterpret_cast<const v4u*>(vrow);
-  const v4f* pg = reinterpret_cast<const v4f*>(p);
-  float o = 0.f;
-  v4u cur[G], nxt[G];
+// The sequential PV sum reads values from LDS: the last block stages a head's
+// values in chunks of kVChunk positions, double-buffered, waves 1-3 loading
+// chunk k+1 while wave 0 sums chunk k. Rows are padded by 16 bytes, so the 64
+// lanes (one row each) spread their 16-byte reads over all LDS banks.
+constexpr int kVChunk = 512;
+constexpr int kVRow = kVChunk + 8;   // f16 elements per staged row
+
+// buf[d][0..n8) = values of dimension d at positions p0 .. p0+n8-1, n8 = n rounded
+// up to 8 (the tail group stays inside the row: vstride is a multiple of 8 and
+// p0 + n <= capacity). Thread t of nt loads NS 16-byte groups before storing any.
+template <int NS>
+__device__ __forceinline__ void stage_values(const uint16_t* __restrict__ vbase, int vstride, int p0,
+                                             int n, uint16_t (*buf)[kVRow], int t, int nt) {
+  const int gpr = (n + 7) >> 3;  // 16-byte groups per row
+  const int items = kHeadDim * gpr;
+  for (int base = 0; base < items; base += nt * NS) {
+    v4u v[NS];
 #pragma unroll
-  for (int k = 0; k < G; k++)
-    if (8 * k < full) cur[k] = vg[k];
-  for (int s = 0; s < full; s += 8 * G) {
-#pragma unroll
-    for (int k = 0; k < G; k++)
-      if (s + 8 * G + 8 * k < full) nxt[k] = vg[(s + 8 * G) / 8 + k];
-#pragma unroll
-    for (int k = 0; k < G; k++) {
-      if (s + 8 * k < full) {
-        const v4f pa = pg[(s + 8 * k) / 4], pb = pg[(s + 8 * k) / 4 + 1];
-        o = fmaf(pa.x, f16_lo(cur[k].x), o);
-        o = fmaf(pa.y, f16_hi(cur[k].x), o);
-        o = fmaf(pa.z, f16_lo(cur[k].y), o);
-        o = fmaf(pa.w, f16_hi(cur[k].y), o);
-        o = fmaf(pb.x, f16_lo(cur[k].z), o);
-        o = fmaf(pb.y, f16_hi(cur[k].z), o);
-        o = fmaf(pb.z, f16_lo(cur[k].w), o);
-        o = fmaf(pb.w, f16_hi(cur[k].w), o);
+    for (int j = 0; j < NS; j++) {
+      const int i = base + t + j * nt;
+      if (i < items) {
+        const int d = i / gpr, gi = i - d * gpr;
+        v[j] = *reinterpret_cast<const v4u*>(vbase + (size_t)d * vstride + p0 + 8 * gi);
       }
     }
 #pragma unroll
-    for (int k = 0; k < G; k++) cur[k] = nxt[k];
+    for (int j = 0; j < NS; j++) {
+      const int i = base + t + j * nt;
+      if (i < items) {
+        const int d = i / gpr, gi = i - d * gpr;
+        *reinterpret_cast<v4u*>(&buf[d][8 * gi]) = v[j];
+      }
+    }
   }
-  for (int s = full; s < ctx; s++) o = fmaf(p[s], (float)__builtin_bit_cast(_Float16, vrow[s]), o);
+}
+
+// Eight steps of the PV sum: o += p[s] * v[s] in order, v eight f16 values.
+__device__ __forceinline__ float pv8(const v4f pa, const v4f pb, const v4u v, float o) {
+  o = fmaf(pa.x, f16_lo(v.x), o);
+  o = fmaf(pa.y, f16_hi(v.x), o);
+  o = fmaf(pa.z, f16_lo(v.y), o);
+  o = fmaf(pa.w, f16_hi(v.y), o);
+  o = fmaf(pb.x, f16_lo(v.z), o);
+  o = fmaf(pb.y, f16_hi(v.z), o);
+  o = fmaf(pb.z, f16_lo(v.w), o);
+  o = fmaf(pb.w, f16_hi(v.w), o);
   return o;
+}
+
+// o += p[s] * v[s] for s < n, ascending, rounding to f32 at every step (lane d
+// holds output dimension d; row = its staged values). The product is exact in
+// the fused form, so each step is the CPU's f64 sum stored to f32 except in
+// double-rounding ties (probability ~2^-29 per step). row is LDS (p is LDS or
+// global); the reads of the next 16 positions are issued before the current 16
+// are summed.
+struct PvGroup {  // 16 positions: p as 4 x float4, values as 2 x 8 f16
+  v4f p[4];
+  v4u v[2];
+};
+__device__ __forceinline__ void pv_load(const v4f* pg, const v4u* vg, int grp, PvGroup& g) {
+#pragma unroll
+  for (int k = 0; k < 4; k++) g.p[k] = pg[4 * grp + k];
+  g.v[0] = vg[2 * grp];
+  g.v[1] = vg[2 * grp + 1];
+}
+__device__ __forceinline__ float pv_sum(const PvGroup& g, float o) {
+  o = pv8(g.p[0], g.p[1], g.v[0], o);
+  return pv8(g.p[2], g.p[3], g.v[1], o);
+}
+
+__device__ __forceinline__ float pv_lds(const float* __restrict__ p, const uint16_t* row, int n, float o) {
+  const v4f* pg = reinterpret_cast<const v4f*>(p);
+  const v4u* vg = reinterpret_cast<const v4u*>(row);
+  const int groups = n >> 4;
+  // Two named buffers alternate, so no register copies sit between the loads of
+  // one group and the arithmetic of the other.
+  PvGroup a, b;
+  if (groups > 0) pv_load(pg, vg, 0, a);
+  int grp = 0;
+  for (; grp + 2 <= groups; grp += 2) {
+    pv_load(pg, vg, grp + 1, b);
+    o = pv_sum(a, o);
+    if (grp + 2 < groups) pv_load(pg, vg, grp + 2, a);
+    o = pv_sum(b, o);
+  }
+  if (grp < groups) o = pv_sum(a, o);
+  for (int s = groups << 4; s < n; s++) o = fmaf(p[s], (float)__builtin_bit_cast(_Float16, row[s]), o);
+  return o;
+}
+
+// ------------------------------------------------- exact order, one block --
+// Contexts up to kPLds: one 512-thread block per (query, head) does it all in
+// LDS -- scores one position per thread and step, softmax, and the PV sum by
+// wave 0 while the other 7 waves stage the next value chunk -- with no
+// cross-block synchronization. The first value chunk and the first key rows are in flight
+// from the kernel's start.
+constexpr int kAttnThreads = 512;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+
+__device__ __forceinline__ double block_sum_f64_n(double v, double* red) {
+  v = team_sum<64>(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  double t = 0;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; w++) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+static __global__ __launch_bounds__(kAttnThreads) void k_attn_block(ExactArgs a) {
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int past = a.d_pos ? *a.d_pos : a.past;
+  const int pos = past + t;
+  if (pos >= a.capacity || pos >= kPLds) return;  // the host keeps positions inside both
+  const int ctx = pos + 1;
+  const int g = h / (a.heads / a.kv_heads);
+  const int tid = threadIdx.x;
+
+  __shared__ double qs[kHeadDim];
+  __shared__ float wred[kAttnWaves];
+  __shared__ double red[kAttnWaves];
+  __shared__ __attribute__((aligned(16))) float pl[kPLds];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kHeadDim][kVRow];
+
+  // First value chunk: 64 rows x up to 64 16-byte groups, 8 per thread.
+  const uint16_t* vbase = a.vt + (size_t)g * kHeadDim * a.vstride;
+  const int n0 = min(ctx, kVChunk);
+  const int gpr0 = (n0 + 7) >> 3;
+  constexpr int kPre = kHeadDim * (kVChunk / 8) / kAttnThreads;
+  v4u vpre[kPre];
+#pragma unroll
+  for (int j = 0; j < kPre; j++) {
+    const int i = tid + j * kAttnThreads;
+    if (i < kHeadDim * gpr0) {
+      const int d = i / gpr0, gi = i - d * gpr0;
+      vpre[j] = *reinterpret_cast<const v4u*>(vbase + (size_t)d * a.vstride + 8 * gi);
+    }
+  }
+  const uint16_t* kb = a.kc + (size_t)g * a.capacity * kHeadDim;
+  v4u kr[8];
+  if (tid < ctx) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) kr[j] = reinterpret_cast<const v4u*>(kb + (size_t)tid * kHeadDim)[j];
+  }
+  if (tid < kHeadDim) qs[tid] = (double)a.q[((size_t)t * a.heads + h) * kHeadDim + tid];
+  __syncthreads();
+
+  // Scores: dot += q[i] * k[i], i ascending, in f64 (each product is exact), stored f32.
+  float m = -INFINITY;
+  for (int p = tid; p < ctx; p += kAttnThreads) {
+    if (p != tid) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) kr[j] = reinterpret_cast<const v4u*>(kb + (size_t)p * kHeadDim)[j];
+    }
+    double dot = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t u[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        dot = fma(qs[8 * j + 2 * e], (double)f16_lo(u[e]), dot);
+        dot = fma(qs[8 * j + 2 * e + 1], (double)f16_hi(u[e]), dot);
+      }
+    }
+    const float s = (float)(dot * 0.125);  // scale = 1/sqrt(64), exact
+    pl[p] = s;
+    m = fmaxf(m, s);
+  }
+#pragma unroll
+  for (int j = 0; j < kPre; j++) {
+    const int i = tid + j * kAttnThreads;
+    if (i < kHeadDim * gpr0) {
+      const int d = i / gpr0, gi = i - d * gpr0;
+      *reinterpret_cast<v4u*>(&vbuf[0][d][8 * gi]) = vpre[j];
+    }
+  }
+  m = wave_max(m);
+  if ((tid & (kWave - 1)) == 0) wred[tid / kWave] = m;
+  __syncthreads();
+  float mb = wred[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; w++) mb = fmaxf(mb, wred[w]);
+  const double M = mb;
+  // e = exp(s - max) stored f32; the sum over the unrounded e in f64; p = f32(e32 * (1/sum)).
+  double sum = 0.0;
+  for (int p = tid; p < ctx; p += kAttnThreads) {
+    const double e = exp((double)pl[p] - M);
+    pl[p] = (float)e;
+    sum += e;
+  }
+  sum = block_sum_f64_n(sum, red);
+  const double inv = 1.0 / sum;
+  for (int p = tid; p < ctx; p += kAttnThreads) pl[p] = (float)((double)pl[p] * inv);
+  __syncthreads();
+
+  const int nch = (ctx + kVChunk - 1) / kVChunk;
+  float o = 0.f;
+  for (int k = 0; k < nch; k++) {
+    const int p0 = k * kVChunk;
+    if (tid < kWave) {
+      o = pv_lds(pl + p0, vbuf[k & 1][tid], min(kVChunk, ctx - p0), o);
+    } else if (k + 1 < nch) {
+      // 448 threads x 10 groups cover a chunk's 64 x 64 groups in one pass
+      stage_values<10>(vbase, a.vstride, p0 + kVChunk, min(kVChunk, ctx - p0 - kVChunk), vbuf[(k + 1) & 1],
+                      tid - kWave, kAttnThreads - kWave);
+    }
+    __syncthreads();
+  }
+  if (tid < kHeadDim) a.out[((size_t)t * a.heads + h) * kHeadDim + tid] = o;
 }
 
 // grid (spans, heads, seq). Block (span, h, t) scores positions span*256 ..
@@ -118,6 +291,7 @@ static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
   __shared__ double red[kBlock / kWave];
   __shared__ int is_last;
   __shared__ __attribute__((aligned(16))) float pl[kPLds];
+  __shared__ __attribute__((aligned(16))) uint16_t vbuf[2][kHeadDim][kVRow];
 
   v4u kr[8];
   if (p < ctx) {
@@ -158,6 +332,11 @@ static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
   if (!is_last) return;
   __threadfence();
 
+  // The first value chunk loads while the softmax runs.
+  const uint16_t* vbase = a.vt + (size_t)g * kHeadDim * a.vstride;
+  const int nch = (ctx + kVChunk - 1) / kVChunk;
+  stage_values<16>(vbase, a.vstride, 0, min(ctx, kVChunk), vbuf[0], tid, kBlock);
+
   // The global max is the max of the span maxima (max is order-free).
   float m = -INFINITY;
   for (int c = tid; c < nspan; c += kBlock) m = fmaxf(m, a.maxes[row * a.max_stride + c]);
@@ -178,10 +357,20 @@ static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
   const double inv = 1.0 / sum;
   for (int i = tid; i < ctx; i += kBlock) pb[i] = (float)((double)pb[i] * inv);
   __syncthreads();
-  if (tid < kHeadDim) {
-    const uint16_t* vrow = a.vt + ((size_t)g * kHeadDim + tid) * a.vstride;
-    a.out[row * kHeadDim + tid] = pv_chain(pb, vrow, ctx);
+  float o = 0.f;
+  for (int k = 0; k < nch; k++) {
+    const int p0 = k * kVChunk;
+    if (tid < kWave) {
+      // separate calls, so the LDS one compiles to LDS reads rather than flat ones
+      if (ctx <= kPLds) o = pv_lds(pl + p0, vbuf[k & 1][tid], min(kVChunk, ctx - p0), o);
+      else o = pv_lds(sc + p0, vbuf[k & 1][tid], min(kVChunk, ctx - p0), o);
+    } else if (k + 1 < nch) {
+      stage_values<16>(vbase, a.vstride, p0 + kVChunk, min(kVChunk, ctx - p0 - kVChunk), vbuf[(k + 1) & 1],
+                       tid - kWave, kBlock - kWave);
+    }
+    __syncthreads();
   }
+  if (tid < kHeadDim) a.out[row * kHeadDim + tid] = o;
   if (tid == 0) a.counters[row] = 0;
 }
 

@@ -1,20 +1,19 @@
 // The fused decode step: the whole of GpuModel.#forward for one position
-// (src/gpu/model.js:240-402) as 5 launches per layer plus the gather and the
-// output head, instead of the reference's ~15 dispatches and 2 copies per
-// layer. Every launch reads its position from device memory, so the same
-// launches are captured once in a hipGraph and replayed every token.
+// (src/gpu/model.js:240-402) as 5 launches per layer plus the output head and
+// the pick, instead of the reference's ~15 dispatches and 2 copies per layer.
+// Every launch reads its position from device memory, so the same launches are
+// captured once in a hipGraph and replayed every token.
 //
 // Per layer (the order of src/cpu/model.js:89-143):
 //   1. rmsnorm(x) -> q|k|v matvec + bias -> rope (f64) -> q, f16 K/V append
-//   2. attention: scores per 256-position span (f64 dots); the last span block
-//      of each head does the softmax and the sequential PV sum
+//   2. attention per head (scores as f64 dots, softmax, sequential PV sum)
 //   3. o-proj matvec, residual add into x
 //   4. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
 //   5. down matvec, residual add into x
-// then rmsnorm -> lm_head -> logits and argmax; the last block to finish
-// writes the token (the reference reads back 151,936 logits and scans them on
-// the host, src/gpu/model.js:372-382, web/bench.html:129-131) and advances
-// the position.
+// then rmsnorm -> lm_head -> logits and per-block argmax partials, and the pick,
+// which chooses the token (the reference reads back 151,936 logits and scans
+// them on the host, src/gpu/model.js:372-382, web/bench.html:129-131),
+// advances the position and gathers the next position's embedding.
 //
 // A matvec launch is latency-bound at these sizes (a layer's int4 weights are
 // 7.5 MB), so each team issues the loads of its whole share of the weights
@@ -45,14 +44,11 @@ struct FusedArgs {
   uint16_t* vt;         // this layer's values [kv_heads][64][vstride]
   int vstride;
   int heads, kv_heads;
-  // EPI_QKV, EPI_LOGITS: the decode state
+  // EPI_QKV: the decode state
   int* state;           // [0] position, [1] forced length
   int capacity;
   // EPI_LOGITS
-  ArgPair* partials;
-  int* counter;
-  int* tokens;          // [capacity + 1]
-  int* pred;            // [capacity]
+  ArgPair* partials;     // [blocks]: each block's best (value, index)
 };
 
 // Rows of work item `it`. QKV: a rope pair (j, j+32) of a q or k head, or two
@@ -150,8 +146,6 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   __shared__ ArgPair tbest[kBlock / TL];
-  __shared__ ArgPair wred[kBlock / kWave];
-  __shared__ int is_last;
   double* xs = smem;
   using T = Teams<TL>;
   const int lane = T::lane();
@@ -201,32 +195,46 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
           i = tbest[t].i;
         }
       }
-      a.partials[blockIdx.x] = {v, i};
-      __threadfence();
-      is_last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    float v = NAN;
-    int i = 0x7fffffff;
-    for (int b = threadIdx.x; b < (int)gridDim.x; b += kBlock) {
-      const ArgPair p = a.partials[b];
-      if (argmax_better(p.v, p.i, v, i)) {
-        v = p.v;
-        i = p.i;
-      }
-    }
-    argmax_block(v, i, wred);
-    if (threadIdx.x == 0) {
-      const int tok = (a.out[0] != a.out[0]) ? 0 : i;
-      const int p = a.state[0];
-      if (p < a.capacity) a.pred[p] = tok;
-      if (p + 1 >= a.state[1] && p + 1 <= a.capacity) a.tokens[p + 1] = tok;
-      a.state[0] = p + 1;
-      *a.counter = 0;
+      a.partials[blockIdx.x] = {v, i};  // reduced by k_pick, the next launch
     }
   }
+}
+
+// The end of a step with logits: the best of the head's block partials is the
+// token (lowest index among equal maxima, NaN logits -> 0, the reference's
+// host-side scan of src/gpu/model.js:372-382); it is recorded, the position
+// advances, and x becomes the embedding of the next position's token -- the
+// caller's below the forced length, else this one -- so the next step needs no
+// gather launch of its own.
+__global__ __launch_bounds__(kBlock) void k_pick(const ArgPair* __restrict__ partials, int nparts,
+                                                 const float* __restrict__ logits, int* state,
+                                                 int* tokens, int* pred, int capacity,
+                                                 const uint16_t* __restrict__ embed, int hidden,
+                                                 int vocab, float* __restrict__ x) {
+  __shared__ ArgPair wred[kBlock / kWave];
+  __shared__ int next;
+  float v = NAN;
+  int i = 0x7fffffff;
+  for (int b = threadIdx.x; b < nparts; b += kBlock) {
+    const ArgPair p = partials[b];
+    if (argmax_better(p.v, p.i, v, i)) {
+      v = p.v;
+      i = p.i;
+    }
+  }
+  argmax_block(v, i, wred);
+  if (threadIdx.x == 0) {
+    const int tok = (logits[0] != logits[0]) ? 0 : i;
+    const int p = state[0];
+    if (p < capacity) pred[p] = tok;
+    if (p + 1 >= state[1] && p + 1 <= capacity) tokens[p + 1] = tok;
+    state[0] = p + 1;
+    int t = p + 1 <= capacity ? tokens[p + 1] : tok;
+    next = (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
+  }
+  __syncthreads();
+  const uint16_t* row = embed + (size_t)next * hidden;
+  for (int k = threadIdx.x; k < hidden; k += kBlock) x[k] = __builtin_bit_cast(float, (uint32_t)row[k] << 16);
 }
 
 // x = the bf16 embedding row of the token at the current position, widened exactly.
@@ -248,7 +256,7 @@ __global__ void k_advance(int* state) {
 }
 
 constexpr int kLmRows = 4;          // rows per team in the output head
-constexpr int kLmMaxBlocks = 2048;  // the head's teams take ceil(items / (teams * blocks)) items each
+constexpr int kLmMaxBlocks = 1024;  // the head's teams take ceil(items / (teams * blocks)) items each
 
 // Chunks per lane a kernel is built for: the smallest instantiated count that
 // covers ceil(nchunks / TL).
@@ -310,7 +318,7 @@ int lm_head_blocks(const ModelDev& m) {
 size_t lm_partials_bytes(const ModelDev& m) { return (size_t)lm_head_blocks(m) * sizeof(ArgPair); }
 
 int launches_per_step(const ModelDev& m, StepInput in) {
-  return (in == STEP_GATHER ? 1 : 0) + 5 * m.layers + 1;
+  return (in == STEP_GATHER ? 1 : 0) + 5 * m.layers + 2;
 }
 
 // Records the event that opens a launch of `role` (see StepTimer).
@@ -321,14 +329,18 @@ static hipError_t mark(hipStream_t s, StepTimer* t, int role) {
   return hipEventRecord(t->events[t->n++], s);
 }
 
+hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c) {
+  hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, m.embed, c.tokens, c.state, c.capacity,
+                     m.hidden, m.vocab, c.x);
+  return hipGetLastError();
+}
+
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
                         bool logits, StepTimer* timer) {
   hipError_t e;
   if (in == STEP_GATHER) {
     if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(kBlock), 0, s, m.embed, c.tokens, c.state,
-                       c.capacity, m.hidden, m.vocab, c.x);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = enqueue_gather(s, m, c)) != hipSuccess) return e;
   }
   const int kv_dim = m.kv_heads * m.head_dim;
   for (int L = 0; L < m.layers; L++) {
@@ -372,7 +384,11 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     a.score_stride = c.score_stride;
     a.max_stride = attn_spans(c.capacity);
     if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
+    if (c.capacity <= kPLds) {
+      hipLaunchKernelGGL(k_attn_block, dim3(m.heads, 1), dim3(kAttnThreads), 0, s, a);
+    } else {
+      hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
+    }
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
     f = FusedArgs{};
@@ -410,15 +426,16 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     f.gain = m.final_norm;
     f.out = c.logits;
     f.partials = static_cast<ArgPair*>(c.lm_partials);
-    f.counter = c.lm_counter;
-    f.state = c.state;
-    f.tokens = c.tokens;
-    f.pred = c.pred;
-    f.capacity = c.capacity;
     if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
     if ((e = fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows,
                                                      kLmMaxBlocks)) != hipSuccess)
       return e;
+    // The pick gathers the next input row, so it is timed with the gathers.
+    if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_pick, dim3(1), dim3(kBlock), 0, s, static_cast<const ArgPair*>(c.lm_partials),
+                       lm_head_blocks(m), c.logits, c.state, c.tokens, c.pred, c.capacity, m.embed,
+                       m.hidden, m.vocab, c.x);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return mark(s, timer, QH_ROLE_COUNT);
 }

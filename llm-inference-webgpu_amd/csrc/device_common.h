@@ -222,6 +222,94 @@ __device__ __forceinline__ double chunk_int4(const v4u w, const XV x, float s,
   return acc;
 }
 
+// The same chunk dots for R rows at once, element-major: the R accumulation
+// chains interleave (so a lone wave is not stalled on one chain's f64 latency)
+// and each x element is read once for all rows. Each row's sum still runs over
+// its elements in ascending order, so the results are those of chunk_*.
+template <int R>
+__device__ __forceinline__ void chunk_rows_f16(const v4u (&w)[R], const XV x, double (&acc)[R]) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const double x0 = x[2 * j], x1 = x[2 * j + 1];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = fma((double)f16_lo(w[r][j]), x0, acc[r]);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = fma((double)f16_hi(w[r][j]), x1, acc[r]);
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void chunk_rows_int8(const v4u (&w)[R], const XV x, const float (&s)[R],
+                                                double (&acc)[R]) {
+  bool fast = true;
+#pragma unroll
+  for (int r = 0; r < R; r++) fast = fast && scale_biasable(s[r]);
+  if (fast) {
+    float c[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) c[r] = -128.f * s[r];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t m[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) m[r] = w[r][j] ^ 0x80808080u;  // q + 128 in every byte
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const double xb = x[4 * j + b];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          acc[r] = fma((double)fmaf((float)((m[r] >> (8 * b)) & 0xffu), s[r], c[r]), xb, acc[r]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = chunk_int8(w[r], x, s[r], acc[r]);
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void chunk_rows_int4(const v4u (&w)[R], const XV x, const float (&s)[R],
+                                                const float (&z)[R], double (&acc)[R]) {
+  bool fast = true;
+  int zi[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    zi[r] = (int)z[r];
+    fast = fast && scale_biasable(s[r]) && (float)zi[r] == z[r] && (unsigned)zi[r] <= 15u;
+  }
+  if (fast) {
+    float c[R];
+    uint32_t bias[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      c[r] = -16.f * s[r];
+      bias[r] = (uint32_t)(16 - zi[r]) * 0x01010101u;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t ev[R], od[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        ev[r] = (w[r][j] & 0x0F0F0F0Fu) + bias[r];         // elements 8j, 8j+2, 8j+4, 8j+6
+        od[r] = ((w[r][j] >> 4) & 0x0F0F0F0Fu) + bias[r];  // elements 8j+1, +3, +5, +7
+      }
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        const double xe = x[8 * j + 2 * b], xo = x[8 * j + 2 * b + 1];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          acc[r] = fma((double)fmaf((float)((ev[r] >> (8 * b)) & 0xffu), s[r], c[r]), xe, acc[r]);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+          acc[r] = fma((double)fmaf((float)((od[r] >> (8 * b)) & 0xffu), s[r], c[r]), xo, acc[r]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = chunk_int4(w[r], x, s[r], z[r], acc[r]);
+  }
+}
+
 // ------------------------------------------------------------ matvec core --
 // Where element i of an f64 activation vector sits in a staged copy:
 // chunk-transposed (XT) for a matrix with W = 1 << lw weights per chunk and nc
@@ -280,12 +368,9 @@ __device__ __forceinline__ void mv_team(const DMat& m, const int (&rows)[R], con
     for (int b = 0; b < NB; b++) {
       const XV xc = XT ? XV{xs + (size_t)b * xstride + 2 * c, 2 * m.nchunks}
                        : XV{xs + (size_t)b * xstride + (size_t)c * W, 2};
-#pragma unroll
-      for (int i = 0; i < R; i++) {
-        if constexpr (FMT == QH_FMT_F16) acc[b][i] = chunk_f16(w[i], xc, acc[b][i]);
-        else if constexpr (FMT == QH_FMT_INT8) acc[b][i] = chunk_int8(w[i], xc, srow[i], acc[b][i]);
-        else acc[b][i] = chunk_int4(w[i], xc, s[i], z[i], acc[b][i]);
-      }
+      if constexpr (FMT == QH_FMT_F16) chunk_rows_f16<R>(w, xc, acc[b]);
+      else if constexpr (FMT == QH_FMT_INT8) chunk_rows_int8<R>(w, xc, srow, acc[b]);
+      else chunk_rows_int4<R>(w, xc, s, z, acc[b]);
     }
   }
 #pragma unroll
@@ -343,12 +428,9 @@ __device__ __forceinline__ void wtile_dot(const DMat& m, const WTile<FMT, R, KC>
     const int c = tl + k * TL;
     if (c < m.nchunks) {
       const XV xc{xs + 2 * c, 2 * m.nchunks};
-#pragma unroll
-      for (int i = 0; i < R; i++) {
-        if constexpr (FMT == QH_FMT_F16) acc[i] = chunk_f16(t.w[k][i], xc, acc[i]);
-        else if constexpr (FMT == QH_FMT_INT8) acc[i] = chunk_int8(t.w[k][i], xc, t.s[0][i], acc[i]);
-        else acc[i] = chunk_int4(t.w[k][i], xc, t.s[k][i], t.z[k][i], acc[i]);
-      }
+      if constexpr (FMT == QH_FMT_F16) chunk_rows_f16<R>(t.w[k], xc, acc);
+      else if constexpr (FMT == QH_FMT_INT8) chunk_rows_int8<R>(t.w[k], xc, t.s[0], acc);
+      else chunk_rows_int4<R>(t.w[k], xc, t.s[k], t.z[k], acc);
     }
   }
 #pragma unroll

@@ -470,14 +470,12 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   A((size_t)md.heads * spans * 4, (void**)&d.maxes);
   A(256, (void**)&d.attn_counters);
   A(qh::lm_partials_bytes(md), &d.lm_partials);
-  A(256, (void**)&d.lm_counter);
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
     rc = fail(QH_ERR_NOMEM, "pinned allocation failed");
   }
   if (!rc && (hipMemset(d.kv, 0, kv_bytes) != hipSuccess || hipMemset(d.state, 0, 256) != hipSuccess ||
               hipMemset(d.tokens, 0, (size_t)(capacity + 1) * 4) != hipSuccess ||
               hipMemset(d.pred, 0, (size_t)capacity * 4) != hipSuccess ||
-              hipMemset(d.lm_counter, 0, 256) != hipSuccess ||
               hipMemset(d.attn_counters, 0, 256) != hipSuccess)) {
     rc = fail(QH_ERR_DEVICE, "clearing the cache failed");
   }
@@ -656,7 +654,7 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   if (!c->exec) {
     QH_HIP(hipStreamSynchronize(s));
     QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-    hipError_t e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, true);
+    hipError_t e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(s, &g);
     QH_HIP(e);
@@ -667,6 +665,9 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   c->h_pinned[3] = first_token;
   QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s));
   if ((rc = set_state(c, c->length, c->length + 1))) return rc;
+  // Each replayed step starts from the row its predecessor's pick gathered; the
+  // first starts from this gather.
+  QH_HIP(qh::enqueue_gather(s, m->dev, c->dev));
   for (int i = 0; i < steps; i++) QH_HIP(hipGraphLaunch(c->exec, s));
   c->busy = true;
   c->pending_start = c->length;
@@ -710,7 +711,7 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
   BusyGuard guard(c);
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
-  const int n_ev = qh::launches_per_step(m->dev, qh::STEP_GATHER) + 1;
+  const int n_ev = qh::launches_per_step(m->dev, qh::STEP_CARRIED) + 1;
   std::vector<hipEvent_t> ev(n_ev, nullptr);
   std::vector<int> roles(n_ev, 0);
   for (auto& e : ev) QH_HIP(hipEventCreate(&e));
@@ -719,9 +720,11 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
   c->h_pinned[3] = first_token;
   hipError_t err = hipMemcpyAsync(c->dev.tokens + start, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s);
   if (err == hipSuccess && (rc = set_state(c, start, start + 1))) err = hipErrorUnknown;
+  // The same launches as a decode replay: one gather, then steps that carry their input.
+  if (err == hipSuccess) err = qh::enqueue_gather(s, m->dev, c->dev);
   for (int i = 0; i < steps && err == hipSuccess; i++) {
     qh::StepTimer t{ev.data(), roles.data(), n_ev, 0};
-    err = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, true, &t);
+    err = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true, &t);
     if (err == hipSuccess) err = hipStreamSynchronize(s);
     for (int k = 0; err == hipSuccess && k + 1 < t.n; k++) {
       float ms = 0.f;

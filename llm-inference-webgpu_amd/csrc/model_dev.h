@@ -50,12 +50,13 @@ struct CacheDev {
   int score_stride;    // capacity rounded up to 4
   int* attn_counters;  // [heads], zero between launches
   void* lm_partials;   // argmax block partials
-  int* lm_counter;
   int lm_blocks;
 };
 
-// How a step obtains its input row.
-enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1 };
+// How a step obtains its input row: gathered from the embedding of tokens[pos],
+// written into cache.x by the caller, or carried over from the previous step
+// (whose output head ends by gathering the embedding of the token it chose).
+enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1, STEP_CARRIED = 2 };
 
 // Optional per-launch timing: an event is recorded before every launch (tagged with
 // its QH_ROLE_*) and one after the last, so launch i took events[i+1] - events[i].
@@ -66,12 +67,14 @@ struct StepTimer {
   int n;         // events recorded
 };
 
-// Launches one decode position: [gather] -> layers -> (lm_head + argmax, or a
-// position advance when `logits` is false). With STEP_HIDDEN the caller has
-// already written the input row into cache.x.
+// Launches one decode position: [gather] -> layers -> (lm_head, then the argmax
+// pick that advances the position and gathers the next input row; or a position
+// advance alone when `logits` is false).
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
                         bool logits, StepTimer* timer = nullptr);
-// Launches in one step (the events a StepTimer needs, minus the final one).
+// cache.x = the embedding of tokens[position] (what STEP_GATHER starts with).
+hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c);
+// Launches in one step with logits (the events a StepTimer needs, minus the final one).
 int launches_per_step(const ModelDev& m, StepInput in);
 // Blocks the lm_head launch uses (sizes lm_partials).
 int lm_head_blocks(const ModelDev& m);

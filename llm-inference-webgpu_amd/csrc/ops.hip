@@ -339,7 +339,11 @@ hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t*
   a.vstride = value_stride(capacity);
   a.heads = heads;
   a.kv_heads = kv_heads;
-  hipLaunchKernelGGL(k_attn_exact, dim3(a.max_stride, heads, seq), dim3(kBlock), 0, s, a);
+  if (total <= kPLds) {
+    hipLaunchKernelGGL(k_attn_block, dim3(heads, seq), dim3(kAttnThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(k_attn_exact, dim3(a.max_stride, heads, seq), dim3(kBlock), 0, s, a);
+  }
   return hipGetLastError();
 }
 
