@@ -137,6 +137,9 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--isolated", choices=["all", "none"], default="all")
+    ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
+                    help="decode by hipGraph replay (default) or direct launches of the same "
+                         "kernels (for profilers that do not follow graph launches)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -159,6 +162,7 @@ def main():
 
     prompt = H.synth_tokens(args.seed, "config4.prompt", cfg.vocab, args.context)
     cache = model.newCache(capacity)
+    model.decode_use_graph(cache, args.launch == "graph")
     t0 = time.perf_counter()
     first = model.forward_tokens(prompt, cache)["argmax"]
     prefill_s = time.perf_counter() - t0

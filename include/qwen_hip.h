@@ -239,6 +239,11 @@ int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int3
 /* Enqueue the graph replays without waiting (for timing); qh_decode_collect waits and copies. */
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps);
 int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens);
+/* use_graph = 0: later decodes on this cache enqueue every kernel of a step directly instead
+ * of replaying the captured graph (same kernels, same tokens), for tools that cannot follow
+ * graph launches. No counterpart in the reference, which re-encodes every step
+ * (src/gpu/model.js:261). Default 1. */
+int qh_decode_use_graph(qh_cache* c, int32_t use_graph);
 
 /* Kernel roles of one decode step, the grouping of the reference's in-situ profile
  * ("GPU ms per token by role", web/decode-profile.html:88-192). */

@@ -107,6 +107,7 @@ struct qh_cache {
   std::vector<void*> allocs;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  bool use_graph = true;  // false: decode enqueues every kernel directly
   bool busy = false;
   int pending_start = 0, pending_steps = 0;
   float* d_hidden = nullptr;
@@ -651,7 +652,7 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   if (rc) return rc;
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
-  if (!c->exec) {
+  if (c->use_graph && !c->exec) {
     QH_HIP(hipStreamSynchronize(s));
     QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
     hipError_t e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
@@ -668,11 +669,21 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   // Each replayed step starts from the row its predecessor's pick gathered; the
   // first starts from this gather.
   QH_HIP(qh::enqueue_gather(s, m->dev, c->dev));
-  for (int i = 0; i < steps; i++) QH_HIP(hipGraphLaunch(c->exec, s));
+  for (int i = 0; i < steps; i++) {
+    if (c->use_graph) QH_HIP(hipGraphLaunch(c->exec, s));
+    else QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true));
+  }
   c->busy = true;
   c->pending_start = c->length;
   c->pending_steps = steps;
   c->length += steps;
+  return QH_OK;
+}
+
+int qh_decode_use_graph(qh_cache* c, int32_t use_graph) {
+  QH_CHECK(c, QH_ERR_INVALID, "decode_use_graph needs a cache");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  c->use_graph = use_graph != 0;
   return QH_OK;
 }
 

@@ -151,7 +151,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_cache_set_length": [vp, i32], "qh_cache_present": [vp, i32, vp, vp],
         "qh_forward": [vp, vp, vp, i32, vp, vp], "qh_forward_tokens": [vp, vp, vp, i32, vp, vp],
         "qh_decode": [vp, vp, i32, i32, vp], "qh_decode_launch": [vp, vp, i32, i32],
-        "qh_decode_collect": [vp, vp, i32, vp],
+        "qh_decode_collect": [vp, vp, i32, vp], "qh_decode_use_graph": [vp, i32],
         "qh_decode_profile": [vp, vp, i32, i32, vp, vp, vp],
     }
     for name, args in sigs.items():
@@ -547,6 +547,11 @@ class GpuModel:
         out = np.empty(steps, np.int32)
         _check(self.lib.qh_decode(self.handle, cache.handle, first_token, steps, _ptr(out)))
         return out
+
+    def decode_use_graph(self, cache: GpuKVCache, use_graph: bool) -> None:
+        """False: later decodes on `cache` launch each kernel directly (same kernels and
+        tokens) instead of replaying the captured graph."""
+        _check(self.lib.qh_decode_use_graph(cache.handle, int(bool(use_graph))))
 
     def decode_launch(self, cache: GpuKVCache, first_token: int, steps: int) -> None:
         _check(self.lib.qh_decode_launch(self.handle, cache.handle, first_token, steps))
