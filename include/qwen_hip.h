@@ -197,6 +197,18 @@ typedef struct qh_model qh_model;
 typedef struct qh_cache qh_cache;
 
 int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out);
+
+/* Arithmetic of the model's forward/decode kernels.
+ *   QH_NUMERICS_FAST (default): split-K online-softmax attention in f32 (one pass over the f16
+ *     cache, slots merged in the o-projection's staging); matvecs as in EXACT. Logits agree
+ *     with the CPU path (src/cpu/model.js:55-166) to f32 rounding (~1e-6 relative).
+ *   QH_NUMERICS_EXACT: every kernel evaluates the CPU path's arithmetic in its order (f64
+ *     accumulation stored to f32, attention by the global max with a sequential f32 PV sum),
+ *     so logits and the f16 cache are the oracle's bit for bit up to f64 ordering noise.
+ * Set before the model's first cache is created. No counterpart in the reference, whose GPU
+ * path has one f32 arithmetic (src/gpu/kernels.js). */
+enum { QH_NUMERICS_FAST = 0, QH_NUMERICS_EXACT = 1 };
+int qh_model_set_numerics(qh_model* m, int32_t numerics);
 /* Upload one tensor by its checkpoint name (src/core/config.js:88-119), copied from host.
  *   model.embed_tokens.weight  QH_FMT_BF16 [vocab, hidden]: the input gather table
  *   lm_head.weight             F16 | INT8 | INT4 [vocab, hidden]: the output projection (for a

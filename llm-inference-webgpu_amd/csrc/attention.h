@@ -11,8 +11,8 @@
 //
 // Two algorithms:
 //
-// Exact order (k_attn_block up to kPLds positions, k_attn_exact beyond), what
-// the model path uses. It evaluates groupedAttention (src/core/attention.js:
+// Exact order (k_attn_block up to kPLds positions, k_attn_exact beyond), the
+// model's QH_NUMERICS_EXACT path. It evaluates groupedAttention (src/core/attention.js:
 // 32-66) step for step: each score is a sequential f64 dot stored to f32, the
 // softmax shifts by the global max and normalizes with an f64 sum
 // (src/core/ops.js:66-78), and the output accumulates sequentially over
@@ -23,11 +23,10 @@
 // result matches the CPU to the bit apart from f64-order noise, so a device f16
 // cache and the CPU's same-f16 cache stay identical.
 //
-// Split-K online softmax (k_attention_splitk), for long contexts: one block
-// per (query, kv head, split of chunks) stages K/V once for all the query heads
-// that share it and keeps scores in LDS; the last split to finish combines.
-// Exact to f32 rounding, not to the CPU's order; checked within the kernel
-// tolerance.
+// Split-K online softmax (k_attn_slots + a combine), the decode step's path
+// (QH_NUMERICS_FAST) and qh_attention_splitk: one wave per (query, head, run of
+// 64-position chunks), partials merged afterwards. Exact to f32 rounding, not to
+// the CPU's order; checked within the kernel tolerance.
 #pragma once
 
 #include "device_common.h"
@@ -35,14 +34,9 @@
 namespace qh {
 
 constexpr int kChunk = 64;        // split-K: positions per chunk
-constexpr int kMaxSplits = 128;   // split-K: splits per (query, kv head)
 constexpr int kHeadDim = 64;
-constexpr int kMaxGroup = 8;      // query heads per kv head
-constexpr int kPartialStride = kHeadDim + 2;  // split-K partial: m, l, acc[64]
 constexpr int kPLds = 4096;       // exact: probabilities kept in LDS up to this context
 static_assert(kSpan == kBlock, "exact attention scores one position per thread");
-
-__host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
 
 // ------------------------------------------------------------ exact order --
 
@@ -375,180 +369,248 @@ static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
 }
 
 // -------------------------------------------------------------- split-K --
+// Split-K online softmax (the decode path's attention, and qh_attention_splitk).
+// The context is cut into 64-position chunks; a "slot" is every S-th chunk, and
+// one wave owns one (query, head, slot): lane p scores position p of
+// a chunk against the head's query (q as wave-uniform scalars, keys as f16 via
+// v_fma_mix), the wave keeps the running max m and sum l over its slot, and lane
+// d accumulates output dimension d over the chunk's positions with the chunk's
+// probabilities read lane by lane. The slot's partial (m, l, o[64]) goes to
+// `part`; a combine (k_attn_combine, or the decode o-projection's staging)
+// merges the slots of a head:
+//   M = max_s m_s,  L = sum_s l_s e^(m_s - M),  out = sum_s o_s e^(m_s - M) / L.
+// f32 throughout; agrees with groupedAttention (src/core/attention.js:32-66) to
+// f32 rounding. The chunks of a slot depend on the query's own context only, so
+// a prefill row and the same position decoded alone give the same bits.
+constexpr int kPartStride = 68;   // floats per slot partial: m, l, 2 pad, o[64]
+constexpr int kDecodeSlots = 16;  // slots per head in the decode step (combined in staging)
+constexpr int kOpSlots = 64;      // slots per head in the standalone operator
 
-struct SplitArgs {
+__host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
+
+// Slot s of a query owns chunks s, s + S, s + 2S, ... below attn_chunks(ctx)
+// (S slots per query head); a slot with no chunk writes the neutral partial
+// (m = -inf, l = 0, o = 0). The first chunk a slot reads does not depend on the
+// context, so its loads start before the position arrives from the device.
+__host__ __device__ inline int slots_used(int ctx, int max_slots) {
+  const int n = attn_chunks(ctx);
+  return n < max_slots ? n : max_slots;
+}
+
+struct SlotArgs {
   const float* q;        // [seq][heads*64], rotated
   const uint16_t* kc;    // [kv_heads][capacity][64] f16
   const uint16_t* vt;    // [kv_heads][64][vstride] f16
-  float* partials;       // [seq][kv_heads][s_grid][group][66]
-  int* counters;         // [seq][kv_heads], zero between launches
-  float* out;            // [seq][heads*64]
-  int past, seq, capacity, vstride, heads, kv_heads, s_grid;
+  const int* d_pos;      // when set, past is read from the device (decode)
+  float* part;           // [seq][heads][max_slots][kPartStride]
+  int past, capacity, vstride, heads, kv_heads, max_slots;
 };
 
-__host__ __device__ inline void attn_splits(int ctx, int* nchunks, int* cps, int* splits) {
-  const int n = attn_chunks(ctx);
-  const int s = n < kMaxSplits ? n : kMaxSplits;
-  const int c = (n + s - 1) / s;
-  *nchunks = n;
-  *cps = c;
-  *splits = (n + c - 1) / c;
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, dpp32<CTRL>(v));
+}
+// Max over a team of TL lanes (16 or 64); every lane ends with the same value.
+template <int TL>
+__device__ __forceinline__ float team_max(float v) {
+  v = dpp_max<kDppQuadXor1>(v);
+  v = dpp_max<kDppQuadXor2>(v);
+  v = dpp_max<kDppHalfMirror>(v);
+  v = dpp_max<kDppMirror>(v);
+  if constexpr (TL >= 32) v = fmaxf(v, swz_xor16(v));
+  if constexpr (TL >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
 }
 
-// Grid width that covers every query with context <= max_ctx. The split count
-// is not monotone in ctx past kMaxSplits chunks (129 chunks need 65 splits, 128
-// need 128), so the bound is min(chunks, kMaxSplits), not splits(max_ctx).
-__host__ __device__ inline int attn_grid_splits(int max_ctx) {
-  const int n = attn_chunks(max_ctx);
-  return n < kMaxSplits ? n : kMaxSplits;
+// Loads chunk `c`: key row p0+lane and, for lane d, values of dimension d at
+// positions p0 .. p0+63 as eight 16-byte groups. Every load is unconditional and
+// in bounds -- rows past `lim` (the cache capacity) read row lim-1, groups past
+// it the group holding lim-1 (vstride >= lim rounded up to 8) -- so no load waits
+// on a branch; the caller masks what lies past the context.
+__device__ __forceinline__ void slot_load(const uint16_t* kb, const uint16_t* vrow, int c, int lim,
+                                          int lane, v4u (&kr)[8], v4u (&vr)[8]) {
+  const int p0 = c * kChunk;
+  const int p = min(p0 + lane, lim - 1);
+  const v4u* kp = reinterpret_cast<const v4u*>(kb + (size_t)p * kHeadDim);
+#pragma unroll
+  for (int j = 0; j < 8; j++) kr[j] = kp[j];
+  const int last = (lim - 1) & ~7;
+#pragma unroll
+  for (int j = 0; j < 8; j++) vr[j] = *reinterpret_cast<const v4u*>(vrow + min(p0 + 8 * j, last));
 }
 
-[[maybe_unused]] static __global__ __launch_bounds__(kBlock) void k_attention_splitk(SplitArgs a) {
-  const int split = blockIdx.x;
-  const int g = blockIdx.y;
-  const int t = blockIdx.z;
-  const int pos = a.past + t;
+// One chunk of positions p0 .. p0+63 of a slot: scores (lane = position), the
+// online-softmax update of (m, l, o), and o += p * v over the chunk (lane =
+// output dimension, probabilities broadcast through the wave's LDS row `eb`).
+__device__ __forceinline__ void slot_chunk(const v4f (&q4)[kHeadDim / 4], const v4u (&kr)[8], v4u (&vr)[8],
+                                           int p0, int ctx, int lane, float* eb, float& m, float& l,
+                                           float& o) {
+  float dot = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t u[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      dot = fmaf(q4[2 * j + e / 2][2 * (e % 2)], f16_lo(u[e]), dot);
+      dot = fmaf(q4[2 * j + e / 2][2 * (e % 2) + 1], f16_hi(u[e]), dot);
+    }
+  }
+  const bool valid = p0 + lane < ctx;
+  const float sc = valid ? dot * 0.125f : -INFINITY;  // scale 1/sqrt(64)
+  const float mn = fmaxf(m, team_max<64>(sc));
+  const float ex = valid ? expf(sc - mn) : 0.f;
+  const float alpha = expf(m - mn);  // 0 on the first chunk (m = -inf)
+  l = l * alpha + team_sum<64>(ex);
+  o *= alpha;
+  if (ctx - p0 < kChunk) {
+    // tail chunk: values past the context are not this chunk's (their weight is 0)
+    const int n = ctx - p0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int q0 = 8 * j + 2 * e;
+        uint32_t w = vr[j][e];
+        if (q0 >= n) w = 0;
+        else if (q0 + 1 >= n) w &= 0xffffu;
+        vr[j][e] = w;
+      }
+    }
+  }
+  // LDS operations of one wave complete in order: no block barrier is needed.
+  eb[lane] = ex;
+  __builtin_amdgcn_wave_barrier();
+  const v4f* e4 = reinterpret_cast<const v4f*>(eb);
+#pragma unroll
+  for (int j = 0; j < 8; j++) o = pv8(e4[2 * j], e4[2 * j + 1], vr[j], o);
+  __builtin_amdgcn_wave_barrier();
+  m = mn;
+}
+
+template <int MAXS>
+static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
+  __shared__ __attribute__((aligned(16))) float ebuf[kBlock / kWave][kChunk];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int item = blockIdx.x * (kBlock / kWave) + wave;
+  const int t = blockIdx.y;
+  const int h = item / MAXS, sl = item % MAXS;
+  if (h >= a.heads) return;
+  const int g = h / (a.heads / a.kv_heads);
+
+  // Everything that does not depend on the position first: the head's query in
+  // VGPRs (a per-lane address keeps the compiler from holding 64 values in scalar
+  // registers) and the slot's first chunk.
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  const v4f* qp = reinterpret_cast<const v4f*>(a.q + ((size_t)t * a.heads + h) * kHeadDim + zero);
+  v4f q4[kHeadDim / 4];
+#pragma unroll
+  for (int i = 0; i < kHeadDim / 4; i++) q4[i] = qp[i];
+  const uint16_t* kb = a.kc + (size_t)g * a.capacity * kHeadDim;
+  const uint16_t* vrow = a.vt + ((size_t)g * kHeadDim + lane) * a.vstride;
+  v4u ka[8], va[8], kb2[8], vb2[8];
+  slot_load(kb, vrow, sl, a.capacity, lane, ka, va);
+
+  const int past = a.d_pos ? *a.d_pos : a.past;
+  const int pos = past + t;
+  if (pos >= a.capacity) return;  // the host keeps positions inside the cache
   const int ctx = pos + 1;
-  int nchunks, cps, nsplit;
-  attn_splits(ctx, &nchunks, &cps, &nsplit);
-  if (split >= nsplit || nsplit > a.s_grid) return;
-  const int c0 = split * cps;
-  const int c1 = min(c0 + cps, nchunks);
-  const int group = a.heads / a.kv_heads;
-  const int tid = threadIdx.x;
-
-  __shared__ float qs[kMaxGroup][kHeadDim];
-  __shared__ __attribute__((aligned(16))) _Float16 ks[kChunk][kHeadDim + 2];
-  __shared__ _Float16 vs[kChunk][kHeadDim + 2];
-  __shared__ float sc[kMaxGroup][kChunk];
-  __shared__ float mst[kMaxGroup], lst[kMaxGroup], alpha[kMaxGroup];
-  __shared__ int is_last;
-
-  const size_t qrow = (size_t)t * a.heads * kHeadDim;
-  for (int idx = tid; idx < group * kHeadDim; idx += kBlock) {
-    qs[idx / kHeadDim][idx % kHeadDim] = a.q[qrow + (size_t)g * group * kHeadDim + idx];
+  const int nch = attn_chunks(ctx);
+  float* eb = ebuf[wave];
+  float m = -INFINITY, l = 0.f, o = 0.f;
+  // Chunks alternate between two named buffers, so the next chunk's loads stay in
+  // flight while this one is summed (no register copies wait on them). The
+  // prefetch is unconditional (past the slot it re-reads an in-bounds chunk),
+  // which keeps the outstanding-load count the same on every path.
+  for (int c = sl; c < nch; c += 2 * MAXS) {
+    slot_load(kb, vrow, min(c + MAXS, nch - 1), a.capacity, lane, kb2, vb2);
+    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this chunk's arithmetic
+    slot_chunk(q4, ka, va, c * kChunk, ctx, lane, eb, m, l, o);
+    if (c + MAXS >= nch) break;
+    slot_load(kb, vrow, min(c + 2 * MAXS, nch - 1), a.capacity, lane, ka, va);
+    __builtin_amdgcn_sched_barrier(0);
+    slot_chunk(q4, kb2, vb2, (c + MAXS) * kChunk, ctx, lane, eb, m, l, o);
   }
-  if (tid < kMaxGroup) {
-    mst[tid] = -INFINITY;
-    lst[tid] = 0.f;
+  float* dst = a.part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
+  dst[4 + lane] = o;
+  if (lane == 0) {
+    dst[0] = m;
+    dst[1] = l;
   }
-  float acc0 = 0.f, acc1 = 0.f;  // outputs tid and tid + 256 of [group][64]
-  const int o0 = tid, o1 = tid + kBlock;
-  __syncthreads();
+}
 
-  const uint16_t* kbase = a.kc + (size_t)g * a.capacity * kHeadDim;
-  const uint16_t* vbase = a.vt + (size_t)g * kHeadDim * a.vstride;
-  for (int c = c0; c < c1; c++) {
-    const int p0 = c * kChunk;
-    const int n = min(kChunk, ctx - p0);
-    for (int e = tid; e < kChunk * 8; e += kBlock) {
-      // keys: position p, 16-byte part; values: dimension d, 8 positions from p8
-      const int p = e >> 3, part = e & 7;
-      v4u kv4 = {0, 0, 0, 0}, vv4 = {0, 0, 0, 0};
-      if (p < n) kv4 = reinterpret_cast<const v4u*>(kbase + (size_t)(p0 + p) * kHeadDim)[part];
-      const int d = e >> 3, p8 = (e & 7) * 8;
-      if (p8 < n) vv4 = *reinterpret_cast<const v4u*>(vbase + (size_t)d * a.vstride + p0 + p8);
+// out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t).
+[[maybe_unused]] static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __restrict__ part,
+                                                               float* __restrict__ out, int past,
+                                                               int heads, int max_slots) {
+  const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const int nslots = slots_used(past + t + 1, max_slots);
+  const float* p = part + ((size_t)t * heads + h) * max_slots * kPartStride;
+  float M = -INFINITY;
+  for (int s = 0; s < nslots; s++) M = fmaxf(M, p[(size_t)s * kPartStride]);
+  float L = 0.f, A = 0.f;
+  for (int s = 0; s < nslots; s++) {
+    const float w = expf(p[(size_t)s * kPartStride] - M);
+    L = fmaf(w, p[(size_t)s * kPartStride + 1], L);
+    A = fmaf(w, p[(size_t)s * kPartStride + 4 + d], A);
+  }
+  out[((size_t)t * heads + h) * kHeadDim + d] = A / L;
+}
+
+// The decode step's combine, run by the o-projection while it stages its input:
+// xs[lay.pos(i)] = attention output i (i = h*64 + d) as f64, for a single query
+// whose slot partials (kDecodeSlots = 16 per head, empty ones neutral) are at
+// `part`. Thread i < heads*16 owns head h = i/16: it reads the (m, l) of slot
+// i%16 and the four output dimensions 4*(i%16) .. +3 of every slot; the 16 lanes
+// of a head form one DPP team, so M, L and the slot weights e^(m_s - M) / L stay
+// inside it (shared through the wave's own LDS slice). Nothing here depends on
+// the position. heads <= 16. Loads (CombineIn::load) and arithmetic are split as
+// for StageIn.
+struct CombineIn {
+  v4f ov[kDecodeSlots];
+  float mv, lv;
+  __device__ __forceinline__ void load(const float* __restrict__ part, int heads) {
+    static_assert(kDecodeSlots == 16, "one 16-lane team per head");
+    const int i = threadIdx.x;
+    const int h = min(i / kDecodeSlots, heads - 1), k = i % kDecodeSlots;
+    const float* ph = part + (size_t)h * kDecodeSlots * kPartStride;
 #pragma unroll
-      for (int k = 0; k < 4; k++) *reinterpret_cast<uint32_t*>(&ks[p][part * 8 + 2 * k]) = kv4[k];
-      const uint32_t vu[4] = {vv4.x, vv4.y, vv4.z, vv4.w};
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const uint16_t bits = (uint16_t)(vu[k >> 1] >> (16 * (k & 1)));
-        // positions past the context hold no value yet: stage zeros, as their weights are
-        vs[p8 + k][d] = p8 + k < n ? __builtin_bit_cast(_Float16, bits) : (_Float16)0.f;
-      }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < group * kChunk; idx += kBlock) {
-      const int h = idx / kChunk, p = idx % kChunk;
-      float s = -INFINITY;
-      if (p < n) {
-        float d = 0.f;
-#pragma unroll 8
-        for (int j = 0; j < kHeadDim; j += 2) {
-          const uint32_t kk = *reinterpret_cast<const uint32_t*>(&ks[p][j]);
-          d = fmaf(qs[h][j], f16_lo(kk), d);
-          d = fmaf(qs[h][j + 1], f16_hi(kk), d);
-        }
-        s = d * 0.125f;
-      }
-      sc[h][p] = s;
-    }
-    __syncthreads();
-    {
-      const int wave = tid / kWave, lane = tid & (kWave - 1);
-      for (int h = wave; h < group; h += kBlock / kWave) {
-        const float v = sc[h][lane];
-        const float m_old = mst[h];
-        const float m_new = fmaxf(m_old, wave_max(v));
-        const float e = lane < n ? expf(v - m_new) : 0.f;
-        const float sum = team_sum<64>(e);
-        sc[h][lane] = e;
-        if (lane == 0) {
-          const float al = expf(m_old - m_new);
-          alpha[h] = al;
-          lst[h] = lst[h] * al + sum;
-          mst[h] = m_new;
-        }
-      }
-    }
-    __syncthreads();
-    if (o0 < group * kHeadDim) {
-      const int h = o0 / kHeadDim, d = o0 % kHeadDim;
-      float s = acc0 * alpha[h];
-      for (int p = 0; p < n; p++) s = fmaf(sc[h][p], (float)vs[p][d], s);
-      acc0 = s;
-    }
-    if (o1 < group * kHeadDim) {
-      const int h = o1 / kHeadDim, d = o1 % kHeadDim;
-      float s = acc1 * alpha[h];
-      for (int p = 0; p < n; p++) s = fmaf(sc[h][p], (float)vs[p][d], s);
-      acc1 = s;
-    }
-    __syncthreads();
+    for (int s = 0; s < kDecodeSlots; s++)
+      ov[s] = *reinterpret_cast<const v4f*>(ph + (size_t)s * kPartStride + 4 + 4 * k);
+    mv = ph[(size_t)k * kPartStride];
+    lv = ph[(size_t)k * kPartStride + 1];
   }
+};
 
-  float* pbase = a.partials + (((size_t)t * a.kv_heads + g) * a.s_grid) * group * kPartialStride;
-  {
-    float* mine = pbase + (size_t)split * group * kPartialStride;
-    if (o0 < group * kHeadDim) {
-      const int h = o0 / kHeadDim, d = o0 % kHeadDim;
-      mine[h * kPartialStride + 2 + d] = acc0;
-      if (d == 0) {
-        mine[h * kPartialStride] = mst[h];
-        mine[h * kPartialStride + 1] = lst[h];
-      }
-    }
-    if (o1 < group * kHeadDim) {
-      const int h = o1 / kHeadDim, d = o1 % kHeadDim;
-      mine[h * kPartialStride + 2 + d] = acc1;
-      if (d == 0) {
-        mine[h * kPartialStride] = mst[h];
-        mine[h * kPartialStride + 1] = lst[h];
-      }
-    }
+// `wl` is LDS of kBlock floats.
+__device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int heads, double* xs, XLayout lay,
+                                                   float* wl) {
+  const int i = threadIdx.x;
+  const int h = min(i / kDecodeSlots, heads - 1), k = i % kDecodeSlots;
+  const float M = team_max<16>(in.mv);     // slot 0 always holds position 0
+  const float w = expf(in.mv - M);         // 0 for an empty slot (m = -inf)
+  const float L = team_sum<16>(w * in.lv);
+  wl[i] = w / L;
+  __builtin_amdgcn_wave_barrier();
+  const float* wh = wl + (i & ~(kDecodeSlots - 1));
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kDecodeSlots; s++) {
+    const float ws = wh[s];
+    acc.x = fmaf(ws, in.ov[s].x, acc.x);
+    acc.y = fmaf(ws, in.ov[s].y, acc.y);
+    acc.z = fmaf(ws, in.ov[s].z, acc.z);
+    acc.w = fmaf(ws, in.ov[s].w, acc.w);
   }
-  __threadfence();
-  __syncthreads();
-  int* counter = a.counters + (size_t)t * a.kv_heads + g;
-  if (tid == 0) is_last = atomicAdd(counter, 1) == nsplit - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  for (int idx = tid; idx < group * kHeadDim; idx += kBlock) {
-    const int h = idx / kHeadDim, d = idx % kHeadDim;
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, pbase[((size_t)s * group + h) * kPartialStride]);
-    float L = 0.f, A = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-      const float* ps = pbase + ((size_t)s * group + h) * kPartialStride;
-      const float w = expf(ps[0] - M);
-      L = fmaf(w, ps[1], L);
-      A = fmaf(w, ps[2 + d], A);
-    }
-    a.out[qrow + (size_t)(g * group + h) * kHeadDim + d] = A / L;
+  if (i < heads * kDecodeSlots) {
+    const int j = h * kHeadDim + 4 * k;
+    xs[lay.pos(j)] = (double)acc.x;
+    xs[lay.pos(j + 1)] = (double)acc.y;
+    xs[lay.pos(j + 2)] = (double)acc.z;
+    xs[lay.pos(j + 3)] = (double)acc.w;
   }
-  if (tid == 0) *counter = 0;
+  __syncthreads();
 }
 
 }  // namespace qh

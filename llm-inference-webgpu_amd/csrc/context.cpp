@@ -351,31 +351,19 @@ int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cac
   int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
                            kv_heads, head_dim);
   if (rc) return rc;
-  const size_t pf = qh::attention_partials_floats(seq, heads, kv_heads, past + seq);
-  const size_t need = pf * sizeof(float) + (size_t)seq * kv_heads * sizeof(int) + 256;
-  void* parts = nullptr;
-  int* counters = nullptr;
-  // Counters live in the context scratch's counter region (after the argmax counter), which
-  // only ever holds zeroed counters; partials in the region after it.
-  const size_t n_counters = (size_t)seq * kv_heads;
-  const size_t part_room = ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64;
-  if ((n_counters + 16) * sizeof(int) <= qh_ctx::kScratchCounterBytes && pf * sizeof(float) <= part_room) {
-    counters = static_cast<int*>(ctx->d_scratch) + 16;
-    parts = static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes;
-    QH_HIP(qh::launch_attention_splitk(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
-                                       d_out, seq, past, heads, kv_heads,
-                                       static_cast<float*>(parts), counters));
+  const size_t bytes = qh::attention_partials_floats(seq, heads) * sizeof(float);
+  // Partials in the context scratch after its counter region; larger prefill shapes get a
+  // temporary buffer.
+  if (bytes <= ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64) {
+    float* parts = reinterpret_cast<float*>(static_cast<char*>(ctx->d_scratch) + qh_ctx::kScratchCounterBytes);
+    QH_HIP(qh::launch_attention_splitk(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out,
+                                       seq, past, heads, kv_heads, parts));
     return QH_OK;
   }
-  // Larger prefill shapes get a temporary buffer.
   void* tmp = nullptr;
-  QH_HIP(hipMallocAsync(&tmp, need, ctx->stream));
-  QH_HIP(hipMemsetAsync(tmp, 0, 256 + (size_t)seq * kv_heads * sizeof(int), ctx->stream));
-  counters = static_cast<int*>(tmp);
-  parts = static_cast<char*>(tmp) + (((size_t)seq * kv_heads * sizeof(int) + 255) & ~(size_t)255);
+  QH_HIP(hipMallocAsync(&tmp, bytes, ctx->stream));
   hipError_t e = qh::launch_attention_splitk(ctx->stream, d_q, d_key_cache, d_value_cache, capacity,
-                                             d_out, seq, past, heads, kv_heads,
-                                             static_cast<float*>(parts), counters);
+                                             d_out, seq, past, heads, kv_heads, static_cast<float*>(tmp));
   QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
   return QH_OK;

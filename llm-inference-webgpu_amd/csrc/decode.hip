@@ -6,8 +6,10 @@
 //
 // Per layer (the order of src/cpu/model.js:89-143):
 //   1. rmsnorm(x) -> q|k|v matvec + bias -> rope (f64) -> q, f16 K/V append
-//   2. attention per head (scores as f64 dots, softmax, sequential PV sum)
-//   3. o-proj matvec, residual add into x
+//   2. attention: QH_NUMERICS_FAST, split-K slot partials (one wave per head and
+//      run of 64 positions); QH_NUMERICS_EXACT, per head in the CPU's order
+//      (f64 dots, global-max softmax, sequential PV sum)
+//   3. [FAST: merge the attention slots while staging] o-proj matvec, residual add into x
 //   4. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
 //   5. down matvec, residual add into x
 // then rmsnorm -> lm_head -> logits and per-block argmax partials, and the pick,
@@ -20,13 +22,15 @@
 // (WTile) before the block stages its activation vector, and a team with more
 // than one work item loads the next item's weights before the current item's
 // arithmetic.
+#include <type_traits>
+
 #include "attention.h"
 #include "device_common.h"
 #include "model_dev.h"
 
 namespace qh {
 
-enum { PRO_RMSNORM = 0, PRO_COPY = 1 };
+enum { PRO_RMSNORM = 0, PRO_COPY = 1, PRO_COMBINE = 2 };
 enum { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 struct FusedArgs {
@@ -49,6 +53,7 @@ struct FusedArgs {
   int capacity;
   // EPI_LOGITS
   ArgPair* partials;     // [blocks]: each block's best (value, index)
+  // PRO_COMBINE: `in` holds the attention slot partials of the current position
 };
 
 // Rows of work item `it`. QKV: a rope pair (j, j+32) of a q or k head, or two
@@ -76,21 +81,48 @@ __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows
   }
 }
 
+// Operands of an item's epilogue that do not depend on its sums, loaded with its
+// weights: QKV the two rows' biases and the rope angle of the pair at the current
+// position; RESIDUAL the rows' residual inputs.
+template <int EPI, int R>
+struct EpiIn {
+  float bias[2];
+  double cs, sn;
+  float res[R];
+};
+
+template <int EPI, int R>
+__device__ __forceinline__ void epi_load(const FusedArgs& a, int it, int pos, const int (&rows)[R],
+                                         EpiIn<EPI, R>& e) {
+  if constexpr (EPI == EPI_QKV) {
+    e.bias[0] = a.bias[rows[0]];
+    e.bias[1] = a.bias[rows[1]];
+    const int j = it & 31;  // the rope pair of a q/k item (unused by v items)
+    e.cs = a.rope_cos[(size_t)pos * 32 + j];
+    e.sn = a.rope_sin[(size_t)pos * 32 + j];
+  }
+  if constexpr (EPI == EPI_RESIDUAL) {
+#pragma unroll
+    for (int i = 0; i < R; i++) e.res[i] = a.out[rows[i]];
+  }
+}
+
 // Lane 0 of the team that summed item `it` (acc = the R row sums) stores it.
 template <int R, int EPI>
 __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, const int (&rows)[R],
-                                         const double (&acc)[R], float& bv, int& bi) {
+                                         const double (&acc)[R], const EpiIn<EPI, R>& e, float& bv,
+                                         int& bi) {
   if constexpr (EPI == EPI_QKV) {
     // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts).
-    const float v0 = (float)(acc[0] + (double)a.bias[rows[0]]);
-    const float v1 = (float)(acc[1] + (double)a.bias[rows[1]]);
+    const float v0 = (float)(acc[0] + (double)e.bias[0]);
+    const float v1 = (float)(acc[1] + (double)e.bias[1]);
     const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
     const int rope_pairs = (a.heads + a.kv_heads) * 32;
     if (pos >= a.capacity) return;  // the host keeps positions inside the cache
     if (it < rope_pairs) {
       const int head = it / 32, j = it % 32;
       float lo, hi;
-      rope_pair(v0, v1, a.rope_cos[(size_t)pos * 32 + j], a.rope_sin[(size_t)pos * 32 + j], &lo, &hi);
+      rope_pair(v0, v1, e.cs, e.sn, &lo, &hi);
       if (head < a.heads) {
         a.out[head * kHeadDim + j] = lo;
         a.out[head * kHeadDim + j + 32] = hi;
@@ -102,8 +134,8 @@ __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, co
     } else {
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        const int e = rows[i] - hidden - kvd;  // kv head e/64, dimension e%64
-        a.vt[(size_t)e * a.vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
+        const int el = rows[i] - hidden - kvd;  // kv head el/64, dimension el%64
+        a.vt[(size_t)el * a.vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
       }
     }
   }
@@ -111,7 +143,7 @@ __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, co
 #pragma unroll
     for (int i = 0; i < R; i++) {
       const int r = it * R + i;
-      if (r < a.w.rows) a.out[r] = a.out[r] + (float)acc[i];
+      if (r < a.w.rows) a.out[r] = e.res[i] + (float)acc[i];
     }
   }
   if constexpr (EPI == EPI_SWIGLU) {
@@ -141,47 +173,75 @@ __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, co
   }
 }
 
-template <int FMT, int TL, int R, int KC, int PRO, int EPI>
+// One work item's loads (rows, weights, epilogue operands) for item min(it, last):
+// past the end a team re-reads the last item, unconditionally, so no load waits
+// on a branch.
+template <int FMT, int TL, int R, int KC, int EPI>
+struct Item {
+  int rows[R];
+  WTile<FMT, R, KC> w;
+  EpiIn<EPI, R> e;
+  __device__ __forceinline__ void load(const FusedArgs& a, int it, int pos, int lane) {
+    const int i = min(it, a.items - 1);
+    item_rows<EPI, R>(a, i, rows);
+    wtile_load<FMT, R, KC, TL>(a.w, rows, lane, w);
+    epi_load<EPI, R>(a, i, pos, rows, e);
+  }
+};
+
+// LOOP: a team has several items (the output head): two named item buffers
+// alternate, so the next item's loads are in flight during this one's arithmetic
+// without register copies that would wait on them.
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool LOOP>
 __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   __shared__ ArgPair tbest[kBlock / TL];
+  __shared__ float wl[PRO == PRO_COMBINE ? kBlock : 1];
   double* xs = smem;
   using T = Teams<TL>;
   const int lane = T::lane();
   const int stride = gridDim.x * T::kTeams;
   int it = blockIdx.x * T::kTeams + T::team();
-
-  // This team's first item: weight loads in flight before the staging below.
-  int rows[R];
-  WTile<FMT, R, KC> cur;
-  if (it < a.items) {
-    item_rows<EPI, R>(a, it, rows);
-    wtile_load<FMT, R, KC, TL>(a.w, rows, lane, cur);
-  }
-  const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
-  if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm(a.in, a.gain, a.eps, a.w.cols, xs, red, lay);
-  else stage_copy(a.in, a.w.cols, xs, lay);
-
   int pos = 0;
   if constexpr (EPI == EPI_QKV) pos = a.state[0];
+
+  // Loads in this order: the activations (the previous launch's output), then this
+  // team's first item -- vector loads return in issue order, so the staging below
+  // waits for the activations only, while the weights are still in flight.
+  using Pro = typename std::conditional<PRO == PRO_COMBINE, CombineIn, StageIn>::type;
+  Pro pin;
+  if constexpr (PRO == PRO_COMBINE) pin.load(a.in, a.heads);
+  else pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
+  Item<FMT, TL, R, KC, EPI> A, B;
+  A.load(a, it, pos, lane);
+  const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
+  if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish(pin, a.eps, a.w.cols, xs, red, lay);
+  else if constexpr (PRO == PRO_COMBINE) stage_attn_combine(pin, a.heads, xs, lay, wl);
+  else stage_copy_finish(pin, a.w.cols, xs, lay);
+
   float bv = NAN;
   int bi = 0x7fffffff;
-  while (it < a.items) {
-    const int nx = it + stride;
-    int nrows[R];
-    WTile<FMT, R, KC> nxt;
-    if (nx < a.items) {
-      item_rows<EPI, R>(a, nx, nrows);
-      wtile_load<FMT, R, KC, TL>(a.w, nrows, lane, nxt);
+  double acc[R];
+  if constexpr (!LOOP) {
+    if (it < a.items) {
+      wtile_dot<FMT, R, KC, TL>(a.w, A.w, xs, lane, acc);
+      if (lane == 0) epilogue<R, EPI>(a, it, pos, A.rows, acc, A.e, bv, bi);
     }
-    double acc[R];
-    wtile_dot<FMT, R, KC, TL>(a.w, cur, xs, lane, acc);
-    if (lane == 0) epilogue<R, EPI>(a, it, pos, rows, acc, bv, bi);
-    it = nx;
-#pragma unroll
-    for (int i = 0; i < R; i++) rows[i] = nrows[i];
-    cur = nxt;
+  } else {
+    while (it < a.items) {
+      B.load(a, it + stride, pos, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      wtile_dot<FMT, R, KC, TL>(a.w, A.w, xs, lane, acc);
+      if (lane == 0) epilogue<R, EPI>(a, it, pos, A.rows, acc, A.e, bv, bi);
+      it += stride;
+      if (it >= a.items) break;
+      A.load(a, it + stride, pos, lane);
+      __builtin_amdgcn_sched_barrier(0);
+      wtile_dot<FMT, R, KC, TL>(a.w, B.w, xs, lane, acc);
+      if (lane == 0) epilogue<R, EPI>(a, it, pos, B.rows, acc, B.e, bv, bi);
+      it += stride;
+    }
   }
   if constexpr (EPI == EPI_LOGITS) {
     if (lane == 0) tbest[T::team()] = {bv, bi};
@@ -283,7 +343,11 @@ static hipError_t fused_t(hipStream_t s, FusedArgs a, int items, int max_blocks)
   a.items = items;
   const int blocks = fused_blocks(items, T::kTeams, max_blocks);
   const size_t lds = (size_t)a.w.cols * sizeof(double);
-  hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI>), dim3(blocks), dim3(kBlock), lds, s, a);
+  if ((size_t)blocks * T::kTeams >= (size_t)items) {
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false>), dim3(blocks), dim3(kBlock), lds, s, a);
+  } else {
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true>), dim3(blocks), dim3(kBlock), lds, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -316,6 +380,8 @@ int lm_head_blocks(const ModelDev& m) {
 }
 
 size_t lm_partials_bytes(const ModelDev& m) { return (size_t)lm_head_blocks(m) * sizeof(ArgPair); }
+
+size_t attn_part_bytes(const ModelDev& m) { return (size_t)m.heads * kDecodeSlots * kPartStride * sizeof(float); }
 
 int launches_per_step(const ModelDev& m, StepInput in) {
   return (in == STEP_GATHER ? 1 : 0) + 5 * m.layers + 2;
@@ -368,35 +434,58 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     if ((e = fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2)) != hipSuccess)
       return e;
 
-    ExactArgs a{};
-    a.q = c.q;
-    a.kc = kc;
-    a.vt = vt;
-    a.d_pos = c.state;
-    a.scores = c.scores;
-    a.maxes = c.maxes;
-    a.counters = c.attn_counters;
-    a.out = c.attn;
-    a.capacity = c.capacity;
-    a.vstride = c.vstride;
-    a.heads = m.heads;
-    a.kv_heads = m.kv_heads;
-    a.score_stride = c.score_stride;
-    a.max_stride = attn_spans(c.capacity);
     if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
-    if (c.capacity <= kPLds) {
-      hipLaunchKernelGGL(k_attn_block, dim3(m.heads, 1), dim3(kAttnThreads), 0, s, a);
+    if (m.numerics == QH_NUMERICS_FAST) {
+      SlotArgs a{};
+      a.q = c.q;
+      a.kc = kc;
+      a.vt = vt;
+      a.d_pos = c.state;
+      a.part = c.part;
+      a.capacity = c.capacity;
+      a.vstride = c.vstride;
+      a.heads = m.heads;
+      a.kv_heads = m.kv_heads;
+      a.max_slots = kDecodeSlots;
+      const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
+      hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, 1), dim3(kBlock), 0, s, a);
     } else {
-      hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
+      ExactArgs a{};
+      a.q = c.q;
+      a.kc = kc;
+      a.vt = vt;
+      a.d_pos = c.state;
+      a.scores = c.scores;
+      a.maxes = c.maxes;
+      a.counters = c.attn_counters;
+      a.out = c.attn;
+      a.capacity = c.capacity;
+      a.vstride = c.vstride;
+      a.heads = m.heads;
+      a.kv_heads = m.kv_heads;
+      a.score_stride = c.score_stride;
+      a.max_stride = attn_spans(c.capacity);
+      if (c.capacity <= kPLds) {
+        hipLaunchKernelGGL(k_attn_block, dim3(m.heads, 1), dim3(kAttnThreads), 0, s, a);
+      } else {
+        hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
+      }
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
     f = FusedArgs{};
     f.w = l.o;
-    f.in = c.attn;
     f.out = c.x;
     if ((e = mark(s, timer, QH_ROLE_OPROJ)) != hipSuccess) return e;
-    if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
+    if (m.numerics == QH_NUMERICS_FAST) {
+      f.in = c.part;
+      f.heads = m.heads;
+      f.state = c.state;
+      if ((e = fused<2, PRO_COMBINE, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
+    } else {
+      f.in = c.attn;
+      if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
+    }
 
     f = FusedArgs{};
     f.eps = m.eps;

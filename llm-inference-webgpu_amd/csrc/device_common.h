@@ -393,17 +393,18 @@ struct WTile {
 template <int FMT, int R, int KC, int TL>
 __device__ __forceinline__ void wtile_load(const DMat& m, const int (&rows)[R], int tl,
                                            WTile<FMT, R, KC>& t) {
+  // Unconditional loads (a lane past the row end re-reads the row's last chunk,
+  // which wtile_dot skips): no branch, so no load has to wait for a merge.
 #pragma unroll
   for (int k = 0; k < KC; k++) {
-    const int c = tl + k * TL;
-    const bool in = c < m.nchunks;
+    const int c = min(tl + k * TL, m.nchunks - 1);
 #pragma unroll
     for (int i = 0; i < R; i++) {
       const v4u* rp = reinterpret_cast<const v4u*>(m.data + (size_t)rows[i] * m.row_bytes);
-      t.w[k][i] = in ? __builtin_nontemporal_load(&rp[c]) : v4u{0, 0, 0, 0};
+      t.w[k][i] = __builtin_nontemporal_load(&rp[c]);
     }
     if constexpr (FMT == QH_FMT_INT4) {
-      const int g = (in ? c : 0) / m.cpg;
+      const int g = c / m.cpg;
 #pragma unroll
       for (int i = 0; i < R; i++) {
         t.s[k][i] = m.scales[(size_t)rows[i] * m.gpr + g];
@@ -456,30 +457,40 @@ struct Teams {
 constexpr int kStageVec = 8;                           // float4 groups per thread
 constexpr int kStageMax = kStageVec * 4 * kBlock;      // 8192 values
 
+// Staging is split into the loads (StageIn::load) and the arithmetic
+// (stage_*_finish), so a kernel can issue its activation loads before its weight
+// loads: vector loads return in issue order, and waiting for an activation that
+// was issued after the weights would wait for the weights too.
+struct StageIn {
+  v4f v[kStageVec], g[kStageVec];
+  // x (and gain, when given) for n values; n a multiple of 4 and at most kStageMax,
+  // both 16-byte aligned.
+  __device__ __forceinline__ void load(const float* __restrict__ x, const float* __restrict__ gain, int n) {
+    const int n4 = n >> 2;
+#pragma unroll
+    for (int j = 0; j < kStageVec; j++) {
+      const int i = threadIdx.x + j * kBlock;
+      if (i < n4) {
+        v[j] = reinterpret_cast<const v4f*>(x)[i];
+        if (gain) g[j] = reinterpret_cast<const v4f*>(gain)[i];
+      }
+    }
+  }
+};
+
 // xs = x / sqrt(mean(x^2) + eps) * gain as f64 values of the f32 result, with
 // the statistic and the products in f64 as src/core/ops.js:17-24 evaluates
 // them, so the normalized vector is the CPU's up to the order of the f64 sum.
-// cols is a multiple of 4 and at most kStageMax; x and gain are 16-byte aligned.
-// Element i goes to xs[lay.pos(i)].
-__device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
-                                              const float* __restrict__ gain, double eps, int cols,
-                                              double* xs, double* red, XLayout lay) {
+// `in` holds x and gain (StageIn::load); element i goes to xs[lay.pos(i)].
+__device__ __forceinline__ void stage_rmsnorm_finish(const StageIn& in, double eps, int cols, double* xs,
+                                                     double* red, XLayout lay) {
   const int n4 = cols >> 2;
-  v4f v[kStageVec], g[kStageVec];
-#pragma unroll
-  for (int j = 0; j < kStageVec; j++) {
-    const int i = threadIdx.x + j * kBlock;
-    if (i < n4) {
-      v[j] = reinterpret_cast<const v4f*>(x)[i];
-      g[j] = reinterpret_cast<const v4f*>(gain)[i];
-    }
-  }
   double ss = 0;
 #pragma unroll
   for (int j = 0; j < kStageVec; j++) {
     if (threadIdx.x + j * kBlock < n4) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) ss = fma((double)v[j][e], (double)v[j][e], ss);  // v*v exact in f64
+      for (int e = 0; e < 4; e++) ss = fma((double)in.v[j][e], (double)in.v[j][e], ss);  // v*v exact in f64
     }
   }
   ss = block_sum_f64(ss, red);
@@ -489,10 +500,19 @@ __device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
     const int i = threadIdx.x + j * kBlock;
     if (i < n4) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) xs[lay.pos(4 * i + e)] = (double)(float)((double)v[j][e] * scale * (double)g[j][e]);
+      for (int e = 0; e < 4; e++)
+        xs[lay.pos(4 * i + e)] = (double)(float)((double)in.v[j][e] * scale * (double)in.g[j][e]);
     }
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void stage_rmsnorm(const float* __restrict__ x,
+                                              const float* __restrict__ gain, double eps, int cols,
+                                              double* xs, double* red, XLayout lay) {
+  StageIn in;
+  in.load(x, gain, cols);
+  stage_rmsnorm_finish(in, eps, cols, xs, red, lay);
 }
 
 // stage_rmsnorm for any cols and alignment, one element per thread and step.
@@ -512,20 +532,14 @@ __device__ __forceinline__ void stage_rmsnorm_scalar(const float* __restrict__ x
 }
 
 // xs = (double)x for an f32 vector (same bounds and layout as stage_rmsnorm).
-__device__ __forceinline__ void stage_copy(const float* __restrict__ x, int n, double* xs, XLayout lay) {
+__device__ __forceinline__ void stage_copy_finish(const StageIn& in, int n, double* xs, XLayout lay) {
   const int n4 = n >> 2;
-  v4f v[kStageVec];
-#pragma unroll
-  for (int j = 0; j < kStageVec; j++) {
-    const int i = threadIdx.x + j * kBlock;
-    if (i < n4) v[j] = reinterpret_cast<const v4f*>(x)[i];
-  }
 #pragma unroll
   for (int j = 0; j < kStageVec; j++) {
     const int i = threadIdx.x + j * kBlock;
     if (i < n4) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) xs[lay.pos(4 * i + e)] = (double)v[j][e];
+      for (int e = 0; e < 4; e++) xs[lay.pos(4 * i + e)] = (double)in.v[j][e];
     }
   }
   __syncthreads();

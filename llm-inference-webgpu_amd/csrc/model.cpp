@@ -87,6 +87,8 @@ struct qh_model {
   qh::ModelDev dev{};
   size_t bytes = 0;
   int live_caches = 0;
+  int caches_made = 0;
+  int numerics = QH_NUMERICS_FAST;
 
   int alloc(size_t n, void** p) {
     if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
@@ -416,7 +418,21 @@ int qh_model_finalize(qh_model* m) {
   d.layers_host = m->layers.data();
   d.rope_cos = dcos;
   d.rope_sin = dsin;
+  if (m->numerics == QH_NUMERICS_FAST && c.heads > 16) m->numerics = QH_NUMERICS_EXACT;
+  d.numerics = m->numerics;
   m->finalized = true;
+  return QH_OK;
+}
+
+int qh_model_set_numerics(qh_model* m, int32_t numerics) {
+  QH_CHECK(m, QH_ERR_INVALID, "model is NULL");
+  QH_CHECK(numerics == QH_NUMERICS_FAST || numerics == QH_NUMERICS_EXACT, QH_ERR_INVALID,
+           "unknown numerics mode %d", numerics);
+  QH_CHECK(m->caches_made == 0, QH_ERR_STATE, "set the numerics before the model's first cache");
+  QH_CHECK(numerics != QH_NUMERICS_FAST || m->cfg.heads <= 16, QH_ERR_INVALID,
+           "fast numerics supports at most 16 query heads (got %d)", m->cfg.heads);
+  m->numerics = numerics;
+  m->dev.numerics = numerics;
   return QH_OK;
 }
 
@@ -470,6 +486,7 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   A((size_t)md.heads * d.score_stride * 4, (void**)&d.scores);
   A((size_t)md.heads * spans * 4, (void**)&d.maxes);
   A(256, (void**)&d.attn_counters);
+  A(qh::attn_part_bytes(md), (void**)&d.part);
   A(qh::lm_partials_bytes(md), &d.lm_partials);
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
     rc = fail(QH_ERR_NOMEM, "pinned allocation failed");
@@ -488,6 +505,7 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
     return rc;
   }
   m->live_caches++;
+  m->caches_made++;
   *out = c;
   return QH_OK;
 }

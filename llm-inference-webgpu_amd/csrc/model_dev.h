@@ -21,6 +21,7 @@ struct LayerDev {
 
 struct ModelDev {
   int hidden, intermediate, layers, heads, kv_heads, head_dim, vocab, max_positions;
+  int numerics;                 // QH_NUMERICS_*
   double eps;
   const LayerDev* layers_host;  // host array of per-layer descriptors
   DMat lm_head;                 // [vocab, hidden]
@@ -49,6 +50,7 @@ struct CacheDev {
   float* maxes;        // [heads][spans(capacity)]: per-span score maxima
   int score_stride;    // capacity rounded up to 4
   int* attn_counters;  // [heads], zero between launches
+  float* part;         // [heads][kDecodeSlots][kPartStride]: split-K attention slot partials
   void* lm_partials;   // argmax block partials
   int lm_blocks;
 };
@@ -79,5 +81,7 @@ int launches_per_step(const ModelDev& m, StepInput in);
 // Blocks the lm_head launch uses (sizes lm_partials).
 int lm_head_blocks(const ModelDev& m);
 size_t lm_partials_bytes(const ModelDev& m);
+// Bytes of the split-K attention slot partials of one position (CacheDev::part).
+size_t attn_part_bytes(const ModelDev& m);
 
 }  // namespace qh

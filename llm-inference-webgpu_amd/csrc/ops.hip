@@ -347,28 +347,31 @@ hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t*
   return hipGetLastError();
 }
 
-size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx) {
-  return (size_t)seq * kv_heads * attn_grid_splits(max_ctx) * (heads / kv_heads) * kPartialStride;
+size_t attention_partials_floats(int seq, int heads) {
+  return (size_t)seq * heads * kOpSlots * kPartStride;
 }
 
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
                                    const uint16_t* vt, int capacity, float* out, int seq, int past,
-                                   int heads, int kv_heads, float* partials, int* counters) {
-  SplitArgs a{};
+                                   int heads, int kv_heads, float* partials) {
+  SlotArgs a{};
   a.q = q;
   a.kc = kc;
   a.vt = vt;
-  a.partials = partials;
-  a.counters = counters;
-  a.out = out;
+  a.part = partials;
   a.past = past;
-  a.seq = seq;
   a.capacity = capacity;
   a.vstride = value_stride(capacity);
   a.heads = heads;
   a.kv_heads = kv_heads;
-  a.s_grid = attn_grid_splits(past + seq);
-  hipLaunchKernelGGL(k_attention_splitk, dim3(a.s_grid, kv_heads, seq), dim3(kBlock), 0, s, a);
+  a.max_slots = kOpSlots;
+  const int waves = heads * kOpSlots;
+  const int per_block = kBlock / kWave;
+  hipLaunchKernelGGL(k_attn_slots<kOpSlots>, dim3((waves + per_block - 1) / per_block, seq), dim3(kBlock), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_combine, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
+                     kOpSlots);
   return hipGetLastError();
 }
 

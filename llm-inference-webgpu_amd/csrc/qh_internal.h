@@ -100,12 +100,12 @@ hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t*
                                   const uint16_t* vt, int capacity, float* out, int seq, int past,
                                   int heads, int kv_heads, float* scores, int* counters);
 size_t attention_exact_floats(int seq, int heads, int past);
-// Split-K attention. `partials` holds attention_partials_floats(...) floats and `counters`
-// seq*kv_heads ints, zeroed before first use (the kernel leaves them zeroed).
+// Split-K attention: slot partials, then a combine launch. `partials` holds
+// attention_partials_floats(seq, heads) floats (no initial contents needed).
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
                                    const uint16_t* vt, int capacity, float* out, int seq, int past,
-                                   int heads, int kv_heads, float* partials, int* counters);
-size_t attention_partials_floats(int seq, int heads, int kv_heads, int max_ctx);
+                                   int heads, int kv_heads, float* partials);
+size_t attention_partials_floats(int seq, int heads);
 // f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).
 void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);

@@ -24,13 +24,15 @@ def tiny(hip, **kw):
     return hip.ModelConfig(**base)
 
 
-@pytest.fixture(scope="module", params=["f16", "int8", "int4"])
+@pytest.fixture(scope="module", params=[(s, n) for n in ("fast", "exact") for s in ("f16", "int8", "int4")],
+                ids=lambda p: f"{p[0]}-{p[1]}")
 def tiny_model(request, ctx, hip):
-    scheme = request.param
+    scheme, numerics = request.param
     cfg = tiny(hip)
     ckpt = hip.synthesize_checkpoint(cfg, seed=3)
     lm = "int8" if scheme != "f16" else "f16"
-    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, scheme, 128, lm), cfg, maxPositions=256)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, scheme, 128, lm), cfg, maxPositions=256,
+                              numerics=numerics)
     oracle = O.OracleModel(cfg, ckpt, scheme=scheme, group=128, lm_head=lm, kv_f16=True)
     yield cfg, model, oracle, scheme
     model.destroy()
@@ -162,12 +164,13 @@ def full_ckpt(hip):
     return hip.synthesize_checkpoint(hip.QWEN25_05B, seed=1)
 
 
-def test_config1_full_shape_greedy_matches_oracle(ctx, hip, full_ckpt):
+@pytest.mark.parametrize("numerics", ["fast", "exact"])
+def test_config1_full_shape_greedy_matches_oracle(ctx, hip, full_ckpt, numerics):
     """Config 1: 16 seeded prompt ids, 32 greedy tokens, Qwen2.5-0.5B shape. Weights are
     the reference GPU path's f16; the oracle sees the same f16 weights and f16 cache."""
     cfg = hip.QWEN25_05B
     model = hip.GpuModel.load(ctx, hip.device_tensors(full_ckpt, cfg, "f16", 128, "f16"), cfg,
-                              maxPositions=64)
+                              maxPositions=64, numerics=numerics)
     prompt = hip.synth_tokens(1, "config1.prompt", cfg.vocab, 16)
     cache = model.newCache(48)
     out = model.forward_tokens(prompt, cache)
@@ -184,12 +187,15 @@ def test_config1_full_shape_greedy_matches_oracle(ctx, hip, full_ckpt):
     model.destroy()
 
 
-def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt):
+@pytest.mark.parametrize("numerics", ["fast", "exact"])
+def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt, numerics):
     """Config 4's model (int4-g128 layers, int8 output head, f16 cache) on a shorter
-    context: 64 prompt ids then 24 greedy tokens, plus the per-layer present K/V."""
+    context: 64 prompt ids then 24 greedy tokens, plus the per-layer present K/V (exact
+    numerics: all but f64-ordering ties bit-identical; fast: f32 rounding in attention
+    flips the f16 rounding of a few cache entries)."""
     cfg = hip.QWEN25_05B
     model = hip.GpuModel.load(ctx, hip.device_tensors(full_ckpt, cfg, "int4", 128, "int8"), cfg,
-                              maxPositions=128)
+                              maxPositions=128, numerics=numerics)
     prompt = hip.synth_tokens(4, "config4.prompt", cfg.vocab, 64)
     cache = model.newCache(96)
     out = model.forward_tokens(prompt, cache)
@@ -198,18 +204,55 @@ def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt):
     ologits = oracle.forward(prompt, ocache)
     print(f"config4 logits rel {rel_err(out['logits'], ologits):.2e}")
     assert rel_err(out["logits"], ologits) <= LOGIT_REL
-    worst, same, total = 0.0, 0, 0
+    worst, worst_ulps, min_cos, same, total = 0.0, 0.0, 1.0, 0, 0   # ulps: of the layer's largest entry
     for L in range(cfg.layers):
         for kind in ("key", "value"):
             g, o = cache.present(L)[kind], ocache.present(L)[kind]
             worst = max(worst, rel_err(g, o))
+            top = np.float16(np.max(np.abs(o)))
+            worst_ulps = max(worst_ulps, float(np.max(np.abs(g - o))) / float(np.spacing(top)))
+            gd, od = g.astype(np.float64).ravel(), o.astype(np.float64).ravel()
+            min_cos = min(min_cos, float(gd @ od / (np.linalg.norm(gd) * np.linalg.norm(od))))
             same += int(np.sum(g.view(np.uint32) == o.view(np.uint32)))
             total += g.size
-    print(f"config4 worst per-layer present rel {worst:.2e}, bit-identical {same}/{total}")
-    assert worst <= 5e-4      # PER_LAYER_REL, test/model.test.js:39
-    assert same / total >= 0.999
+    print(f"config4 {numerics}: per-layer present max-abs rel {worst:.2e} ({worst_ulps:.2f} f16 ulp of the max), "
+          f"min cosine {min_cos:.9f}, bit-identical {same}/{total}")
+    if numerics == "exact":
+        assert worst <= 5e-4      # PER_LAYER_REL, test/model.test.js:39
+        assert same / total >= 0.999
+    else:
+        # An f32-rounding difference can move a cache entry across an f16 rounding boundary,
+        # and later positions attend to the moved entry: the per-layer bound for an f16 cache
+        # is one f16 unit at the layer's largest entry (up to 2^-10 of it, above 5e-4).
+        assert worst_ulps <= 1.0
+        assert min_cos >= 0.99999
     gen = model.decode(cache, out["argmax"], 23)
     want, _ = oracle.generate(prompt, 24)
     assert [out["argmax"]] + list(gen) == list(want)
     cache.destroy()
     model.destroy()
+
+
+def test_fast_numerics_long_context_matches_exact(ctx, hip):
+    """Past 16 x 64 positions each split-K slot of the fast path spans several chunks
+    (slot_plan); the fast step must stay within the logit tolerance of the exact one and
+    choose the same greedy tokens."""
+    cfg = tiny(hip)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=11)
+    tensors = hip.device_tensors(ckpt, cfg, "int4", 128, "int8")
+    fast = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=1600, numerics="fast")
+    exact = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=1600, numerics="exact")
+    prompt = hip.synth_tokens(11, "long", cfg.vocab, 1400)
+    cf, ce = fast.newCache(1500), exact.newCache(1500)
+    a = fast.forward_tokens(prompt, cf)
+    b = exact.forward_tokens(prompt, ce)
+    print(f"long context fast vs exact logits rel {rel_err(a['logits'], b['logits']):.2e}")
+    assert rel_err(a["logits"], b["logits"]) <= LOGIT_REL
+    assert a["argmax"] == b["argmax"]
+    assert list(fast.decode(cf, a["argmax"], 16)) == list(exact.decode(ce, b["argmax"], 16))
+    with pytest.raises(hip.QwenHipError, match="before the model's first cache"):
+        hip._check(fast.lib.qh_model_set_numerics(fast.handle, 1))
+    for c in (cf, ce):
+        c.destroy()
+    fast.destroy()
+    exact.destroy()
