@@ -105,6 +105,13 @@ typedef struct {
  * x f32 [seq, cols], bias f32 [rows] or NULL, y f32 [seq, rows]. */
 int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
               float* d_y, int32_t seq);
+/* The batched-prefill contraction on the matrix cores (no counterpart kernel in the reference,
+ * whose prefill is batchedMatvec, kernels.js:232-290, selected by model.js:297-306):
+ * y [M, rows] = x [M, cols] . W^T (+ bias) for int8 / int4 weights, as bf16 MFMA over the exact
+ * weight codes and a two-term bf16 split of x (products exact, f32 accumulation, scales
+ * factored out). cols must be a multiple of 32. x, y f32 [M, cols] / [M, rows]. */
+int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+                      float* d_y, int32_t M);
 /* The isolated-matvec form: f16 activation x [cols], f32 y [rows]. */
 int qh_matvec_xh(qh_ctx* ctx, const qh_weight* w, const uint16_t* d_x, float* d_y);
 /* A list of `count` same-shape matrices in one launch: weight i starts at

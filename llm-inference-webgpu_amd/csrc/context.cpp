@@ -234,6 +234,26 @@ int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_
   return QH_OK;
 }
 
+int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+                      float* d_y, int32_t M) {
+  QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
+  qh::DMat m;
+  int rc = qh::make_dmat(w, &m);
+  if (rc) return rc;
+  QH_CHECK(m.format == QH_FMT_INT8 || m.format == QH_FMT_INT4, QH_ERR_INVALID,
+           "the MFMA prefill takes int8 or int4 weights (format %d given)", m.format);
+  QH_CHECK(m.cols % 32 == 0, QH_ERR_INVALID, "cols %d must be a multiple of 32", m.cols);
+  QH_CHECK(d_x && d_y, QH_ERR_INVALID, "matmul needs x and y");
+  QH_CHECK(((uintptr_t)d_x & 15) == 0, QH_ERR_INVALID, "x must be 16-byte aligned");
+  QH_CHECK(M >= 1, QH_ERR_INVALID, "M %d must be at least 1", M);
+  void* tmp = nullptr;
+  QH_HIP(hipMallocAsync(&tmp, qh::matmul_prefill_scratch_bytes(m, M), ctx->stream));
+  hipError_t e = qh::launch_matmul_prefill(ctx->stream, m, d_x, d_bias, d_y, M, tmp);
+  QH_HIP(hipFreeAsync(tmp, ctx->stream));
+  QH_HIP(e);
+  return QH_OK;
+}
+
 int qh_matvec_xh(qh_ctx* ctx, const qh_weight* w, const uint16_t* d_x, float* d_y) {
   return qh_matvec_xh_list(ctx, w, 1, 0, 0, d_x, 0, d_y);
 }

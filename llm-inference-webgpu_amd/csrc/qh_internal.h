@@ -82,6 +82,11 @@ namespace qh {
 hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
                          int seq, double* x64_scratch = nullptr);
 size_t matvec_x64_bytes(const DMat& m, int seq);
+// The batched-prefill contraction on bf16 MFMA (int8 / int4 weights): y [M, rows] = x [M, cols] . W^T
+// (+ bias). `scratch` holds matmul_prefill_scratch_bytes(w, M) bytes.
+hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias, float* y,
+                                 int M, void* scratch);
+size_t matmul_prefill_scratch_bytes(const DMat& w, int M);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,

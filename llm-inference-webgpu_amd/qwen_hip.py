@@ -139,6 +139,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_attention": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_attention_splitk": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
+        "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32],
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
         "qh_quantize_int4": [vp, i32, i32, i32, vp, vp, vp],
@@ -405,6 +406,11 @@ class GpuContext:
     def matvec(self, w: Weight, x: DeviceBuffer, bias, y: DeviceBuffer, seq: int = 1) -> None:
         _check(self.lib.qh_matvec(self.handle, ctypes.byref(w), x.ptr, bias.ptr if bias else None,
                                   y.ptr, seq))
+
+    def matmul_prefill(self, w: Weight, x: DeviceBuffer, bias, y: DeviceBuffer, M: int) -> None:
+        """y [M, rows] = x [M, cols] . W^T (+ bias) on bf16 MFMA (int8 / int4 weights)."""
+        _check(self.lib.qh_matmul_prefill(self.handle, ctypes.byref(w), x.ptr,
+                                          bias.ptr if bias else None, y.ptr, M))
 
     def matvec_xh_list(self, w: Weight, count: int, data_stride: int, scale_stride: int,
                        x: DeviceBuffer, x_stride: int, y: DeviceBuffer) -> None:

@@ -149,6 +149,45 @@ def test_batched_matvec_equals_single_position_bitwise(ctx, hip, fmt, seq):
     free(wb, dX, db, dY, dy)
 
 
+MFMA_REL = KERNEL_REL   # bf16 MFMA over exact codes and a two-term bf16 split of x (2^-17), f32 sums
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("M,rows,cols", [(1, 896, 896), (17, 1152, 896), (64, 896, 896), (130, 896, 4864),
+                                         (512, 896, 896), (100, 9728, 896), (512, 896, 4864)])
+def test_matmul_prefill_matches_oracle(ctx, hip, fmt, M, rows, cols):
+    """The MFMA prefill contraction against the oracle's f64 matvec of every position, on
+    the same dequantized weights: within MFMA_REL (a stated tolerance, as the reference
+    gave its tiled matmul one, web/scaling.html:122-127)."""
+    rng = np.random.default_rng(M * 31 + rows + cols)
+    w32 = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    X = rng.standard_normal((M, cols)).astype(np.float32)
+    bias = (rng.standard_normal(rows) * 0.02).astype(np.float32)
+    W, wb, deq = upload_weight(ctx, hip, w32, fmt)
+    dX, db, dY = ctx.upload(X), ctx.upload(bias), ctx.empty(M * rows * 4)
+    ctx.matmul_prefill(W, dX, db, dY, M)
+    got = dY.read(count=M * rows).reshape(M, rows)
+    worst = 0.0
+    for t in range(M):
+        ref = O.matvec(deq, X[t], rows, cols, bias)
+        worst = max(worst, rel_err(got[t], ref))
+    print(f"matmul_prefill {fmt} M={M} {rows}x{cols}: worst row rel {worst:.2e}")
+    assert worst <= MFMA_REL
+    free(wb, dX, db, dY)
+
+
+def test_matmul_prefill_rejects_f16_and_ragged_k(ctx, hip):
+    rng = np.random.default_rng(0)
+    W, wb, _ = upload_weight(ctx, hip, (rng.standard_normal((64, 896)) * 0.02).astype(np.float32), "f16")
+    dX, dY = ctx.upload(np.zeros((4, 896), np.float32)), ctx.empty(4 * 64 * 4)
+    with pytest.raises(hip.QwenHipError, match="int8 or int4"):
+        ctx.matmul_prefill(W, dX, None, dY, 4)
+    W8, wb8, _ = upload_weight(ctx, hip, (rng.standard_normal((64, 48)) * 0.02).astype(np.float32), "int8")
+    with pytest.raises(hip.QwenHipError, match="multiple of 32"):
+        ctx.matmul_prefill(W8, dX, None, dY, 4)
+    free(wb, wb8, dX, dY)
+
+
 @pytest.mark.parametrize("rows,cols", SHAPES + [(151936, 896)])
 def test_matvec_f16_activation_list(ctx, hip, rows, cols):
     # Config 2: int8 weights, x ~ N(0,1) in f16, a list of distinct matrices in one launch.
