@@ -96,6 +96,96 @@ def isolated_matvec(ctx, shapes, reps=5):
     return out
 
 
+class _Ptr:
+    """A device address inside a larger DeviceBuffer (what the operator bindings take)."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
+def attention_sweep(ctx, contexts=(128, 1024, 4096, 32768), heads=14, kv_heads=2, rounds=3):
+    """Config 3: one query over an f16 K/V cache (N(0,1) values) at each context, timed per call
+    over a rotation of distinct caches totalling >= 512 MiB (larger than the last-level cache).
+    Algorithmic bytes per call: K and V (512 B per position over both kv heads) + q and out."""
+    out = {}
+    rng = np.random.default_rng(3)
+    for n_ctx in contexts:
+        cap = n_ctx
+        vstride = (cap + 7) // 8 * 8
+        k_elems, v_elems = kv_heads * cap * 64, kv_heads * 64 * vstride
+        per = 2 * (k_elems + v_elems)
+        copies = int(np.ceil((512 << 20) / per))
+        block = rng.standard_normal(min(k_elems + v_elems, 1 << 22)).astype(np.float16)
+        reps = int(np.ceil(copies * (k_elems + v_elems) / block.size))
+        buf = ctx.upload(np.tile(block, reps)[:copies * (k_elems + v_elems)])
+        q = ctx.upload(rng.standard_normal(heads * 64).astype(np.float32))
+        o = ctx.empty(heads * 64 * 4)
+        algo = 2 * 2 * kv_heads * 64 * n_ctx + 2 * heads * 64 * 4
+        res = {}
+        for name, splitk in (("splitk", True), ("exact", False)):
+            def call(i):
+                base = buf.ptr + i * per
+                ctx.attention(q, _Ptr(base), _Ptr(base + 2 * k_elems), cap, o, 1, n_ctx - 1, heads, kv_heads,
+                              splitk=splitk)
+            for i in range(min(copies, 64)):
+                call(i)   # warm
+            ctx.done()
+            e0, e1 = ctx.event(), ctx.event()
+            ctx.record(e0)
+            for r in range(rounds):
+                for i in range(copies):
+                    call(i)
+            ctx.record(e1)
+            ms = ctx.elapsed_ms(e0, e1) / (rounds * copies)
+            ctx.destroy_event(e0), ctx.destroy_event(e1)
+            res[name] = {"us_per_call": round(ms * 1e3, 3), "GBps": round(algo / (ms * 1e-3) / 1e9, 1)}
+        out[str(n_ctx)] = {"caches": copies, "bytes_per_call": algo, **res}
+        log(f"attention ctx {n_ctx} x{copies}: split-K {res['splitk']['us_per_call']} us, "
+            f"exact {res['exact']['us_per_call']} us per call")
+        for b in (buf, q, o):
+            b.free()
+    return out
+
+
+def prefill_bench(ctx, cfg, ckpt, seed, prompt_len=512):
+    """Config 5: time-to-first-token of a seeded prompt with int8 layers and head, through
+    one decode step per position, the reference's 8-position tiles, and the MFMA contraction.
+    A token's time covers the embedding gather, all layers, the head and the argmax readback."""
+    tensors = H.device_tensors(ckpt, cfg, "int8", 128, "int8")
+    model = H.GpuModel.load(ctx, tensors, cfg, maxPositions=prompt_len + 8)
+    del tensors
+    prompt = H.synth_tokens(seed, "config5.prompt", cfg.vocab, prompt_len)
+    res = {}
+    logits = {}
+    for mode in ("matvec", "batched", "mfma"):
+        model.set_matmul(mode)
+        cache = model.newCache(prompt_len + 8)
+        model.forward_tokens(prompt, cache)   # warm (allocations, code objects)
+        best = None
+        for _ in range(3):
+            cache.length = 0
+            t0 = time.perf_counter()
+            r = model.forward_tokens(prompt, cache)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        logits[mode] = r
+        res[mode] = {"ttft_ms": round(best * 1e3, 2), "prompt_tok_per_s": round(prompt_len / best, 1)}
+        cache.destroy()
+        log(f"prefill {prompt_len} ({mode}): {best * 1e3:.1f} ms")
+    ref = logits["batched"]["logits"].astype(np.float64)
+    for mode in ("matvec", "mfma"):
+        got = logits[mode]["logits"].astype(np.float64)
+        res[mode]["logits_rel_vs_batched"] = float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+        res[mode]["argmax_equal"] = logits[mode]["argmax"] == logits["batched"]["argmax"]
+    lin = 2 * prompt_len * sum(r * c for r, c in (
+        (cfg.hidden + 2 * cfg.kv_dim, cfg.hidden), (cfg.hidden, cfg.hidden),
+        (2 * cfg.intermediate, cfg.hidden), (cfg.hidden, cfg.intermediate))) * cfg.layers
+    res["linear_gflop"] = round(lin / 1e9, 1)
+    res["mfma_linear_tflops_lower_bound"] = round(lin / (res["mfma"]["ttft_ms"] * 1e-3) / 1e12, 1)
+    model.destroy()
+    return res
+
+
 def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
     """The oracle (a C port of the reference CPU path, f64 accumulation) on one core:
     its KV cache is loaded with the GPU cache's context (the same f16 values), then it
@@ -136,7 +226,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=32)
     ap.add_argument("--cpu-steps", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--isolated", choices=["all", "none"], default="all")
+    ap.add_argument("--isolated", choices=["all", "none"], default="all",
+                    help="the isolated config-2 matvec, config-3 attention and config-5 prefill lines")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
                     help="decode by hipGraph replay (default) or direct launches of the same "
                          "kernels (for profilers that do not follow graph launches)")
@@ -166,7 +257,7 @@ def main():
     t0 = time.perf_counter()
     first = model.forward_tokens(prompt, cache)["argmax"]
     prefill_s = time.perf_counter() - t0
-    log(f"prefilled {args.context} positions in {prefill_s:.2f}s (decode path, one position per step)")
+    log(f"prefilled {args.context} positions in {prefill_s:.2f}s (8-position batched tiles)")
 
     if args.warmup:
         model.decode(cache, first, args.warmup)
@@ -207,11 +298,13 @@ def main():
                 "traffic": None, "bytes_per_launch": rb[dominant]}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
-    iso = None
+    iso = attn = prefill = None
     if args.isolated == "all":
         d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
         iso = isolated_matvec(ctx, [("q_o", d, d), ("k_v", kv, d), ("gate_up", ffn, d),
                                     ("down", d, ffn), ("lm_head", V, d)])
+        attn = attention_sweep(ctx)
+        prefill = prefill_bench(ctx, cfg, ckpt, args.seed)
 
     cpu, match = (None, None)
     if not args.no_cpu:
@@ -233,6 +326,8 @@ def main():
         "profile_tokens_match_timed": deterministic,
         "greedy_match_cpu_sample": match,
         "matvec_isolated": iso,
+        "attention_decode": attn,
+        "prefill_512": prefill,
         "prefill_s": round(prefill_s, 3),
     }
     print(json.dumps(line), flush=True)

@@ -108,8 +108,8 @@ int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_
 /* The batched-prefill contraction on the matrix cores (no counterpart kernel in the reference,
  * whose prefill is batchedMatvec, kernels.js:232-290, selected by model.js:297-306):
  * y [M, rows] = x [M, cols] . W^T (+ bias) for int8 / int4 weights, as bf16 MFMA over the exact
- * weight codes and a two-term bf16 split of x (products exact, f32 accumulation, scales
- * factored out). cols must be a multiple of 32. x, y f32 [M, cols] / [M, rows]. */
+ * weight codes and an exact three-term bf16 split of x (products exact, f32 accumulation,
+ * scales factored out). cols must be a multiple of 32. x, y f32 [M, cols] / [M, rows]. */
 int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
                       float* d_y, int32_t M);
 /* The isolated-matvec form: f16 activation x [cols], f32 y [rows]. */
@@ -216,6 +216,19 @@ int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out);
  * path has one f32 arithmetic (src/gpu/kernels.js). */
 enum { QH_NUMERICS_FAST = 0, QH_NUMERICS_EXACT = 1 };
 int qh_model_set_numerics(qh_model* m, int32_t numerics);
+
+/* How forward() processes several positions (GpuModel.load's `matmul` option, model.js:87-98,
+ * 133-138, 297-317):
+ *   QH_MATMUL_BATCHED (default): all positions per layer, each weight read once per 8-position
+ *     tile (batchedMatvec); every output is summed as the decode step sums it, so a prefill and
+ *     the same positions decoded one by one give the same bits (README.md:256-272).
+ *   QH_MATMUL_MATVEC: one decode step per position (the reference's 'matvec').
+ *   QH_MATMUL_MFMA: all positions per layer, int8/int4 weights contracted on bf16 MFMA
+ *     (qh_matmul_prefill; f16 weights use the batched tiles); within a stated tolerance of the
+ *     others, as the reference's 'tiled' was (web/scaling.html:122-127).
+ * May be changed between forward() calls. */
+enum { QH_MATMUL_BATCHED = 0, QH_MATMUL_MATVEC = 1, QH_MATMUL_MFMA = 2 };
+int qh_model_set_matmul(qh_model* m, int32_t matmul);
 /* Upload one tensor by its checkpoint name (src/core/config.js:88-119), copied from host.
  *   model.embed_tokens.weight  QH_FMT_BF16 [vocab, hidden]: the input gather table
  *   lm_head.weight             F16 | INT8 | INT4 [vocab, hidden]: the output projection (for a

@@ -583,11 +583,10 @@ struct CombineIn {
   }
 };
 
-// `wl` is LDS of kBlock floats.
-__device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int heads, double* xs, XLayout lay,
-                                                   float* wl) {
+// The merged output dimensions 4*(i%16) .. +3 of head i/16 for thread i. `wl` is
+// LDS of kBlock floats.
+__device__ __forceinline__ v4f attn_combine_quad(const CombineIn& in, float* wl) {
   const int i = threadIdx.x;
-  const int h = min(i / kDecodeSlots, heads - 1), k = i % kDecodeSlots;
   const float M = team_max<16>(in.mv);     // slot 0 always holds position 0
   const float w = expf(in.mv - M);         // 0 for an empty slot (m = -inf)
   const float L = team_sum<16>(w * in.lv);
@@ -603,8 +602,15 @@ __device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int head
     acc.z = fmaf(ws, in.ov[s].z, acc.z);
     acc.w = fmaf(ws, in.ov[s].w, acc.w);
   }
+  return acc;
+}
+
+__device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int heads, double* xs, XLayout lay,
+                                                   float* wl) {
+  const v4f acc = attn_combine_quad(in, wl);
+  const int i = threadIdx.x;
   if (i < heads * kDecodeSlots) {
-    const int j = h * kHeadDim + 4 * k;
+    const int j = (i / kDecodeSlots) * kHeadDim + 4 * (i % kDecodeSlots);
     xs[lay.pos(j)] = (double)acc.x;
     xs[lay.pos(j + 1)] = (double)acc.y;
     xs[lay.pos(j + 2)] = (double)acc.z;

@@ -111,7 +111,8 @@ int qh_open(int device, qh_ctx** out) {
   }
   c->scratch_bytes = 1 << 20;
   if (hipMalloc(&c->d_scratch, c->scratch_bytes) != hipSuccess ||
-      hipMemset(c->d_scratch, 0, c->scratch_bytes) != hipSuccess ||
+      hipMemsetAsync(c->d_scratch, 0, c->scratch_bytes, c->stream) != hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess ||
       hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
     hipFree(c->d_scratch);
     hipStreamDestroy(c->stream);

@@ -507,26 +507,31 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, c.state);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-  } else {
-    FusedArgs f{};
-    f.eps = m.eps;
-    f.w = m.lm_head;
-    f.in = c.x;
-    f.gain = m.final_norm;
-    f.out = c.logits;
-    f.partials = static_cast<ArgPair*>(c.lm_partials);
-    if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
-    if ((e = fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows,
-                                                     kLmMaxBlocks)) != hipSuccess)
-      return e;
-    // The pick gathers the next input row, so it is timed with the gathers.
-    if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_pick, dim3(1), dim3(kBlock), 0, s, static_cast<const ArgPair*>(c.lm_partials),
-                       lm_head_blocks(m), c.logits, c.state, c.tokens, c.pred, c.capacity, m.embed,
-                       m.hidden, m.vocab, c.x);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+  } else if ((e = enqueue_head(s, m, c, timer)) != hipSuccess) {
+    return e;
   }
   return mark(s, timer, QH_ROLE_COUNT);
+}
+
+hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer) {
+  hipError_t e;
+  FusedArgs f{};
+  f.eps = m.eps;
+  f.w = m.lm_head;
+  f.in = c.x;
+  f.gain = m.final_norm;
+  f.out = c.logits;
+  f.partials = static_cast<ArgPair*>(c.lm_partials);
+  if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
+  if ((e = fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, kLmMaxBlocks)) !=
+      hipSuccess)
+    return e;
+  // The pick gathers the next input row, so it is timed with the gathers.
+  if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
+  hipLaunchKernelGGL(k_pick, dim3(1), dim3(kBlock), 0, s, static_cast<const ArgPair*>(c.lm_partials),
+                     lm_head_blocks(m), c.logits, c.state, c.tokens, c.pred, c.capacity, m.embed, m.hidden,
+                     m.vocab, c.x);
+  return hipGetLastError();
 }
 
 }  // namespace qh

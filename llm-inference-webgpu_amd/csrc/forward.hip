@@ -1,0 +1,209 @@
+// The batched prefill forward: GpuModel.#forward (src/gpu/model.js:240-402) over
+// `seq` positions at once, each weight read once per 8-position tile
+// (QH_MATMUL_BATCHED, the reference's batchedMatvec, src/gpu/kernels.js:232-290,
+// selected by src/gpu/model.js:297-306) or once per prefill on the matrix cores
+// (QH_MATMUL_MFMA, prefill.hip).
+//
+// Per layer, over all positions: rmsnorm -> q|k|v matmul + bias -> rope (f64) with
+// the f16 K/V append -> attention (the decode step's algorithm for the model's
+// numerics, one query per position) -> o matmul, residual add -> rmsnorm -> gate|up
+// matmul -> swiglu -> down matmul, residual add. The last position's row then goes
+// through the decode step's own output head and pick.
+//
+// QH_MATMUL_BATCHED sums every output exactly as the decode step does (same
+// matvec summation order, same rope, attention and merge arithmetic, same f32
+// residual adds), so a prefill and the same positions decoded one by one give
+// the same bits -- the reference's prefill == incremental decode property
+// (README.md:256-272, web/model.html:169-198). QH_MATMUL_MFMA is held to a stated
+// tolerance instead.
+#include "attention.h"
+#include "device_common.h"
+#include "model_dev.h"
+
+namespace qh {
+
+// Rows of q|k|v (f32, bias included) at positions past+t: q and k heads rotated
+// as the decode step's QKV epilogue does (rope_pair over f64 angles), q to `q`,
+// k and v to the f16 caches. grid (ceil(items / 256), seq).
+__global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ q, uint16_t* __restrict__ kc,
+                          uint16_t* __restrict__ vt, const double* __restrict__ rope_cos,
+                          const double* __restrict__ rope_sin, int past, int heads, int kv_heads,
+                          int capacity, int vstride) {
+  const int t = blockIdx.y, pos = past + t;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int hidden = heads * kHeadDim, kvd = kv_heads * kHeadDim;
+  const float* row = qkv + (size_t)t * (hidden + 2 * kvd);
+  const int rope_pairs = (heads + kv_heads) * 32;
+  if (i < rope_pairs) {
+    const int head = i / 32, j = i % 32;
+    const int base = head < heads ? head * kHeadDim : hidden + (head - heads) * kHeadDim;
+    float lo, hi;
+    rope_pair(row[base + j], row[base + j + 32], rope_cos[(size_t)pos * 32 + j], rope_sin[(size_t)pos * 32 + j],
+              &lo, &hi);
+    if (head < heads) {
+      q[(size_t)t * hidden + head * kHeadDim + j] = lo;
+      q[(size_t)t * hidden + head * kHeadDim + j + 32] = hi;
+    } else {
+      uint16_t* k = kc + ((size_t)(head - heads) * capacity + pos) * kHeadDim;
+      k[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
+      k[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
+    }
+  } else if (i < rope_pairs + kvd) {
+    const int e = i - rope_pairs;  // kv head e/64, dimension e%64
+    vt[(size_t)e * vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)row[hidden + kvd + e]);
+  }
+}
+
+// The decode step's slot merge for every query: out [seq][heads*64]. grid (seq).
+__global__ __launch_bounds__(kBlock) void k_attn_merge_rows(const float* __restrict__ part, int heads,
+                                                            float* __restrict__ out) {
+  __shared__ float wl[kBlock];
+  const int t = blockIdx.x;
+  CombineIn in;
+  in.load(part + (size_t)t * heads * kDecodeSlots * kPartStride, heads);
+  const v4f acc = attn_combine_quad(in, wl);
+  const int i = threadIdx.x;
+  if (i < heads * kDecodeSlots) {
+    float* o = out + (size_t)t * heads * kHeadDim + (i / kDecodeSlots) * kHeadDim + 4 * (i % kDecodeSlots);
+    o[0] = acc.x;
+    o[1] = acc.y;
+    o[2] = acc.z;
+    o[3] = acc.w;
+  }
+}
+
+// h[t][j] = silu(g) * u over interleaved gate|up rows (g = gu[t][2j], u = gu[t][2j+1]), in
+// f64 as the decode step's SWIGLU epilogue (src/core/ops.js:81-91).
+__global__ void k_swiglu_pairs(const float* __restrict__ gu, float* __restrict__ h, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double g = gu[2 * i], u = gu[2 * i + 1];
+  h[i] = (float)(g / (1.0 + exp(-g)) * u);
+}
+
+// rows [seq][hidden] = bf16 embedding rows of tokens[past .. past+seq-1], widened exactly.
+__global__ void k_embed_rows(const uint16_t* __restrict__ embed, const int* __restrict__ tokens, int past,
+                             int hidden, int vocab, float* __restrict__ rows) {
+  const int t = blockIdx.x;
+  int tok = tokens[past + t];
+  tok = (tok < 0 || tok >= vocab) ? 0 : tok;  // ids are validated on the host
+  const uint16_t* src = embed + (size_t)tok * hidden;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+    rows[(size_t)t * hidden + i] = __builtin_bit_cast(float, (uint32_t)src[i] << 16);
+}
+
+int prefill_chunk(const ModelDev& m, const CacheDev& c) {
+  int p = c.capacity < kPrefillChunk ? c.capacity : kPrefillChunk;
+  if (m.numerics == QH_NUMERICS_EXACT && c.capacity > kPLds) {
+    // exact attention past kPLds keeps every query's scores: bound them to 64M floats
+    const size_t per = (size_t)m.heads * (c.score_stride + attn_spans(c.capacity));
+    const size_t fit = ((size_t)64 << 20) / per;
+    p = (int)std::max<size_t>(1, std::min<size_t>(p, fit));
+  }
+  return p;
+}
+
+PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
+  const size_t P = prefill_chunk(m, c);
+  const size_t d = m.hidden, kv = (size_t)m.kv_heads * m.head_dim, f = m.intermediate;
+  PrefillBytes b{};
+  b.floats = P * (5 * d + (d + 2 * kv) + 3 * f);
+  if (m.numerics == QH_NUMERICS_FAST) b.floats += P * m.heads * kDecodeSlots * kPartStride;
+  else if (c.capacity > kPLds) b.floats += P * m.heads * (c.score_stride + attn_spans(c.capacity));
+  b.counters = m.numerics == QH_NUMERICS_EXACT ? P * m.heads : 0;
+  size_t scratch = 0;
+  for (int L = 0; L < m.layers; L++) {
+    const LayerDev& l = m.layers_host[L];
+    for (const DMat* w : {&l.qkv, &l.o, &l.gu, &l.down}) {
+      scratch = std::max(scratch, matvec_x64_bytes(*w, (int)P));
+      if (matmul == QH_MATMUL_MFMA && w->format != QH_FMT_F16)
+        scratch = std::max(scratch, matmul_prefill_scratch_bytes(*w, (int)P));
+    }
+  }
+  b.scratch = scratch;
+  return b;
+}
+
+static hipError_t matmul(hipStream_t s, int mode, const DMat& w, const float* x, const float* bias, float* y,
+                         int seq, const PrefillDev& p) {
+  if (mode == QH_MATMUL_MFMA && w.format != QH_FMT_F16)
+    return launch_matmul_prefill(s, w, x, bias, y, seq, p.scratch);
+  return launch_matvec(s, w, x, bias, y, seq, static_cast<double*>(p.scratch));
+}
+
+hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p,
+                                  int mode, int past, int seq) {
+  hipError_t e;
+  const int d = m.hidden, kvd = m.kv_heads * m.head_dim, f = m.intermediate;
+  const size_t n = (size_t)seq * d;
+  for (int L = 0; L < m.layers; L++) {
+    const LayerDev& l = m.layers_host[L];
+    uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
+    uint16_t* vt = kc + c.key_elems;
+    if ((e = launch_rmsnorm(s, p.X, l.in_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
+    if ((e = matmul(s, mode, l.qkv, p.XN, l.qkv_bias, p.QKV, seq, p)) != hipSuccess) return e;
+    const int items = (m.heads + m.kv_heads) * 32 + kvd;
+    hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, p.Q, kc, vt, m.rope_cos,
+                       m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (m.numerics == QH_NUMERICS_FAST) {
+      SlotArgs a{};
+      a.q = p.Q;
+      a.kc = kc;
+      a.vt = vt;
+      a.part = p.part;
+      a.past = past;
+      a.capacity = c.capacity;
+      a.vstride = c.vstride;
+      a.heads = m.heads;
+      a.kv_heads = m.kv_heads;
+      a.max_slots = kDecodeSlots;
+      const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
+      hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, seq), dim3(kBlock),
+                         0, s, a);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+      hipLaunchKernelGGL(k_attn_merge_rows, dim3(seq), dim3(kBlock), 0, s, p.part, m.heads, p.ATT);
+    } else {
+      ExactArgs a{};
+      a.q = p.Q;
+      a.kc = kc;
+      a.vt = vt;
+      a.scores = p.scores;
+      a.score_stride = c.score_stride;
+      a.max_stride = attn_spans(c.capacity);
+      a.maxes = p.scores + (size_t)seq * m.heads * c.score_stride;
+      a.counters = p.counters;
+      a.out = p.ATT;
+      a.past = past;
+      a.capacity = c.capacity;
+      a.vstride = c.vstride;
+      a.heads = m.heads;
+      a.kv_heads = m.kv_heads;
+      // the kernel the decode step picks for this cache (the same arithmetic per query)
+      if (c.capacity <= kPLds) {
+        hipLaunchKernelGGL(k_attn_block, dim3(m.heads, seq), dim3(kAttnThreads), 0, s, a);
+      } else {
+        hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, seq), dim3(kBlock), 0, s, a);
+      }
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = matmul(s, mode, l.o, p.ATT, nullptr, p.Y, seq, p)) != hipSuccess) return e;
+    if ((e = launch_add(s, p.X, p.Y, (int)n)) != hipSuccess) return e;
+    if ((e = launch_rmsnorm(s, p.X, l.post_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
+    if ((e = matmul(s, mode, l.gu, p.XN, nullptr, p.GU, seq, p)) != hipSuccess) return e;
+    const size_t nh = (size_t)seq * f;
+    hipLaunchKernelGGL(k_swiglu_pairs, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, s, p.GU, p.H, nh);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = matmul(s, mode, l.down, p.H, nullptr, p.Y, seq, p)) != hipSuccess) return e;
+    if ((e = launch_add(s, p.X, p.Y, (int)n)) != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t enqueue_embed_rows(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p, int past,
+                              int seq) {
+  hipLaunchKernelGGL(k_embed_rows, dim3(seq), dim3(256), 0, s, m.embed, c.tokens, past, m.hidden, m.vocab, p.X);
+  return hipGetLastError();
+}
+
+}  // namespace qh

@@ -13,6 +13,7 @@
 // the token from device memory, so nothing is re-encoded per token.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdio>
 #include <cstring>
@@ -89,6 +90,7 @@ struct qh_model {
   int live_caches = 0;
   int caches_made = 0;
   int numerics = QH_NUMERICS_FAST;
+  int matmul = QH_MATMUL_BATCHED;
 
   int alloc(size_t n, void** p) {
     if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
@@ -115,6 +117,10 @@ struct qh_cache {
   float* d_hidden = nullptr;
   size_t hidden_cap = 0;
   int32_t* h_pinned = nullptr;  // [0..1] state staging, [2] argmax readback
+  // Batched-prefill workspace (allocated at the first batched forward).
+  qh::PrefillDev pw{};
+  qh::PrefillBytes pw_bytes{};
+  void* pw_mem = nullptr;
 
   int alloc(size_t n, void** p) {
     if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
@@ -232,16 +238,20 @@ int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t r
   s.group = format == QH_FMT_INT4 ? group : 0;
   const size_t nb = data_bytes(format, rows, cols);
   const size_t ns = format == QH_FMT_INT8 ? (size_t)rows : format == QH_FMT_INT4 ? (size_t)rows * (cols / group) : 0;
+  // Every copy and fill of the library goes on the context's stream, which does not
+  // synchronize with the null stream; the host arrays are borrowed, so wait before returning.
+  hipStream_t st = m->ctx->stream;
   bool ok = hipMalloc(&s.data, nb) == hipSuccess &&
-            hipMemcpy(s.data, h_data, nb, hipMemcpyHostToDevice) == hipSuccess;
+            hipMemcpyAsync(s.data, h_data, nb, hipMemcpyHostToDevice, st) == hipSuccess;
   if (ok && ns) {
     ok = hipMalloc((void**)&s.scales, ns * 4) == hipSuccess &&
-         hipMemcpy(s.scales, h_scales, ns * 4, hipMemcpyHostToDevice) == hipSuccess;
+         hipMemcpyAsync(s.scales, h_scales, ns * 4, hipMemcpyHostToDevice, st) == hipSuccess;
   }
   if (ok && format == QH_FMT_INT4) {
     ok = hipMalloc((void**)&s.zeros, ns * 4) == hipSuccess &&
-         hipMemcpy(s.zeros, h_zeros, ns * 4, hipMemcpyHostToDevice) == hipSuccess;
+         hipMemcpyAsync(s.zeros, h_zeros, ns * 4, hipMemcpyHostToDevice, st) == hipSuccess;
   }
+  ok = hipStreamSynchronize(st) == hipSuccess && ok;
   if (!ok) {
     free_staged(s);
     return fail(QH_ERR_NOMEM, "uploading %s failed", name);
@@ -278,11 +288,14 @@ int stack_rows(qh_model* m, const std::vector<const Staged*>& parts, qh::DMat* o
   if (!rc && a.format != QH_FMT_F16) rc = m->alloc(gpr * rows * 4, (void**)&scales);
   if (!rc && a.format == QH_FMT_INT4) rc = m->alloc(gpr * rows * 4, (void**)&zeros);
   if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
   size_t r0 = 0;
   for (const Staged* p : parts) {
-    QH_HIP(hipMemcpy((char*)data + r0 * rb, p->data, rb * p->rows, hipMemcpyDeviceToDevice));
-    if (scales) QH_HIP(hipMemcpy(scales + r0 * gpr, p->scales, gpr * p->rows * 4, hipMemcpyDeviceToDevice));
-    if (zeros) QH_HIP(hipMemcpy(zeros + r0 * gpr, p->zeros, gpr * p->rows * 4, hipMemcpyDeviceToDevice));
+    QH_HIP(hipMemcpyAsync((char*)data + r0 * rb, p->data, rb * p->rows, hipMemcpyDeviceToDevice, st));
+    if (scales)
+      QH_HIP(hipMemcpyAsync(scales + r0 * gpr, p->scales, gpr * p->rows * 4, hipMemcpyDeviceToDevice, st));
+    if (zeros)
+      QH_HIP(hipMemcpyAsync(zeros + r0 * gpr, p->zeros, gpr * p->rows * 4, hipMemcpyDeviceToDevice, st));
     r0 += p->rows;
   }
   return dmat_of(a, data, scales, zeros, rows, out);
@@ -301,15 +314,16 @@ int interleave_rows(qh_model* m, const Staged& a, const Staged& b, qh::DMat* out
   if (!rc && a.format != QH_FMT_F16) rc = m->alloc(gpr * rows * 4, (void**)&scales);
   if (!rc && a.format == QH_FMT_INT4) rc = m->alloc(gpr * rows * 4, (void**)&zeros);
   if (rc) return rc;
+  hipStream_t st = m->ctx->stream;
   for (int k = 0; k < 2; k++) {
     const Staged& s = k == 0 ? a : b;
-    QH_HIP(hipMemcpy2D((char*)data + k * rb, 2 * rb, s.data, rb, rb, s.rows, hipMemcpyDeviceToDevice));
+    QH_HIP(hipMemcpy2DAsync((char*)data + k * rb, 2 * rb, s.data, rb, rb, s.rows, hipMemcpyDeviceToDevice, st));
     if (scales)
-      QH_HIP(hipMemcpy2D((char*)scales + k * gpr * 4, 2 * gpr * 4, s.scales, gpr * 4, gpr * 4, s.rows,
-                         hipMemcpyDeviceToDevice));
+      QH_HIP(hipMemcpy2DAsync((char*)scales + k * gpr * 4, 2 * gpr * 4, s.scales, gpr * 4, gpr * 4, s.rows,
+                              hipMemcpyDeviceToDevice, st));
     if (zeros)
-      QH_HIP(hipMemcpy2D((char*)zeros + k * gpr * 4, 2 * gpr * 4, s.zeros, gpr * 4, gpr * 4, s.rows,
-                         hipMemcpyDeviceToDevice));
+      QH_HIP(hipMemcpy2DAsync((char*)zeros + k * gpr * 4, 2 * gpr * 4, s.zeros, gpr * 4, gpr * 4, s.rows,
+                              hipMemcpyDeviceToDevice, st));
   }
   return dmat_of(a, data, scales, zeros, rows, out);
 }
@@ -357,9 +371,12 @@ int qh_model_finalize(qh_model* m) {
     if ((rc = dmat_of(dn, dn.data, dn.scales, dn.zeros, dn.rows, &d.down))) return rc;
     float* bias = nullptr;
     if ((rc = m->alloc((size_t)(c.hidden + 2 * kv_dim) * 4, (void**)&bias))) return rc;
-    QH_HIP(hipMemcpy(bias, S[p + "self_attn.q_proj.bias"].data, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice));
-    QH_HIP(hipMemcpy(bias + c.hidden, S[p + "self_attn.k_proj.bias"].data, (size_t)kv_dim * 4, hipMemcpyDeviceToDevice));
-    QH_HIP(hipMemcpy(bias + c.hidden + kv_dim, S[p + "self_attn.v_proj.bias"].data, (size_t)kv_dim * 4, hipMemcpyDeviceToDevice));
+    hipStream_t st = m->ctx->stream;
+    QH_HIP(hipMemcpyAsync(bias, S[p + "self_attn.q_proj.bias"].data, (size_t)c.hidden * 4, hipMemcpyDeviceToDevice, st));
+    QH_HIP(hipMemcpyAsync(bias + c.hidden, S[p + "self_attn.k_proj.bias"].data, (size_t)kv_dim * 4,
+                          hipMemcpyDeviceToDevice, st));
+    QH_HIP(hipMemcpyAsync(bias + c.hidden + kv_dim, S[p + "self_attn.v_proj.bias"].data, (size_t)kv_dim * 4,
+                          hipMemcpyDeviceToDevice, st));
     d.qkv_bias = bias;
     d.in_norm = static_cast<const float*>(S[p + "input_layernorm.weight"].data);
     d.post_norm = static_cast<const float*>(S[p + "post_attention_layernorm.weight"].data);
@@ -393,6 +410,8 @@ int qh_model_finalize(qh_model* m) {
   m->keep(em.data);
   m->bytes += data_bytes(QH_FMT_BF16, em.rows, em.cols);
   em = Staged{};
+  // The stacking copies read the staged buffers: let them finish before freeing those.
+  QH_HIP(hipStreamSynchronize(m->ctx->stream));
   for (auto& n : consumed) free_staged(m->staged[n]);
   m->staged.clear();
 
@@ -402,8 +421,9 @@ int qh_model_finalize(qh_model* m) {
   qh::rope_tables_f64(c.head_dim, c.rope_theta, c.max_positions, cs.data(), sn.data());
   double *dcos = nullptr, *dsin = nullptr;
   if ((rc = m->alloc(cs.size() * 8, (void**)&dcos)) || (rc = m->alloc(sn.size() * 8, (void**)&dsin))) return rc;
-  QH_HIP(hipMemcpy(dcos, cs.data(), cs.size() * 8, hipMemcpyHostToDevice));
-  QH_HIP(hipMemcpy(dsin, sn.data(), sn.size() * 8, hipMemcpyHostToDevice));
+  QH_HIP(hipMemcpyAsync(dcos, cs.data(), cs.size() * 8, hipMemcpyHostToDevice, m->ctx->stream));
+  QH_HIP(hipMemcpyAsync(dsin, sn.data(), sn.size() * 8, hipMemcpyHostToDevice, m->ctx->stream));
+  QH_HIP(hipStreamSynchronize(m->ctx->stream));
 
   qh::ModelDev& d = m->dev;
   d.hidden = c.hidden;
@@ -433,6 +453,14 @@ int qh_model_set_numerics(qh_model* m, int32_t numerics) {
            "fast numerics supports at most 16 query heads (got %d)", m->cfg.heads);
   m->numerics = numerics;
   m->dev.numerics = numerics;
+  return QH_OK;
+}
+
+int qh_model_set_matmul(qh_model* m, int32_t matmul) {
+  QH_CHECK(m, QH_ERR_INVALID, "model is NULL");
+  QH_CHECK(matmul == QH_MATMUL_BATCHED || matmul == QH_MATMUL_MATVEC || matmul == QH_MATMUL_MFMA,
+           QH_ERR_INVALID, "unknown matmul mode %d", matmul);
+  m->matmul = matmul;
   return QH_OK;
 }
 
@@ -491,10 +519,11 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
     rc = fail(QH_ERR_NOMEM, "pinned allocation failed");
   }
-  if (!rc && (hipMemset(d.kv, 0, kv_bytes) != hipSuccess || hipMemset(d.state, 0, 256) != hipSuccess ||
-              hipMemset(d.tokens, 0, (size_t)(capacity + 1) * 4) != hipSuccess ||
-              hipMemset(d.pred, 0, (size_t)capacity * 4) != hipSuccess ||
-              hipMemset(d.attn_counters, 0, 256) != hipSuccess)) {
+  hipStream_t st = m->ctx->stream;  // ordered before every later use of the cache
+  if (!rc && (hipMemsetAsync(d.kv, 0, kv_bytes, st) != hipSuccess || hipMemsetAsync(d.state, 0, 256, st) != hipSuccess ||
+              hipMemsetAsync(d.tokens, 0, (size_t)(capacity + 1) * 4, st) != hipSuccess ||
+              hipMemsetAsync(d.pred, 0, (size_t)capacity * 4, st) != hipSuccess ||
+              hipMemsetAsync(d.attn_counters, 0, 256, st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)) {
     rc = fail(QH_ERR_DEVICE, "clearing the cache failed");
   }
   d.lm_blocks = qh::lm_head_blocks(md);
@@ -519,6 +548,7 @@ int qh_cache_free(qh_cache* c) {
   if (c->graph) hipGraphDestroy(c->graph);
   for (void* p : c->allocs) hipFree(p);
   hipFree(c->d_hidden);
+  if (c->pw_mem) hipFree(c->pw_mem);
   hipHostFree(c->h_pinned);
   c->m->live_caches--;
   delete c;
@@ -547,8 +577,9 @@ int qh_cache_present(qh_cache* c, int32_t layer, float* h_key, float* h_value) {
   QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight");
   const qh::CacheDev& d = c->dev;
   std::vector<uint16_t> buf(d.layer_elems);
+  QH_HIP(hipMemcpyAsync(buf.data(), d.kv + (size_t)layer * d.layer_elems, buf.size() * 2, hipMemcpyDeviceToHost,
+                        c->m->ctx->stream));
   QH_HIP(hipStreamSynchronize(c->m->ctx->stream));
-  QH_HIP(hipMemcpy(buf.data(), d.kv + (size_t)layer * d.layer_elems, buf.size() * 2, hipMemcpyDeviceToHost));
   const int n = c->length, hd = md.head_dim;
   const uint16_t* vt = buf.data() + d.key_elems;
   for (int h = 0; h < md.kv_heads; h++) {
@@ -597,6 +628,77 @@ int finish_forward(qh_cache* c, int seq, float* h_logits, int32_t* h_argmax) {
   return QH_OK;
 }
 
+// The batched-prefill workspace for the model's current matmul mode: one allocation,
+// carved in the order prefill_bytes() counts it.
+int ensure_prefill(qh_cache* c) {
+  qh_model* m = c->m;
+  const qh::PrefillBytes b = qh::prefill_bytes(m->dev, c->dev, m->matmul);
+  if (c->pw_mem && b.floats <= c->pw_bytes.floats && b.counters <= c->pw_bytes.counters &&
+      b.scratch <= c->pw_bytes.scratch)
+    return QH_OK;
+  hipStream_t s = m->ctx->stream;
+  QH_HIP(hipStreamSynchronize(s));
+  if (c->pw_mem) hipFree(c->pw_mem);
+  c->pw_mem = nullptr;
+  const size_t fbytes = (b.floats * 4 + 255) & ~(size_t)255, cbytes = (b.counters * 4 + 255) & ~(size_t)255;
+  if (hipMalloc(&c->pw_mem, fbytes + cbytes + b.scratch + 256) != hipSuccess) {
+    c->pw_mem = nullptr;
+    return fail(QH_ERR_NOMEM, "prefill workspace of %zu bytes", fbytes + cbytes + b.scratch);
+  }
+  QH_HIP(hipMemsetAsync(static_cast<char*>(c->pw_mem) + fbytes, 0, cbytes, s));
+  c->pw_bytes = b;
+  const qh::ModelDev& d = m->dev;
+  const size_t P = qh::prefill_chunk(d, c->dev);
+  const size_t hd = d.hidden, kv = (size_t)d.kv_heads * d.head_dim, f = d.intermediate;
+  float* p = static_cast<float*>(c->pw_mem);
+  qh::PrefillDev& w = c->pw;
+  w.positions = (int)P;
+  w.X = p, p += P * hd;
+  w.XN = p, p += P * hd;
+  w.Q = p, p += P * hd;
+  w.ATT = p, p += P * hd;
+  w.Y = p, p += P * hd;
+  w.QKV = p, p += P * (hd + 2 * kv);
+  w.GU = p, p += P * 2 * f;
+  w.H = p, p += P * f;
+  w.part = w.scores = p;
+  w.counters = reinterpret_cast<int*>(static_cast<char*>(c->pw_mem) + fbytes);
+  w.scratch = static_cast<char*>(c->pw_mem) + fbytes + cbytes;
+  return QH_OK;
+}
+
+// forward() over seq > 1 positions, batched: the input rows (host `h_hidden`, else the
+// cache's tokens) pass through the layers in chunks, then the last row through the head.
+int batched_forward(qh_cache* c, const float* h_hidden, int seq, bool want, int forced) {
+  qh_model* m = c->m;
+  int rc = ensure_prefill(c);
+  if (rc) return rc;
+  hipStream_t s = m->ctx->stream;
+  const qh::ModelDev& d = m->dev;
+  const int P = c->pw.positions;
+  int n = 0;
+  for (int done = 0; done < seq; done += n) {
+    n = std::min(P, seq - done);
+    const int past = c->length + done;
+    if (h_hidden) {
+      QH_HIP(hipMemcpyAsync(c->pw.X, h_hidden + (size_t)done * d.hidden, (size_t)n * d.hidden * 4,
+                            hipMemcpyHostToDevice, s));
+    } else {
+      QH_HIP(qh::enqueue_embed_rows(s, d, c->dev, c->pw, past, n));
+    }
+    QH_HIP(qh::enqueue_prefill_layers(s, d, c->dev, c->pw, m->matmul, past, n));
+  }
+  QH_HIP(hipMemcpyAsync(c->dev.x, c->pw.X + (size_t)(n - 1) * d.hidden, (size_t)d.hidden * 4,
+                        hipMemcpyDeviceToDevice, s));
+  if (want) {
+    if ((rc = set_state(c, c->length + seq - 1, forced))) return rc;
+    QH_HIP(qh::enqueue_head(s, d, c->dev));
+  } else if ((rc = set_state(c, c->length + seq, forced))) {
+    return rc;
+  }
+  return QH_OK;
+}
+
 struct BusyGuard {
   qh_cache* c;
   explicit BusyGuard(qh_cache* c_) : c(c_) { c->busy = true; }
@@ -617,6 +719,11 @@ int qh_forward(qh_model* m, qh_cache* c, const float* h_hidden, int32_t seq, flo
   BusyGuard guard(c);
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
+  const bool want = h_logits || h_argmax;
+  if (seq > 1 && m->matmul != QH_MATMUL_MATVEC) {
+    if ((rc = batched_forward(c, h_hidden, seq, want, INT_MAX))) return rc;
+    return finish_forward(c, seq, h_logits, h_argmax);
+  }
   const size_t need = (size_t)seq * m->dev.hidden * 4;
   if (need > c->hidden_cap) {
     QH_HIP(hipStreamSynchronize(s));
@@ -628,7 +735,6 @@ int qh_forward(qh_model* m, qh_cache* c, const float* h_hidden, int32_t seq, flo
   }
   QH_HIP(hipMemcpyAsync(c->d_hidden, h_hidden, need, hipMemcpyHostToDevice, s));
   if ((rc = set_state(c, c->length, INT_MAX))) return rc;
-  const bool want = h_logits || h_argmax;
   for (int t = 0; t < seq; t++) {
     QH_HIP(hipMemcpyAsync(c->dev.x, c->d_hidden + (size_t)t * m->dev.hidden, (size_t)m->dev.hidden * 4,
                           hipMemcpyDeviceToDevice, s));
@@ -652,8 +758,12 @@ int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t se
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
   QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, h_ids, (size_t)seq * 4, hipMemcpyHostToDevice, s));
-  if ((rc = set_state(c, c->length, c->length + seq))) return rc;
   const bool want = h_logits || h_argmax;
+  if (seq > 1 && m->matmul != QH_MATMUL_MATVEC) {
+    if ((rc = batched_forward(c, nullptr, seq, want, c->length + seq))) return rc;
+    return finish_forward(c, seq, h_logits, h_argmax);
+  }
+  if ((rc = set_state(c, c->length, c->length + seq))) return rc;
   for (int t = 0; t < seq; t++) {
     QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, want && t == seq - 1));
   }
@@ -763,7 +873,8 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
     }
   }
   if (err == hipSuccess && h_tokens) {
-    err = hipMemcpy(h_tokens, c->dev.pred + start, (size_t)steps * 4, hipMemcpyDeviceToHost);
+    err = hipMemcpyAsync(h_tokens, c->dev.pred + start, (size_t)steps * 4, hipMemcpyDeviceToHost, s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
   }
   for (auto& e : ev) hipEventDestroy(e);
   if (rc) return rc;

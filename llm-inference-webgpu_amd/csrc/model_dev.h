@@ -5,6 +5,8 @@
 // launchers in decode.hip.
 #pragma once
 
+#include <algorithm>
+
 #include "qh_internal.h"
 
 namespace qh {
@@ -69,11 +71,44 @@ struct StepTimer {
   int n;         // events recorded
 };
 
+// Workspace of the batched prefill for up to prefill_chunk() positions.
+struct PrefillDev {
+  int positions;       // rows every buffer holds
+  float* X;            // [P][hidden] residual stream
+  float* XN;           // [P][hidden] normalized
+  float* QKV;          // [P][hidden + 2*kv_dim]
+  float* Q;            // [P][hidden] rotated queries
+  float* ATT;          // [P][hidden]
+  float* Y;            // [P][hidden] o / down outputs
+  float* GU;           // [P][2*intermediate] interleaved gate|up
+  float* H;            // [P][intermediate]
+  float* part;         // fast: [P][heads][kDecodeSlots][kPartStride] attention slot partials
+  float* scores;       // exact past kPLds: [P][heads][score_stride] + [P][heads][spans]
+  int* counters;       // exact: [P][heads], zero between launches
+  void* scratch;       // matmul scratch (f64 activations, MFMA splits)
+};
+struct PrefillBytes {
+  size_t floats, counters, scratch;
+};
+constexpr int kPrefillChunk = 512;  // positions per batched prefill pass
+// Positions per pass for this model and cache, and the workspace it needs.
+int prefill_chunk(const ModelDev& m, const CacheDev& c);
+PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul);
+// Layers of positions past .. past+seq-1 over p.X (seq <= p.positions), writing the KV cache.
+hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p,
+                                  int matmul, int past, int seq);
+// p.X = embeddings of cache tokens[past .. past+seq-1].
+hipError_t enqueue_embed_rows(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p, int past,
+                              int seq);
+
 // Launches one decode position: [gather] -> layers -> (lm_head, then the argmax
 // pick that advances the position and gathers the next input row; or a position
 // advance alone when `logits` is false).
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
                         bool logits, StepTimer* timer = nullptr);
+// The output head of the position state[0] over cache.x: final rmsnorm, lm_head, logits and
+// the pick (token recorded, position advanced, next input row gathered).
+hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer = nullptr);
 // cache.x = the embedding of tokens[position] (what STEP_GATHER starts with).
 hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c);
 // Launches in one step with logits (the events a StepTimer needs, minus the final one).

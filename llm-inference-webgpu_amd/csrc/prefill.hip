@@ -5,17 +5,18 @@
 // src/gpu/kernels.js:232-290); this is the M = 512 contraction that replaces it.
 //
 // Arithmetic. A weight code is an exact bf16: int8 q in [-127, 127], int4
-// (level - zero) in [-15, 15]. The activation is split into two bf16 terms,
-// x = hi + lo + r with |r| <= 2^-17 |x| (hi = bf16(x), lo = bf16(x - hi)), and
-// both terms go through v_mfma_f32_16x16x32_bf16 into one f32 accumulator, so
-// every product is exact and only the f32 accumulation rounds. The scale is
+// (level - zero) in [-15, 15]. The activation is split into three bf16 terms
+// that sum to it exactly (x = t0 + t1 + t2: t0 = bf16(x), t1 = bf16(x - t0),
+// t2 = x - t0 - t1, each difference exact in f32 and the last one 8 significant
+// bits), and all three go through v_mfma_f32_16x16x32_bf16 into one f32
+// accumulator, so every product is exact and only the f32 accumulation rounds. The scale is
 // factored out of the code sum: per output column for int8, per 128-column group
 // for int4 (the group's partial sum is scaled into the running total). The
 // reference's own GPU path accumulates in f32 as well (kernels.js:56-76).
 //
 // Tiling. A block computes a 64 (positions) x 64 (weight rows) tile with four
 // waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16), stepping K by 32: each step the
-// block stages the two activation terms (64 x 32 bf16 each) and the weights,
+// block stages the three activation terms (64 x 32 bf16 each) and the weights,
 // widened to bf16 (64 x 32), in LDS rows padded by 16 bytes, while the next
 // step's global loads are already in flight in registers. Long K is split over
 // gridDim.z; partial tiles are summed in a fixed order by k_gemm_finish.
@@ -29,12 +30,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGM = 64, kGN = 64, kGK = 32;
+constexpr int kTerms = 3;       // bf16 terms of an activation
 constexpr int kGRow = kGK + 8;  // bf16 per LDS row: 64 bytes + 16 of padding
 
 struct GemmArgs {
   DMat w;                 // int8 | int4, rows = N, cols = K
-  const uint16_t* xh;     // bf16 [M][K]: hi term
-  const uint16_t* xl;     // bf16 [M][K]: lo term
+  const uint16_t* xt;     // bf16 [kTerms][M][K]: the activation's terms
   float* out;             // splits == 1: Y [M][N]; else partials [splits][M][N]
   const float* bias;      // [N] or NULL (splits == 1 only)
   int M, N, K;
@@ -51,16 +52,17 @@ __device__ __forceinline__ uint32_t small_int_bf16(int v) {
   return __builtin_bit_cast(uint32_t, (float)v) >> 16;
 }
 
-// The activation split: hi = bf16(x), lo = bf16(x - hi).
-__global__ void k_split_bf16(const float* __restrict__ x, uint16_t* __restrict__ hi,
-                             uint16_t* __restrict__ lo, size_t n) {
+// The activation split: t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1) = x - t0 - t1.
+__global__ void k_split_bf16(const float* __restrict__ x, uint16_t* __restrict__ t, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float v = x[i];
-  const uint32_t h = bf16_bits_rne(v);
-  const float r = v - __builtin_bit_cast(float, h << 16);  // exact
-  hi[i] = (uint16_t)h;
-  lo[i] = (uint16_t)bf16_bits_rne(r);
+  float r = x[i];
+#pragma unroll
+  for (int k = 0; k < kTerms; k++) {
+    const uint32_t b = bf16_bits_rne(r);
+    t[(size_t)k * n + i] = (uint16_t)b;
+    r -= __builtin_bit_cast(float, b << 16);  // exact
+  }
 }
 
 // Weights of one K step for thread t: row n0 + t/4, columns k0 + 8*(t%4) .. +7,
@@ -100,7 +102,7 @@ __device__ __forceinline__ v4u wstep_widen(const WStep<FMT>& s) {
 
 template <int FMT>
 __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kGM][kGRow];  // hi, lo
+  __shared__ __attribute__((aligned(16))) uint16_t As[kTerms][kGM][kGRow];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[kGN][kGRow];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
@@ -116,11 +118,16 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a) {
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 15, fk = 8 * (lane >> 4);  // fragment row and k offset
 
-  f32x4 acc[2][2], grp[2][2];
+  f32x4 grp[2][2];
+  double acc[2][2][4];
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) acc[i][j] = grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 2; j++) {
+      grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0;
+    }
 
   // Column scales of this lane's output columns (int8: one per row of W).
   float cs[2] = {1.f, 1.f};
@@ -128,63 +135,62 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; j++) cs[j] = a.w.scales[min(n0 + wn * 32 + 16 * j + fr, a.N - 1)];
   }
-  const int group_steps = FMT == QH_FMT_INT4 ? a.w.cpg : 1;  // K steps per int4 group
+  // K steps per f32 partial: an int4 group, else 128 columns.
+  const int group_steps = FMT == QH_FMT_INT4 ? a.w.cpg : 4;
 
-  v4u xa_h, xa_l;
+  const size_t tstride = (size_t)a.M * a.K;  // elements between activation terms
+  v4u xa[kTerms];
   WStep<FMT> ws;
   if (s0 < s1) {
     const int k = s0 * kGK + sc;
-    xa_h = *reinterpret_cast<const v4u*>(a.xh + arow + k);
-    xa_l = *reinterpret_cast<const v4u*>(a.xl + arow + k);
+#pragma unroll
+    for (int t = 0; t < kTerms; t++) xa[t] = *reinterpret_cast<const v4u*>(a.xt + t * tstride + arow + k);
     wstep_load<FMT>(a.w, brow, k, ws);
   }
   for (int st = s0; st < s1; st++) {
-    *reinterpret_cast<v4u*>(&As[0][sr][sc]) = xa_h;
-    *reinterpret_cast<v4u*>(&As[1][sr][sc]) = xa_l;
+#pragma unroll
+    for (int t = 0; t < kTerms; t++) *reinterpret_cast<v4u*>(&As[t][sr][sc]) = xa[t];
     *reinterpret_cast<v4u*>(&Bs[sr][sc]) = wstep_widen<FMT>(ws);
     __syncthreads();
     if (st + 1 < s1) {  // next step's loads in flight during this step's MFMAs
       const int k = (st + 1) * kGK + sc;
-      xa_h = *reinterpret_cast<const v4u*>(a.xh + arow + k);
-      xa_l = *reinterpret_cast<const v4u*>(a.xl + arow + k);
+#pragma unroll
+      for (int t = 0; t < kTerms; t++) xa[t] = *reinterpret_cast<const v4u*>(a.xt + t * tstride + arow + k);
       wstep_load<FMT>(a.w, brow, k, ws);
     }
-    bf16x8 fa[2][2], fb[2];
+    bf16x8 fa[kTerms][2], fb[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      fa[0][i] = *reinterpret_cast<const bf16x8*>(&As[0][wm * 32 + 16 * i + fr][fk]);
-      fa[1][i] = *reinterpret_cast<const bf16x8*>(&As[1][wm * 32 + 16 * i + fr][fk]);
+#pragma unroll
+      for (int t = 0; t < kTerms; t++)
+        fa[t][i] = *reinterpret_cast<const bf16x8*>(&As[t][wm * 32 + 16 * i + fr][fk]);
       fb[i] = *reinterpret_cast<const bf16x8*>(&Bs[wn * 32 + 16 * i + fr][fk]);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++)
 #pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int t = 0; t < kTerms; t++)
+          grp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[t][i], fb[j], grp[i][j], 0, 0, 0);
+    if ((st + 1) % group_steps == 0 || st + 1 == s1) {  // fold the f32 partial into the f64 total
+      const int g = st / group_steps;
+#pragma unroll
       for (int j = 0; j < 2; j++) {
-        grp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[0][i], fb[j], grp[i][j], 0, 0, 0);
-        grp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[1][i], fb[j], grp[i][j], 0, 0, 0);
-      }
-    if constexpr (FMT == QH_FMT_INT4) {
-      if ((st + 1) % group_steps == 0) {  // end of a group: scale its partial sums in
-        const int g = st / group_steps;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
+        double sg = 1.0;
+        if constexpr (FMT == QH_FMT_INT4) {
           const int n = min(n0 + wn * 32 + 16 * j + fr, a.N - 1);
-          const float sg = a.w.scales[(size_t)n * a.w.gpr + g];
+          sg = a.w.scales[(size_t)n * a.w.gpr + g];
+        }
 #pragma unroll
-          for (int i = 0; i < 2; i++) {
-            acc[i][j] += sg * grp[i][j];
-            grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
+        for (int i = 0; i < 2; i++) {
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[i][j][r] += sg * (double)grp[i][j][r];
+          grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
       }
     }
     __syncthreads();
-  }
-  if constexpr (FMT == QH_FMT_INT8) {
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int j = 0; j < 2; j++) acc[i][j] = cs[j] * grp[i][j];
   }
 
   // D fragment: lane holds rows 4*(lane/16) .. +3 of column lane%16 of each tile.
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 32 + 16 * i + 4 * (lane >> 4) + r;
-        if (m < a.M) dst[(size_t)m * a.N + n] = acc[i][j][r] + b;
+        if (m < a.M) dst[(size_t)m * a.N + n] = (float)(acc[i][j][r] * (double)cs[j] + (double)b);
       }
     }
   }
@@ -230,7 +236,7 @@ static int gemm_steps_per_split(const DMat& w, int M) {
 }
 
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
-  const size_t split_bytes = (size_t)M * w.cols * 2 * sizeof(uint16_t);
+  const size_t split_bytes = (size_t)M * w.cols * kTerms * sizeof(uint16_t);
   const int steps = w.cols / kGK;
   const int per = gemm_steps_per_split(w, M);
   const int splits = (steps + per - 1) / per;
@@ -241,19 +247,17 @@ size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias,
                                  float* y, int M, void* scratch) {
   const size_t nx = (size_t)M * w.cols;
-  uint16_t* xh = static_cast<uint16_t*>(scratch);
-  uint16_t* xl = xh + nx;
-  hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, s, x, xh, xl, nx);
+  uint16_t* xt = static_cast<uint16_t*>(scratch);
+  hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, s, x, xt, nx);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int steps = w.cols / kGK;
   const int per = gemm_steps_per_split(w, M);
   const int splits = (steps + per - 1) / per;
-  float* part = reinterpret_cast<float*>(static_cast<char*>(scratch) + ((nx * 2 * sizeof(uint16_t) + 255) & ~(size_t)255));
+  float* part = reinterpret_cast<float*>(static_cast<char*>(scratch) + ((nx * kTerms * sizeof(uint16_t) + 255) & ~(size_t)255));
   GemmArgs a{};
   a.w = w;
-  a.xh = xh;
-  a.xl = xl;
+  a.xt = xt;
   a.out = splits > 1 ? part : y;
   a.bias = splits > 1 ? nullptr : bias;
   a.M = M;

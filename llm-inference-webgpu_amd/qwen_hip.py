@@ -26,6 +26,7 @@ LIB_PATH = os.path.join(HERE, "libqwen_hip.so")
 QH_OK, QH_ERR_INVALID, QH_ERR_RANGE, QH_ERR_BUSY, QH_ERR_DEVICE, QH_ERR_NOMEM, QH_ERR_STATE = range(7)
 FMT_F32, FMT_F16, FMT_INT8, FMT_INT4, FMT_BF16 = range(5)
 NUMERICS = {"fast": 0, "exact": 1}
+MATMUL = {"batched": 0, "matvec": 1, "mfma": 2}
 FORMAT_OF = {"f32": FMT_F32, "f16": FMT_F16, "int8": FMT_INT8, "int4": FMT_INT4, "bf16": FMT_BF16}
 # Kernel roles of a decode step, in QH_ROLE_* order.
 ROLES = ("embed", "qkv", "attention", "oproj", "gateup", "down", "head")
@@ -149,7 +150,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_model_create": [vp, vp, vp],
         "qh_model_set_tensor": [vp, ctypes.c_char_p, i32, i32, i32, i32, vp, vp, vp],
         "qh_model_finalize": [vp], "qh_model_free": [vp], "qh_model_bytes": [vp, vp],
-        "qh_model_set_numerics": [vp, i32],
+        "qh_model_set_numerics": [vp, i32], "qh_model_set_matmul": [vp, i32],
         "qh_cache_create": [vp, i32, vp], "qh_cache_free": [vp], "qh_cache_length": [vp, vp],
         "qh_cache_set_length": [vp, i32], "qh_cache_present": [vp, i32, vp, vp],
         "qh_forward": [vp, vp, vp, i32, vp, vp], "qh_forward_tokens": [vp, vp, vp, i32, vp, vp],
@@ -495,9 +496,12 @@ class GpuModel:
 
     @staticmethod
     def load(ctx: GpuContext, tensors: dict, config: ModelConfig, maxPositions: int = 2048,
-             onProgress=None, numerics: str = "fast") -> "GpuModel":
+             onProgress=None, numerics: str = "fast", matmul: str = "batched") -> "GpuModel":
         """Upload device tensors (see device_tensors) and finalize. numerics: "fast"
-        (split-K f32 attention) or "exact" (the CPU path's arithmetic, bit for bit)."""
+        (split-K f32 attention) or "exact" (the CPU path's arithmetic, bit for bit).
+        matmul: how forward() runs several positions -- "batched" (8-position weight
+        tiles, bitwise equal to decoding them one by one), "matvec" (one decode step per
+        position) or "mfma" (bf16 matrix cores for int8/int4 weights)."""
         lib = ctx.lib
         h = ctypes.c_void_p()
         cc = config.c_config(maxPositions)
@@ -505,6 +509,7 @@ class GpuModel:
         model = GpuModel(ctx, h.value, config, maxPositions)
         try:
             _check(lib.qh_model_set_numerics(h.value, NUMERICS[numerics]))
+            _check(lib.qh_model_set_matmul(h.value, MATMUL[matmul]))
             total = len(tensors)
             for i, (name, (fmt, rows, cols, group, data, scales, zeros)) in enumerate(tensors.items()):
                 data = np.ascontiguousarray(data)
@@ -519,6 +524,10 @@ class GpuModel:
             lib.qh_model_free(h.value)
             raise
         return model
+
+    def set_matmul(self, matmul: str) -> None:
+        """Switch forward()'s multi-position mode ("batched" | "matvec" | "mfma")."""
+        _check(self.lib.qh_model_set_matmul(self.handle, MATMUL[matmul]))
 
     @property
     def device_bytes(self) -> int:
