@@ -103,45 +103,38 @@ class _Ptr:
         self.ptr = ptr
 
 
-def attention_sweep(ctx, contexts=(128, 1024, 4096, 32768), heads=14, kv_heads=2, rounds=3):
-    """Config 3: one query over an f16 K/V cache (N(0,1) values) at each context, timed per call
-    over a rotation of distinct caches totalling >= 512 MiB (larger than the last-level cache).
-    Algorithmic bytes per call: K and V (512 B per position over both kv heads) + q and out."""
+def attention_sweep(ctx, contexts=(128, 1024, 4096, 32768), heads=14, kv_heads=2, reps=5):
+    """Config 3: one query (position ctx-1) against f16 K/V caches of N(0,1) values, through the
+    list form of the split-K operator: one launch over a rotation of distinct caches totalling
+    >= 512 MiB (larger than the last-level cache). Algorithmic bytes per cache: K and V (512 B
+    per position over both kv heads) + q read + out written."""
     out = {}
     rng = np.random.default_rng(3)
     for n_ctx in contexts:
         cap = n_ctx
         vstride = (cap + 7) // 8 * 8
         k_elems, v_elems = kv_heads * cap * 64, kv_heads * 64 * vstride
-        per = 2 * (k_elems + v_elems)
-        copies = int(np.ceil((512 << 20) / per))
-        block = rng.standard_normal(min(k_elems + v_elems, 1 << 22)).astype(np.float16)
-        reps = int(np.ceil(copies * (k_elems + v_elems) / block.size))
-        buf = ctx.upload(np.tile(block, reps)[:copies * (k_elems + v_elems)])
+        per = k_elems + v_elems
+        copies = int(np.ceil((512 << 20) / (2 * per)))
+        block = rng.standard_normal(min(per, 1 << 22)).astype(np.float16)
+        buf = ctx.upload(np.tile(block, int(np.ceil(copies * per / block.size)))[:copies * per])
         q = ctx.upload(rng.standard_normal(heads * 64).astype(np.float32))
-        o = ctx.empty(heads * 64 * 4)
+        o = ctx.empty(copies * heads * 64 * 4)
         algo = 2 * 2 * kv_heads * 64 * n_ctx + 2 * heads * 64 * 4
-        res = {}
-        for name, splitk in (("splitk", True), ("exact", False)):
-            def call(i):
-                base = buf.ptr + i * per
-                ctx.attention(q, _Ptr(base), _Ptr(base + 2 * k_elems), cap, o, 1, n_ctx - 1, heads, kv_heads,
-                              splitk=splitk)
-            for i in range(min(copies, 64)):
-                call(i)   # warm
-            ctx.done()
-            e0, e1 = ctx.event(), ctx.event()
-            ctx.record(e0)
-            for r in range(rounds):
-                for i in range(copies):
-                    call(i)
-            ctx.record(e1)
-            ms = ctx.elapsed_ms(e0, e1) / (rounds * copies)
-            ctx.destroy_event(e0), ctx.destroy_event(e1)
-            res[name] = {"us_per_call": round(ms * 1e3, 3), "GBps": round(algo / (ms * 1e-3) / 1e9, 1)}
-        out[str(n_ctx)] = {"caches": copies, "bytes_per_call": algo, **res}
-        log(f"attention ctx {n_ctx} x{copies}: split-K {res['splitk']['us_per_call']} us, "
-            f"exact {res['exact']['us_per_call']} us per call")
+        kc, vc = _Ptr(buf.ptr), _Ptr(buf.ptr + 2 * k_elems)
+        ctx.attention_list(q, kc, vc, per, per, copies, cap, o, n_ctx - 1, heads, kv_heads)   # warm
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0)
+        for _ in range(reps):
+            ctx.attention_list(q, kc, vc, per, per, copies, cap, o, n_ctx - 1, heads, kv_heads)
+        ctx.record(e1)
+        ms = ctx.elapsed_ms(e0, e1) / reps
+        ctx.destroy_event(e0), ctx.destroy_event(e1)
+        gbs = copies * algo / (ms * 1e-3) / 1e9
+        out[str(n_ctx)] = {"caches": copies, "bytes_per_launch": copies * algo,
+                           "us_per_launch": round(ms * 1e3, 2), "us_per_cache": round(ms * 1e3 / copies, 4),
+                           "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"attention ctx {n_ctx} x{copies}: {gbs:.0f} GB/s, {ms * 1e3 / copies:.3f} us per cache")
         for b in (buf, q, o):
             b.free()
     return out
@@ -291,11 +284,15 @@ def main():
                          "launches_per_token": n // psteps,
                          "GBps": round(rb[r] * n / (tot_ms * 1e-3) / 1e9, 1)}
     dominant = max(per_kernel, key=lambda r: per_kernel[r]["us_per_token"])
-    dk = per_kernel[dominant]
-    achieved = rb[dominant] / (dk["us_per_launch"] * 1e-6) / 1e9
+    # The dominant kernel's own duration: 240 of the step's launches of it back to back on the
+    # library's stream between two events (no event between launches), at the next position.
+    cache.length = args.context + psteps
+    kernel_us = model.kernel_time(cache, dominant, 240)
+    kbytes = role_bytes(cfg, args.context + psteps)[dominant]
+    achieved = kbytes / (kernel_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": None, "bytes_per_launch": rb[dominant]}
+                "traffic": None, "bytes_per_launch": kbytes, "us_per_launch": round(kernel_us, 3)}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
     iso = attn = prefill = None

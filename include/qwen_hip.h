@@ -165,6 +165,15 @@ int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cac
                         int32_t seq, int32_t past, int32_t heads, int32_t kv_heads,
                         int32_t head_dim);
 
+/* qh_attention_splitk for one query (position `past`) against `count` caches of the same shape
+ * in one launch: key cache i at d_key_cache + i*key_stride, value cache i at d_value_cache +
+ * i*value_stride (f16 elements); out [count][heads*head_dim]. How a working set of caches larger
+ * than the last-level cache is streamed (no counterpart in the reference). */
+int qh_attention_splitk_list(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                             const uint16_t* d_value_cache, size_t key_stride, size_t value_stride,
+                             int32_t count, int32_t capacity, float* d_out, int32_t past, int32_t heads,
+                             int32_t kv_heads, int32_t head_dim);
+
 /* SWIGLU (kernels.js:502-515): gate = silu(gate) * up, in place. */
 int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n);
 /* ADD (kernels.js:518-530): x += delta. */
@@ -295,6 +304,13 @@ enum {
  * h_role_launches[QH_ROLE_COUNT] the launch counts. Tokens are identical to qh_decode's. */
 int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps,
                       int32_t* h_tokens, float* h_role_ms, int32_t* h_role_launches);
+/* The average duration of one decode launch of `role` (QH_ROLE_QKV .. QH_ROLE_DOWN, cycling
+ * through the layers, or QH_ROLE_HEAD: the output head's matvec): `reps` of the step's own
+ * launches at the cache's current position, back to back on the context stream between two
+ * events, so no event sits between them (the hot-vs-cold isolation of
+ * web/decode-profile.html:239-283). It overwrites the position's decode scratch (and, for the
+ * residual roles, the hidden row): rewind or re-prefill before decoding on. */
+int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, float* us_per_launch);
 
 #ifdef __cplusplus
 }

@@ -404,6 +404,9 @@ struct SlotArgs {
   const int* d_pos;      // when set, past is read from the device (decode)
   float* part;           // [seq][heads][max_slots][kPartStride]
   int past, capacity, vstride, heads, kv_heads, max_slots;
+  // A list of same-shape caches, one per blockIdx.z (0 apart from the list operator):
+  // element strides between consecutive key caches, value caches, and partial sets.
+  size_t list_k, list_v, list_part;
 };
 
 template <int CTRL>
@@ -497,6 +500,7 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
   const int h = item / MAXS, sl = item % MAXS;
   if (h >= a.heads) return;
   const int g = h / (a.heads / a.kv_heads);
+  const size_t z = blockIdx.z;
 
   // Everything that does not depend on the position first: the head's query in
   // VGPRs (a per-lane address keeps the compiler from holding 64 values in scalar
@@ -507,8 +511,8 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
   v4f q4[kHeadDim / 4];
 #pragma unroll
   for (int i = 0; i < kHeadDim / 4; i++) q4[i] = qp[i];
-  const uint16_t* kb = a.kc + (size_t)g * a.capacity * kHeadDim;
-  const uint16_t* vrow = a.vt + ((size_t)g * kHeadDim + lane) * a.vstride;
+  const uint16_t* kb = a.kc + z * a.list_k + (size_t)g * a.capacity * kHeadDim;
+  const uint16_t* vrow = a.vt + z * a.list_v + ((size_t)g * kHeadDim + lane) * a.vstride;
   v4u ka[8], va[8], kb2[8], vb2[8];
   slot_load(kb, vrow, sl, a.capacity, lane, ka, va);
 
@@ -532,7 +536,7 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     slot_chunk(q4, kb2, vb2, (c + MAXS) * kChunk, ctx, lane, eb, m, l, o);
   }
-  float* dst = a.part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
+  float* dst = a.part + z * a.list_part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
   dst[4 + lane] = o;
   if (lane == 0) {
     dst[0] = m;
@@ -540,13 +544,16 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
   }
 }
 
-// out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t).
+// out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t) (and list
+// entry z, whose partials are list_part floats and output seq*heads*64 floats further on).
 [[maybe_unused]] static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __restrict__ part,
                                                                float* __restrict__ out, int past,
-                                                               int heads, int max_slots) {
+                                                               int heads, int max_slots, size_t list_part) {
   const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const size_t z = blockIdx.z;
   const int nslots = slots_used(past + t + 1, max_slots);
-  const float* p = part + ((size_t)t * heads + h) * max_slots * kPartStride;
+  const float* p = part + z * list_part + ((size_t)t * heads + h) * max_slots * kPartStride;
+  out += z * (size_t)gridDim.y * heads * kHeadDim;
   float M = -INFINITY;
   for (int s = 0; s < nslots; s++) M = fmaxf(M, p[(size_t)s * kPartStride]);
   float L = 0.f, A = 0.f;

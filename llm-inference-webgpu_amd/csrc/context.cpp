@@ -390,6 +390,28 @@ int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cac
   return QH_OK;
 }
 
+int qh_attention_splitk_list(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                             const uint16_t* d_value_cache, size_t key_stride, size_t value_stride,
+                             int32_t count, int32_t capacity, float* d_out, int32_t past, int32_t heads,
+                             int32_t kv_heads, int32_t head_dim) {
+  int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, 1, past, heads, kv_heads,
+                           head_dim);
+  if (rc) return rc;
+  QH_CHECK(count >= 1 && count <= 65535, QH_ERR_INVALID, "count %d must be in 1..65535", count);
+  const size_t kel = (size_t)kv_heads * capacity * 64;
+  const size_t vel = qh_value_cache_bytes(capacity, kv_heads, 64) / 2;
+  QH_CHECK(count == 1 || (key_stride >= kel && value_stride >= vel && key_stride % 8 == 0 && value_stride % 8 == 0),
+           QH_ERR_INVALID, "cache strides overlap the caches or break 16-byte alignment");
+  void* tmp = nullptr;
+  QH_HIP(hipMallocAsync(&tmp, qh::attention_list_partials_floats(count, heads, past + 1) * sizeof(float), ctx->stream));
+  hipError_t e = qh::launch_attention_splitk_list(ctx->stream, d_q, d_key_cache, d_value_cache, key_stride,
+                                                  value_stride, count, capacity, d_out, past, heads, kv_heads,
+                                                  static_cast<float*>(tmp));
+  QH_HIP(hipFreeAsync(tmp, ctx->stream));
+  QH_HIP(e);
+  return QH_OK;
+}
+
 int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n) {
   QH_CHECK(ctx && d_gate && d_up && n >= 1, QH_ERR_INVALID, "swiglu needs gate, up and n >= 1");
   QH_HIP(qh::launch_swiglu(ctx->stream, d_gate, d_up, n));

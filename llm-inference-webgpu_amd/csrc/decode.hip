@@ -401,6 +401,116 @@ hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c) {
   return hipGetLastError();
 }
 
+// The launch of `role` (QKV, ATTENTION, OPROJ, GATEUP or DOWN) for layer L.
+static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role) {
+  const int kv_dim = m.kv_heads * m.head_dim;
+  const LayerDev& l = m.layers_host[L];
+  uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
+  uint16_t* vt = kc + c.key_elems;
+  FusedArgs f{};
+  switch (role) {
+    case QH_ROLE_QKV:
+      f.eps = m.eps;
+      f.w = l.qkv;
+      f.in = c.x;
+      f.gain = l.in_norm;
+      f.bias = l.qkv_bias;
+      f.out = c.q;
+      f.rope_cos = m.rope_cos;
+      f.rope_sin = m.rope_sin;
+      f.kc = kc;
+      f.vt = vt;
+      f.vstride = c.vstride;
+      f.heads = m.heads;
+      f.kv_heads = m.kv_heads;
+      f.state = c.state;
+      f.capacity = c.capacity;
+      return fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2);
+    case QH_ROLE_ATTENTION:
+      if (m.numerics == QH_NUMERICS_FAST) {
+        SlotArgs a{};
+        a.q = c.q;
+        a.kc = kc;
+        a.vt = vt;
+        a.d_pos = c.state;
+        a.part = c.part;
+        a.capacity = c.capacity;
+        a.vstride = c.vstride;
+        a.heads = m.heads;
+        a.kv_heads = m.kv_heads;
+        a.max_slots = kDecodeSlots;
+        const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
+        hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, 1), dim3(kBlock),
+                           0, s, a);
+      } else {
+        ExactArgs a{};
+        a.q = c.q;
+        a.kc = kc;
+        a.vt = vt;
+        a.d_pos = c.state;
+        a.scores = c.scores;
+        a.maxes = c.maxes;
+        a.counters = c.attn_counters;
+        a.out = c.attn;
+        a.capacity = c.capacity;
+        a.vstride = c.vstride;
+        a.heads = m.heads;
+        a.kv_heads = m.kv_heads;
+        a.score_stride = c.score_stride;
+        a.max_stride = attn_spans(c.capacity);
+        if (c.capacity <= kPLds) {
+          hipLaunchKernelGGL(k_attn_block, dim3(m.heads, 1), dim3(kAttnThreads), 0, s, a);
+        } else {
+          hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
+        }
+      }
+      return hipGetLastError();
+    case QH_ROLE_OPROJ:
+      f.w = l.o;
+      f.out = c.x;
+      if (m.numerics == QH_NUMERICS_FAST) {
+        f.in = c.part;
+        f.heads = m.heads;
+        f.state = c.state;
+        return fused<2, PRO_COMBINE, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
+      }
+      f.in = c.attn;
+      return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
+    case QH_ROLE_GATEUP:
+      f.eps = m.eps;
+      f.w = l.gu;
+      f.in = c.x;
+      f.gain = l.post_norm;
+      f.out = c.h;
+      return fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2);
+    case QH_ROLE_DOWN:
+      f.w = l.down;
+      f.in = c.h;
+      f.out = c.x;
+      return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+// The output head's matvec alone (final rmsnorm, lm_head, logits, block argmax partials).
+static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c) {
+  FusedArgs f{};
+  f.eps = m.eps;
+  f.w = m.lm_head;
+  f.in = c.x;
+  f.gain = m.final_norm;
+  f.out = c.logits;
+  f.partials = static_cast<ArgPair*>(c.lm_partials);
+  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, kLmMaxBlocks);
+}
+
+hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer) {
+  if (role == QH_ROLE_HEAD) return head_matvec(s, m, c);
+  if (layer < 0 || layer >= m.layers) return hipErrorInvalidValue;
+  return layer_role(s, m, c, layer, role);
+}
+
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
                         bool logits, StepTimer* timer) {
   hipError_t e;
@@ -408,100 +518,11 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
     if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
     if ((e = enqueue_gather(s, m, c)) != hipSuccess) return e;
   }
-  const int kv_dim = m.kv_heads * m.head_dim;
   for (int L = 0; L < m.layers; L++) {
-    const LayerDev& l = m.layers_host[L];
-    uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
-    uint16_t* vt = kc + c.key_elems;
-
-    FusedArgs f{};
-    f.eps = m.eps;
-    f.w = l.qkv;
-    f.in = c.x;
-    f.gain = l.in_norm;
-    f.bias = l.qkv_bias;
-    f.out = c.q;
-    f.rope_cos = m.rope_cos;
-    f.rope_sin = m.rope_sin;
-    f.kc = kc;
-    f.vt = vt;
-    f.vstride = c.vstride;
-    f.heads = m.heads;
-    f.kv_heads = m.kv_heads;
-    f.state = c.state;
-    f.capacity = c.capacity;
-    if ((e = mark(s, timer, QH_ROLE_QKV)) != hipSuccess) return e;
-    if ((e = fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2)) != hipSuccess)
-      return e;
-
-    if ((e = mark(s, timer, QH_ROLE_ATTENTION)) != hipSuccess) return e;
-    if (m.numerics == QH_NUMERICS_FAST) {
-      SlotArgs a{};
-      a.q = c.q;
-      a.kc = kc;
-      a.vt = vt;
-      a.d_pos = c.state;
-      a.part = c.part;
-      a.capacity = c.capacity;
-      a.vstride = c.vstride;
-      a.heads = m.heads;
-      a.kv_heads = m.kv_heads;
-      a.max_slots = kDecodeSlots;
-      const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
-      hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, 1), dim3(kBlock), 0, s, a);
-    } else {
-      ExactArgs a{};
-      a.q = c.q;
-      a.kc = kc;
-      a.vt = vt;
-      a.d_pos = c.state;
-      a.scores = c.scores;
-      a.maxes = c.maxes;
-      a.counters = c.attn_counters;
-      a.out = c.attn;
-      a.capacity = c.capacity;
-      a.vstride = c.vstride;
-      a.heads = m.heads;
-      a.kv_heads = m.kv_heads;
-      a.score_stride = c.score_stride;
-      a.max_stride = attn_spans(c.capacity);
-      if (c.capacity <= kPLds) {
-        hipLaunchKernelGGL(k_attn_block, dim3(m.heads, 1), dim3(kAttnThreads), 0, s, a);
-      } else {
-        hipLaunchKernelGGL(k_attn_exact, dim3(attn_spans(c.capacity), m.heads, 1), dim3(kBlock), 0, s, a);
-      }
+    for (int role : {QH_ROLE_QKV, QH_ROLE_ATTENTION, QH_ROLE_OPROJ, QH_ROLE_GATEUP, QH_ROLE_DOWN}) {
+      if ((e = mark(s, timer, role)) != hipSuccess) return e;
+      if ((e = layer_role(s, m, c, L, role)) != hipSuccess) return e;
     }
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-
-    f = FusedArgs{};
-    f.w = l.o;
-    f.out = c.x;
-    if ((e = mark(s, timer, QH_ROLE_OPROJ)) != hipSuccess) return e;
-    if (m.numerics == QH_NUMERICS_FAST) {
-      f.in = c.part;
-      f.heads = m.heads;
-      f.state = c.state;
-      if ((e = fused<2, PRO_COMBINE, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
-    } else {
-      f.in = c.attn;
-      if ((e = fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2)) != hipSuccess) return e;
-    }
-
-    f = FusedArgs{};
-    f.eps = m.eps;
-    f.w = l.gu;
-    f.in = c.x;
-    f.gain = l.post_norm;
-    f.out = c.h;
-    if ((e = mark(s, timer, QH_ROLE_GATEUP)) != hipSuccess) return e;
-    if ((e = fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2)) != hipSuccess) return e;
-
-    f = FusedArgs{};
-    f.w = l.down;
-    f.in = c.h;
-    f.out = c.x;
-    if ((e = mark(s, timer, QH_ROLE_DOWN)) != hipSuccess) return e;
-    if ((e = fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows)) != hipSuccess) return e;
   }
   if (!logits) {
     if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
@@ -515,17 +536,8 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
 
 hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer) {
   hipError_t e;
-  FusedArgs f{};
-  f.eps = m.eps;
-  f.w = m.lm_head;
-  f.in = c.x;
-  f.gain = m.final_norm;
-  f.out = c.logits;
-  f.partials = static_cast<ArgPair*>(c.lm_partials);
   if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
-  if ((e = fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, kLmMaxBlocks)) !=
-      hipSuccess)
-    return e;
+  if ((e = head_matvec(s, m, c)) != hipSuccess) return e;
   // The pick gathers the next input row, so it is timed with the gathers.
   if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
   hipLaunchKernelGGL(k_pick, dim3(1), dim3(kBlock), 0, s, static_cast<const ArgPair*>(c.lm_partials),

@@ -837,6 +837,33 @@ int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int3
   return qh_decode_collect(m, c, steps, h_tokens);
 }
 
+int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, float* us_per_launch) {
+  QH_CHECK(m && c && c->m == m && us_per_launch, QH_ERR_INVALID, "kernel_time needs a model, its cache and an output");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(role >= QH_ROLE_QKV && role <= QH_ROLE_HEAD, QH_ERR_INVALID, "role %d has no single decode kernel", role);
+  QH_CHECK(reps >= 1, QH_ERR_INVALID, "reps must be >= 1");
+  QH_CHECK(c->length < c->dev.capacity, QH_ERR_RANGE, "the cache is full");
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  int rc = set_state(c, c->length, c->length + 1);
+  if (rc) return rc;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  QH_HIP(hipEventCreate(&e0));
+  hipError_t err = hipEventCreate(&e1);
+  if (err == hipSuccess) err = qh::enqueue_role(s, m->dev, c->dev, role, 0);  // warm
+  if (err == hipSuccess) err = hipEventRecord(e0, s);
+  for (int r = 0; r < reps && err == hipSuccess; r++) err = qh::enqueue_role(s, m->dev, c->dev, role, r % m->dev.layers);
+  if (err == hipSuccess) err = hipEventRecord(e1, s);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  QH_HIP(err);
+  *us_per_launch = ms * 1e3f / reps;
+  return QH_OK;
+}
+
 int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps,
                       int32_t* h_tokens, float* h_role_ms, int32_t* h_role_launches) {
   QH_CHECK(m && c && c->m == m && h_role_ms && h_role_launches, QH_ERR_INVALID,

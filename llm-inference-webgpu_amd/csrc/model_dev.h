@@ -109,6 +109,9 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
 // The output head of the position state[0] over cache.x: final rmsnorm, lm_head, logits and
 // the pick (token recorded, position advanced, next input row gathered).
 hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer = nullptr);
+// One launch of a decode role's kernel: QKV, ATTENTION, OPROJ, GATEUP or DOWN of `layer`, or
+// HEAD (the output head's matvec, without the pick) -- the launches the step makes.
+hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer);
 // cache.x = the embedding of tokens[position] (what STEP_GATHER starts with).
 hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c);
 // Launches in one step with logits (the events a StepTimer needs, minus the final one).

@@ -371,8 +371,53 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
-                     kOpSlots);
+                     kOpSlots, (size_t)0);
   return hipGetLastError();
+}
+
+// Slots per head of the list operator: enough for one chunk per slot up to 64 slots.
+static int list_slots(int ctx) {
+  const int n = attn_chunks(ctx);
+  return n <= 4 ? 4 : n <= 16 ? 16 : kOpSlots;
+}
+
+size_t attention_list_partials_floats(int count, int heads, int ctx) {
+  return (size_t)count * heads * list_slots(ctx) * kPartStride;
+}
+
+template <int MAXS>
+static hipError_t list_t(hipStream_t s, SlotArgs a, int count, float* out) {
+  a.max_slots = MAXS;
+  a.list_part = (size_t)a.heads * MAXS * kPartStride;
+  const int waves = a.heads * MAXS, per_block = kBlock / kWave;
+  hipLaunchKernelGGL(k_attn_slots<MAXS>, dim3((waves + per_block - 1) / per_block, 1, count), dim3(kBlock), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
+                     a.list_part);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_splitk_list(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
+                                        size_t list_k, size_t list_v, int count, int capacity, float* out,
+                                        int past, int heads, int kv_heads, float* partials) {
+  SlotArgs a{};
+  a.q = q;
+  a.kc = kc;
+  a.vt = vt;
+  a.part = partials;
+  a.past = past;
+  a.capacity = capacity;
+  a.vstride = value_stride(capacity);
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  a.list_k = list_k;
+  a.list_v = list_v;
+  switch (list_slots(past + 1)) {
+    case 4: return list_t<4>(s, a, count, out);
+    case 16: return list_t<16>(s, a, count, out);
+    default: return list_t<kOpSlots>(s, a, count, out);
+  }
 }
 
 // ------------------------------------------------------------ swiglu / add --

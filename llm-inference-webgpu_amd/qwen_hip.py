@@ -141,6 +141,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_attention_splitk": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
         "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32],
+        "qh_attention_splitk_list": [vp, vp, vp, vp, sz, sz, i32, i32, vp, i32, i32, i32, i32],
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
         "qh_quantize_int4": [vp, i32, i32, i32, vp, vp, vp],
@@ -157,6 +158,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_decode": [vp, vp, i32, i32, vp], "qh_decode_launch": [vp, vp, i32, i32],
         "qh_decode_collect": [vp, vp, i32, vp], "qh_decode_use_graph": [vp, i32],
         "qh_decode_profile": [vp, vp, i32, i32, vp, vp, vp],
+        "qh_decode_kernel_time": [vp, vp, i32, i32, vp],
     }
     for name, args in sigs.items():
         f = getattr(lib, name)
@@ -435,6 +437,12 @@ class GpuContext:
         _check(fn(self.handle, q.ptr, kc.ptr, vc.ptr, capacity, out.ptr, seq, past, heads, kv_heads,
                   head_dim))
 
+    def attention_list(self, q, kc, vc, key_stride, value_stride, count, capacity, out, past, heads,
+                       kv_heads, head_dim=64) -> None:
+        """Split-K attention of one query against `count` caches (strides in f16 elements)."""
+        _check(self.lib.qh_attention_splitk_list(self.handle, q.ptr, kc.ptr, vc.ptr, key_stride, value_stride,
+                                                 count, capacity, out.ptr, past, heads, kv_heads, head_dim))
+
     def swiglu(self, gate, up, n) -> None:
         _check(self.lib.qh_swiglu(self.handle, gate.ptr, up.ptr, n))
 
@@ -589,6 +597,13 @@ class GpuModel:
         _check(self.lib.qh_decode_profile(self.handle, cache.handle, first_token, steps, _ptr(out),
                                           _ptr(ms), _ptr(n)))
         return out, {r: (float(ms[i]), int(n[i])) for i, r in enumerate(ROLES)}
+
+    def kernel_time(self, cache: GpuKVCache, role: str, reps: int = 240) -> float:
+        """Microseconds per back-to-back launch of one decode role's kernel (see the C ABI)."""
+        us = ctypes.c_float()
+        _check(self.lib.qh_decode_kernel_time(self.handle, cache.handle, ROLES.index(role), reps,
+                                              ctypes.byref(us)))
+        return us.value
 
     def destroy(self) -> None:
         if self.handle:

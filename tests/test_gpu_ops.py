@@ -314,6 +314,30 @@ def test_decode_attention_matches_oracle(ctx, hip, ctx_len, splitk):
     free(kc, vc, dq, dout)
 
 
+@pytest.mark.parametrize("ctx_len", [1, 100, 1000, 5000])
+def test_attention_list_matches_single_calls(ctx, hip, ctx_len):
+    """The list form (config 3's rotation in one launch) gives each cache the single-cache
+    split-K result within the kernel tolerance of the oracle."""
+    heads, kv_heads, count, cap = 14, 2, 5, ctx_len + 3
+    vstride = (cap + 7) // 8 * 8
+    rng = np.random.default_rng(ctx_len)
+    kel, vel = kv_heads * cap * 64, kv_heads * 64 * vstride
+    keys = O.f32_to_f16(rng.standard_normal(count * kel).astype(np.float32))
+    vals = O.f32_to_f16(rng.standard_normal(count * vel).astype(np.float32))
+    q = rng.standard_normal(heads * 64).astype(np.float32)
+    dk, dv, dq, dout = ctx.upload(keys), ctx.upload(vals), ctx.upload(q), ctx.empty(count * heads * 64 * 4)
+    ctx.attention_list(dq, dk, dv, kel, vel, count, cap, dout, ctx_len - 1, heads, kv_heads)
+    got = dout.read(count=count * heads * 64).reshape(count, heads * 64)
+    for i in range(count):
+        kr = O.f16_to_f32(keys[i * kel:(i + 1) * kel]).reshape(kv_heads, cap, 64)[:, :ctx_len]
+        vr = O.f16_to_f32(vals[i * vel:(i + 1) * vel]).reshape(kv_heads, 64, vstride)[:, :, :ctx_len]
+        K = np.ascontiguousarray(kr.transpose(1, 0, 2).reshape(ctx_len, -1))
+        V = np.ascontiguousarray(vr.transpose(2, 0, 1).reshape(ctx_len, -1))
+        ref = O.grouped_attention(q, K, V, 1, ctx_len - 1, heads, kv_heads, 64)
+        assert rel_err(got[i], ref) <= KERNEL_REL
+    free(dk, dv, dq, dout)
+
+
 @pytest.mark.parametrize("splitk", [False, True], ids=["exact", "splitk"])
 def test_decode_attention_32k(ctx, hip, splitk):
     ctx_len, heads, kv_heads = 32768, 14, 2
