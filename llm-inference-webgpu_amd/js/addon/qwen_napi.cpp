@@ -1,0 +1,421 @@
+// Node-API binding of libqwen_hip.so: argument marshalling only. Every function
+// takes and returns plain JS values and typed arrays, calls one C-ABI entry
+// point, and turns a non-zero status into a thrown Error (RangeError for
+// QH_ERR_RANGE, as the reference throws for capacity and rope bounds,
+// src/gpu/model.js:249-254) carrying qh_last_error()'s message. Handles are
+// napi externals; the JS driver (../gpu_model.js) owns their lifetime.
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "qwen_hip.h"
+
+namespace {
+
+#define NAPI_OK(call)                                         \
+  do {                                                        \
+    if ((call) != napi_ok) {                                  \
+      napi_throw_error(env, nullptr, "node-api call failed"); \
+      return nullptr;                                         \
+    }                                                         \
+  } while (0)
+
+napi_value fail(napi_env env, int rc) {
+  const char* msg = qh_last_error();
+  std::string code = "QH_ERR_" + std::to_string(rc);
+  if (rc == QH_ERR_RANGE) napi_throw_range_error(env, code.c_str(), msg);
+  else napi_throw_error(env, code.c_str(), msg);
+  return nullptr;
+}
+
+#define QH_CALL(expr)              \
+  do {                             \
+    int rc_ = (expr);              \
+    if (rc_ != QH_OK) return fail(env, rc_); \
+  } while (0)
+
+struct Args {
+  napi_value v[12];
+  size_t n = 12;
+};
+
+bool get_args(napi_env env, napi_callback_info info, Args& a, size_t need) {
+  if (napi_get_cb_info(env, info, &a.n, a.v, nullptr, nullptr) != napi_ok || a.n < need) {
+    napi_throw_type_error(env, nullptr, "missing arguments");
+    return false;
+  }
+  return true;
+}
+
+bool to_i32(napi_env env, napi_value v, int32_t* out) {
+  if (napi_get_value_int32(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a number");
+    return false;
+  }
+  return true;
+}
+
+bool to_f64(napi_env env, napi_value v, double* out) {
+  if (napi_get_value_double(env, v, out) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a number");
+    return false;
+  }
+  return true;
+}
+
+bool to_str(napi_env env, napi_value v, std::string* out) {
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, v, nullptr, 0, &len) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "expected a string");
+    return false;
+  }
+  out->resize(len + 1);
+  napi_get_value_string_utf8(env, v, &(*out)[0], len + 1, &len);
+  out->resize(len);
+  return true;
+}
+
+// The bytes of a typed array (null / undefined give nullptr).
+bool to_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_null || t == napi_undefined) {
+    *data = nullptr;
+    if (bytes) *bytes = 0;
+    return true;
+  }
+  bool is_ta = false;
+  napi_is_typedarray(env, v, &is_ta);
+  if (!is_ta) {
+    napi_throw_type_error(env, nullptr, "expected a typed array");
+    return false;
+  }
+  napi_typedarray_type type;
+  size_t length = 0, offset = 0;
+  napi_value ab;
+  napi_get_typedarray_info(env, v, &type, &length, data, &ab, &offset);
+  size_t el = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: el = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
+    case napi_float64_array: el = 8; break;
+    default: el = 1;
+  }
+  if (bytes) *bytes = length * el;
+  return true;
+}
+
+template <typename T>
+bool to_handle(napi_env env, napi_value v, T** out) {
+  void* p = nullptr;
+  if (napi_get_value_external(env, v, &p) != napi_ok || !p) {
+    napi_throw_type_error(env, nullptr, "expected a live handle");
+    return false;
+  }
+  *out = static_cast<T*>(p);
+  return true;
+}
+
+napi_value external(napi_env env, void* p) {
+  napi_value v;
+  napi_create_external(env, p, nullptr, nullptr, &v);
+  return v;
+}
+
+napi_value typed(napi_env env, napi_typedarray_type type, size_t count, size_t el, void** data) {
+  napi_value ab, ta;
+  if (napi_create_arraybuffer(env, count * el, data, &ab) != napi_ok) return nullptr;
+  napi_create_typedarray(env, type, count, ab, 0, &ta);
+  return ta;
+}
+
+napi_value num(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+// ------------------------------------------------------------------ context
+napi_value Open(napi_env env, napi_callback_info info) {
+  Args a;
+  int32_t dev = 0;
+  if (!get_args(env, info, a, 1) || !to_i32(env, a.v[0], &dev)) return nullptr;
+  qh_ctx* c = nullptr;
+  QH_CALL(qh_open(dev, &c));
+  return external(env, c);
+}
+
+napi_value Close(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_ctx* c;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &c)) return nullptr;
+  QH_CALL(qh_close(c));
+  return nullptr;
+}
+
+napi_value Describe(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_ctx* c;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &c)) return nullptr;
+  char buf[1024];
+  QH_CALL(qh_describe(c, buf, sizeof buf));
+  napi_value s;
+  napi_create_string_utf8(env, buf, NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+// ------------------------------------------------------------- host helpers
+napi_value SynthBf16(napi_env env, napi_callback_info info) {  // (seed, name, std, n)
+  Args a;
+  double seed, std_, n;
+  std::string name;
+  if (!get_args(env, info, a, 4) || !to_f64(env, a.v[0], &seed) || !to_str(env, a.v[1], &name) ||
+      !to_f64(env, a.v[2], &std_) || !to_f64(env, a.v[3], &n))
+    return nullptr;
+  void* d;
+  napi_value out = typed(env, napi_uint16_array, (size_t)n, 2, &d);
+  QH_CALL(qh_synth_bf16((uint64_t)seed, name.c_str(), std_, 0, (size_t)n, static_cast<uint16_t*>(d)));
+  return out;
+}
+
+napi_value SynthTokens(napi_env env, napi_callback_info info) {  // (seed, name, vocab, n)
+  Args a;
+  double seed;
+  int32_t vocab, n;
+  std::string name;
+  if (!get_args(env, info, a, 4) || !to_f64(env, a.v[0], &seed) || !to_str(env, a.v[1], &name) ||
+      !to_i32(env, a.v[2], &vocab) || !to_i32(env, a.v[3], &n))
+    return nullptr;
+  void* d;
+  napi_value out = typed(env, napi_int32_array, (size_t)n, 4, &d);
+  QH_CALL(qh_synth_tokens((uint64_t)seed, name.c_str(), vocab, (size_t)n, static_cast<int32_t*>(d)));
+  return out;
+}
+
+napi_value QuantizeInt8(napi_env env, napi_callback_info info) {  // (Float32Array, rows, cols)
+  Args a;
+  void* w;
+  int32_t rows, cols;
+  if (!get_args(env, info, a, 3) || !to_bytes(env, a.v[0], &w, nullptr) || !to_i32(env, a.v[1], &rows) ||
+      !to_i32(env, a.v[2], &cols))
+    return nullptr;
+  void *q, *s;
+  napi_value tq = typed(env, napi_int8_array, (size_t)rows * cols, 1, &q);
+  napi_value ts = typed(env, napi_float32_array, (size_t)rows, 4, &s);
+  QH_CALL(qh_quantize_int8(static_cast<const float*>(w), rows, cols, static_cast<int8_t*>(q),
+                           static_cast<float*>(s)));
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "q", tq);
+  napi_set_named_property(env, o, "scales", ts);
+  return o;
+}
+
+napi_value QuantizeInt4(napi_env env, napi_callback_info info) {  // (Float32Array, rows, cols, group)
+  Args a;
+  void* w;
+  int32_t rows, cols, group;
+  if (!get_args(env, info, a, 4) || !to_bytes(env, a.v[0], &w, nullptr) || !to_i32(env, a.v[1], &rows) ||
+      !to_i32(env, a.v[2], &cols) || !to_i32(env, a.v[3], &group))
+    return nullptr;
+  if (group < 2 || cols % group) return fail(env, qh_quantize_int4(nullptr, rows, cols, group, nullptr, nullptr, nullptr));
+  const size_t ng = (size_t)rows * (cols / group);
+  void *q, *s, *z;
+  napi_value tq = typed(env, napi_uint8_array, (size_t)rows * cols / 2, 1, &q);
+  napi_value ts = typed(env, napi_float32_array, ng, 4, &s);
+  napi_value tz = typed(env, napi_float32_array, ng, 4, &z);
+  QH_CALL(qh_quantize_int4(static_cast<const float*>(w), rows, cols, group, static_cast<uint8_t*>(q),
+                           static_cast<float*>(s), static_cast<float*>(z)));
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "q", tq);
+  napi_set_named_property(env, o, "scales", ts);
+  napi_set_named_property(env, o, "zeros", tz);
+  return o;
+}
+
+// -------------------------------------------------------------------- model
+bool prop_i32(napi_env env, napi_value o, const char* k, int32_t* out) {
+  napi_value v;
+  return napi_get_named_property(env, o, k, &v) == napi_ok && to_i32(env, v, out);
+}
+bool prop_f64(napi_env env, napi_value o, const char* k, double* out) {
+  napi_value v;
+  return napi_get_named_property(env, o, k, &v) == napi_ok && to_f64(env, v, out);
+}
+
+napi_value ModelCreate(napi_env env, napi_callback_info info) {  // (ctx, config)
+  Args a;
+  qh_ctx* c;
+  if (!get_args(env, info, a, 2) || !to_handle(env, a.v[0], &c)) return nullptr;
+  qh_config cfg{};
+  napi_value o = a.v[1];
+  if (!prop_i32(env, o, "hidden", &cfg.hidden) || !prop_i32(env, o, "intermediate", &cfg.intermediate) ||
+      !prop_i32(env, o, "layers", &cfg.layers) || !prop_i32(env, o, "heads", &cfg.heads) ||
+      !prop_i32(env, o, "kvHeads", &cfg.kv_heads) || !prop_i32(env, o, "headDim", &cfg.head_dim) ||
+      !prop_i32(env, o, "vocab", &cfg.vocab) || !prop_f64(env, o, "ropeTheta", &cfg.rope_theta) ||
+      !prop_f64(env, o, "eps", &cfg.eps) || !prop_i32(env, o, "maxPositions", &cfg.max_positions))
+    return nullptr;
+  qh_model* m = nullptr;
+  QH_CALL(qh_model_create(c, &cfg, &m));
+  return external(env, m);
+}
+
+napi_value ModelSetMode(napi_env env, napi_callback_info info) {  // (model, 'numerics'|'matmul', value)
+  Args a;
+  qh_model* m;
+  std::string which;
+  int32_t v;
+  if (!get_args(env, info, a, 3) || !to_handle(env, a.v[0], &m) || !to_str(env, a.v[1], &which) ||
+      !to_i32(env, a.v[2], &v))
+    return nullptr;
+  QH_CALL(which == "numerics" ? qh_model_set_numerics(m, v) : qh_model_set_matmul(m, v));
+  return nullptr;
+}
+
+// (model, name, format, rows, cols, group, data, scales|null, zeros|null)
+napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  std::string name;
+  int32_t fmt, rows, cols, group;
+  void *data, *scales, *zeros;
+  if (!get_args(env, info, a, 9) || !to_handle(env, a.v[0], &m) || !to_str(env, a.v[1], &name) ||
+      !to_i32(env, a.v[2], &fmt) || !to_i32(env, a.v[3], &rows) || !to_i32(env, a.v[4], &cols) ||
+      !to_i32(env, a.v[5], &group) || !to_bytes(env, a.v[6], &data, nullptr) ||
+      !to_bytes(env, a.v[7], &scales, nullptr) || !to_bytes(env, a.v[8], &zeros, nullptr))
+    return nullptr;
+  QH_CALL(qh_model_set_tensor(m, name.c_str(), fmt, rows, cols, group, data, static_cast<const float*>(scales),
+                              static_cast<const float*>(zeros)));
+  return nullptr;
+}
+
+napi_value ModelFinalize(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &m)) return nullptr;
+  QH_CALL(qh_model_finalize(m));
+  size_t bytes = 0;
+  QH_CALL(qh_model_bytes(m, &bytes));
+  return num(env, (double)bytes);
+}
+
+napi_value ModelFree(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &m)) return nullptr;
+  QH_CALL(qh_model_free(m));
+  return nullptr;
+}
+
+napi_value CacheCreate(napi_env env, napi_callback_info info) {  // (model, capacity)
+  Args a;
+  qh_model* m;
+  int32_t cap;
+  if (!get_args(env, info, a, 2) || !to_handle(env, a.v[0], &m) || !to_i32(env, a.v[1], &cap)) return nullptr;
+  qh_cache* c = nullptr;
+  QH_CALL(qh_cache_create(m, cap, &c));
+  return external(env, c);
+}
+
+napi_value CacheFree(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_cache* c;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &c)) return nullptr;
+  QH_CALL(qh_cache_free(c));
+  return nullptr;
+}
+
+napi_value CacheLength(napi_env env, napi_callback_info info) {  // (cache[, newLength])
+  Args a;
+  qh_cache* c;
+  if (!get_args(env, info, a, 1) || !to_handle(env, a.v[0], &c)) return nullptr;
+  if (a.n >= 2) {
+    int32_t len;
+    if (!to_i32(env, a.v[1], &len)) return nullptr;
+    QH_CALL(qh_cache_set_length(c, len));
+  }
+  int32_t len = 0;
+  QH_CALL(qh_cache_length(c, &len));
+  return num(env, len);
+}
+
+// (model, cache, Int32Array ids | Float32Array hidden, seq, wantLogits, vocab) -> {logits, argmax}
+napi_value Forward(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  qh_cache* c;
+  void* in;
+  int32_t seq, vocab;
+  bool want = true;
+  if (!get_args(env, info, a, 6) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c) ||
+      !to_bytes(env, a.v[2], &in, nullptr) || !to_i32(env, a.v[3], &seq))
+    return nullptr;
+  napi_get_value_bool(env, a.v[4], &want);
+  if (!to_i32(env, a.v[5], &vocab)) return nullptr;
+  napi_typedarray_type type;
+  size_t len, off;
+  void* d;
+  napi_value ab;
+  napi_get_typedarray_info(env, a.v[2], &type, &len, &d, &ab, &off);
+  void* lp = nullptr;
+  napi_value logits = nullptr;
+  if (want) logits = typed(env, napi_float32_array, (size_t)vocab, 4, &lp);
+  int32_t am = -1;
+  if (type == napi_int32_array) {
+    QH_CALL(qh_forward_tokens(m, c, static_cast<const int32_t*>(in), seq, static_cast<float*>(lp),
+                              want ? &am : nullptr));
+  } else {
+    QH_CALL(qh_forward(m, c, static_cast<const float*>(in), seq, static_cast<float*>(lp), want ? &am : nullptr));
+  }
+  napi_value o, nul;
+  napi_get_null(env, &nul);
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "logits", want ? logits : nul);
+  napi_set_named_property(env, o, "argmax", want ? num(env, am) : nul);
+  return o;
+}
+
+napi_value Decode(napi_env env, napi_callback_info info) {  // (model, cache, firstToken, steps) -> Int32Array
+  Args a;
+  qh_model* m;
+  qh_cache* c;
+  int32_t first, steps;
+  if (!get_args(env, info, a, 4) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c) ||
+      !to_i32(env, a.v[2], &first) || !to_i32(env, a.v[3], &steps))
+    return nullptr;
+  void* d;
+  napi_value out = typed(env, napi_int32_array, (size_t)(steps > 0 ? steps : 0), 4, &d);
+  QH_CALL(qh_decode(m, c, first, steps, static_cast<int32_t*>(d)));
+  return out;
+}
+
+napi_value AbiVersion(napi_env env, napi_callback_info) { return num(env, qh_abi_version()); }
+
+}  // namespace
+
+static napi_value Init(napi_env env, napi_value exports) {
+  const struct {
+    const char* name;
+    napi_callback fn;
+  } fns[] = {{"abiVersion", AbiVersion},   {"open", Open},
+             {"close", Close},             {"describe", Describe},
+             {"synthBf16", SynthBf16},     {"synthTokens", SynthTokens},
+             {"quantizeInt8", QuantizeInt8}, {"quantizeInt4", QuantizeInt4},
+             {"modelCreate", ModelCreate}, {"modelSetMode", ModelSetMode},
+             {"modelSetTensor", ModelSetTensor}, {"modelFinalize", ModelFinalize},
+             {"modelFree", ModelFree},     {"cacheCreate", CacheCreate},
+             {"cacheFree", CacheFree},     {"cacheLength", CacheLength},
+             {"forward", Forward},         {"decode", Decode}};
+  for (const auto& f : fns) {
+    napi_value v;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.fn, nullptr, &v);
+    napi_set_named_property(env, exports, f.name, v);
+  }
+  return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)
