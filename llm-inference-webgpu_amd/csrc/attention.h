@@ -490,12 +490,14 @@ __device__ __forceinline__ void slot_chunk(const v4f (&q4)[kHeadDim / 4], const 
   m = mn;
 }
 
+// One wave per block: a slot's loads (the query, 64 key rows, 64 value runs) are
+// all issued up front, and with one wave per CU they are not queued behind three
+// other waves' in the CU's load pipeline. grid (heads * MAXS, seq, list entries).
 template <int MAXS>
-static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
-  __shared__ __attribute__((aligned(16))) float ebuf[kBlock / kWave][kChunk];
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int item = blockIdx.x * (kBlock / kWave) + wave;
+static __global__ __launch_bounds__(kWave) void k_attn_slots(SlotArgs a) {
+  __shared__ __attribute__((aligned(16))) float eb[kChunk];
+  const int lane = threadIdx.x;
+  const int item = blockIdx.x;
   const int t = blockIdx.y;
   const int h = item / MAXS, sl = item % MAXS;
   if (h >= a.heads) return;
@@ -521,20 +523,31 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
   if (pos >= a.capacity) return;  // the host keeps positions inside the cache
   const int ctx = pos + 1;
   const int nch = attn_chunks(ctx);
-  float* eb = ebuf[wave];
   float m = -INFINITY, l = 0.f, o = 0.f;
-  // Chunks alternate between two named buffers, so the next chunk's loads stay in
-  // flight while this one is summed (no register copies wait on them). The
-  // prefetch is unconditional (past the slot it re-reads an in-bounds chunk),
-  // which keeps the outstanding-load count the same on every path.
-  for (int c = sl; c < nch; c += 2 * MAXS) {
-    slot_load(kb, vrow, min(c + MAXS, nch - 1), a.capacity, lane, kb2, vb2);
-    __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before this chunk's arithmetic
+  // This slot's chunks: sl, sl + MAXS, ... below nch (uniform over the wave). Each
+  // next chunk is loaded into the other named buffer before the current one is
+  // summed, so its loads stay in flight (no register copies wait on them); the
+  // last chunk is summed with no load behind it, so the wave ends on its own data.
+  int left = sl < nch ? (nch - 1 - sl) / MAXS + 1 : 0;
+  int c = sl;
+  while (left > 0) {
+    if (left == 1) {
+      slot_chunk(q4, ka, va, c * kChunk, ctx, lane, eb, m, l, o);
+      break;
+    }
+    slot_load(kb, vrow, c + MAXS, a.capacity, lane, kb2, vb2);
+    __builtin_amdgcn_sched_barrier(0);  // issue the next chunk's loads before this one's arithmetic
     slot_chunk(q4, ka, va, c * kChunk, ctx, lane, eb, m, l, o);
-    if (c + MAXS >= nch) break;
-    slot_load(kb, vrow, min(c + 2 * MAXS, nch - 1), a.capacity, lane, ka, va);
+    c += MAXS;
+    if (--left == 1) {
+      slot_chunk(q4, kb2, vb2, c * kChunk, ctx, lane, eb, m, l, o);
+      break;
+    }
+    slot_load(kb, vrow, c + MAXS, a.capacity, lane, ka, va);
     __builtin_amdgcn_sched_barrier(0);
-    slot_chunk(q4, kb2, vb2, (c + MAXS) * kChunk, ctx, lane, eb, m, l, o);
+    slot_chunk(q4, kb2, vb2, c * kChunk, ctx, lane, eb, m, l, o);
+    c += MAXS;
+    --left;
   }
   float* dst = a.part + z * a.list_part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
   dst[4 + lane] = o;
@@ -542,6 +555,13 @@ static __global__ __launch_bounds__(kBlock) void k_attn_slots(SlotArgs a) {
     dst[0] = m;
     dst[1] = l;
   }
+}
+
+// k_attn_slots over `seq` queries (grid.y) and `count` list entries (grid.z).
+template <int MAXS>
+static hipError_t launch_attn_slots(hipStream_t s, const SlotArgs& a, int seq, int count) {
+  hipLaunchKernelGGL(k_attn_slots<MAXS>, dim3(a.heads * MAXS, seq, count), dim3(kWave), 0, s, a);
+  return hipGetLastError();
 }
 
 // out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t) (and list
@@ -623,6 +643,18 @@ __device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int head
     xs[lay.pos(j + 2)] = (double)acc.z;
     xs[lay.pos(j + 3)] = (double)acc.w;
   }
+  __syncthreads();
+}
+
+// The same merge staged for the f32 matvec core: thread i's quad is 4-element group
+// i of the attention output (i = h*16 + k holds elements 64h + 4k .. +3), stored with
+// its chunk sums after the heads*64 values.
+template <int FMT>
+__device__ __forceinline__ void stage_attn_combine_f32(const CombineIn& in, int heads, float* xs, XLayoutF lay,
+                                                       float* wl) {
+  const v4f acc = attn_combine_quad(in, wl);
+  const int i = threadIdx.x;
+  stage_group_f32<FMT>(acc, i, i < heads * kDecodeSlots, xs, xs + heads * kHeadDim, lay);
   __syncthreads();
 }
 

@@ -53,6 +53,7 @@ struct FusedArgs {
   int capacity;
   // EPI_LOGITS
   ArgPair* partials;     // [blocks]: each block's best (value, index)
+  int f32;              // fast numerics: the f32 matvec core
   // PRO_COMBINE: `in` holds the attention slot partials of the current position
 };
 
@@ -108,14 +109,16 @@ __device__ __forceinline__ void epi_load(const FusedArgs& a, int it, int pos, co
 }
 
 // Lane 0 of the team that summed item `it` (acc = the R row sums) stores it.
-template <int R, int EPI>
+// acc is f64 (exact numerics) or f32 (fast numerics, int8 row scale applied).
+template <int R, int EPI, typename Acc>
 __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, const int (&rows)[R],
-                                         const double (&acc)[R], const EpiIn<EPI, R>& e, float& bv,
+                                         const Acc (&acc)[R], const EpiIn<EPI, R>& e, float& bv,
                                          int& bi) {
+  constexpr bool kF32 = std::is_same<Acc, float>::value;
   if constexpr (EPI == EPI_QKV) {
-    // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts).
-    const float v0 = (float)(acc[0] + (double)e.bias[0]);
-    const float v1 = (float)(acc[1] + (double)e.bias[1]);
+    // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts; f32: one add).
+    const float v0 = kF32 ? __fadd_rn((float)acc[0], e.bias[0]) : (float)((double)acc[0] + (double)e.bias[0]);
+    const float v1 = kF32 ? __fadd_rn((float)acc[1], e.bias[1]) : (float)((double)acc[1] + (double)e.bias[1]);
     const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
     const int rope_pairs = (a.heads + a.kv_heads) * 32;
     if (pos >= a.capacity) return;  // the host keeps positions inside the cache
@@ -143,18 +146,23 @@ __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, co
 #pragma unroll
     for (int i = 0; i < R; i++) {
       const int r = it * R + i;
-      if (r < a.w.rows) a.out[r] = e.res[i] + (float)acc[i];
+      if (r < a.w.rows) a.out[r] = __fadd_rn(e.res[i], (float)acc[i]);
     }
   }
   if constexpr (EPI == EPI_SWIGLU) {
-    // h[j] = silu(g) * u over the f32 gate and up outputs, in f64 (src/core/ops.js:81-91).
+    // h[j] = silu(g) * u over the f32 gate and up outputs, in f64 (src/core/ops.js:81-91),
+    // or in f32 (fast numerics, the WGSL kernel's evaluation).
 #pragma unroll
     for (int i = 0; i < R; i += 2) {
       const int r = it * R + i;
       if (r + 1 < a.w.rows) {
-        const double g = (float)acc[i];
-        const double u = (float)acc[i + 1];
-        a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * u);
+        if constexpr (kF32) {
+          a.out[r >> 1] = swiglu_f32((float)acc[i], (float)acc[i + 1]);
+        } else {
+          const double g = (float)acc[i];
+          const double u = (float)acc[i + 1];
+          a.out[r >> 1] = (float)(g / (1.0 + exp(-g)) * u);
+        }
       }
     }
   }
@@ -191,14 +199,15 @@ struct Item {
 
 // LOOP: a team has several items (the output head): two named item buffers
 // alternate, so the next item's loads are in flight during this one's arithmetic
-// without register copies that would wait on them.
-template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool LOOP>
+// without register copies that would wait on them. F32: the fast-numerics core
+// (f32 staging with chunk sums, f32 sums); else f64 as the CPU path sums.
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool LOOP, bool F32>
 __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
   __shared__ ArgPair tbest[kBlock / TL];
   __shared__ float wl[PRO == PRO_COMBINE ? kBlock : 1];
-  double* xs = smem;
+  using Acc = typename std::conditional<F32, float, double>::type;
   using T = Teams<TL>;
   const int lane = T::lane();
   const int stride = gridDim.x * T::kTeams;
@@ -215,31 +224,44 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   else pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
   Item<FMT, TL, R, KC, EPI> A, B;
   A.load(a, it, pos, lane);
-  const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
-  if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish(pin, a.eps, a.w.cols, xs, red, lay);
-  else if constexpr (PRO == PRO_COMBINE) stage_attn_combine(pin, a.heads, xs, lay, wl);
-  else stage_copy_finish(pin, a.w.cols, xs, lay);
+  if constexpr (F32) {
+    float* xs = reinterpret_cast<float*>(smem);
+    const XLayoutF lay = chunk_layout_f<FMT>(a.w.nchunks);
+    if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish_f32<FMT>(pin, a.eps, a.w.cols, xs, red, lay);
+    else if constexpr (PRO == PRO_COMBINE) stage_attn_combine_f32<FMT>(pin, a.heads, xs, lay, wl);
+    else stage_copy_finish_f32<FMT>(pin, a.w.cols, xs, lay);
+  } else {
+    double* xs = smem;
+    const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
+    if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish(pin, a.eps, a.w.cols, xs, red, lay);
+    else if constexpr (PRO == PRO_COMBINE) stage_attn_combine(pin, a.heads, xs, lay, wl);
+    else stage_copy_finish(pin, a.w.cols, xs, lay);
+  }
 
+  auto dot = [&](const WTile<FMT, R, KC>& w, Acc (&acc)[R]) {
+    if constexpr (F32) wtile_dot_f32<FMT, R, KC, TL>(a.w, w, reinterpret_cast<const float*>(smem), lane, acc);
+    else wtile_dot<FMT, R, KC, TL>(a.w, w, smem, lane, acc);
+  };
   float bv = NAN;
   int bi = 0x7fffffff;
-  double acc[R];
+  Acc acc[R];
   if constexpr (!LOOP) {
     if (it < a.items) {
-      wtile_dot<FMT, R, KC, TL>(a.w, A.w, xs, lane, acc);
-      if (lane == 0) epilogue<R, EPI>(a, it, pos, A.rows, acc, A.e, bv, bi);
+      dot(A.w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, A.rows, acc, A.e, bv, bi);
     }
   } else {
     while (it < a.items) {
       B.load(a, it + stride, pos, lane);
       __builtin_amdgcn_sched_barrier(0);
-      wtile_dot<FMT, R, KC, TL>(a.w, A.w, xs, lane, acc);
-      if (lane == 0) epilogue<R, EPI>(a, it, pos, A.rows, acc, A.e, bv, bi);
+      dot(A.w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, A.rows, acc, A.e, bv, bi);
       it += stride;
       if (it >= a.items) break;
       A.load(a, it + stride, pos, lane);
       __builtin_amdgcn_sched_barrier(0);
-      wtile_dot<FMT, R, KC, TL>(a.w, B.w, xs, lane, acc);
-      if (lane == 0) epilogue<R, EPI>(a, it, pos, B.rows, acc, B.e, bv, bi);
+      dot(B.w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, B.rows, acc, B.e, bv, bi);
       it += stride;
     }
   }
@@ -337,18 +359,25 @@ static int fused_blocks(int items, int teams, int max_blocks) {
   return blocks;
 }
 
-template <int FMT, int TL, int R, int KC, int PRO, int EPI>
-static hipError_t fused_t(hipStream_t s, FusedArgs a, int items, int max_blocks) {
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool F32>
+static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks) {
   using T = Teams<TL>;
   a.items = items;
   const int blocks = fused_blocks(items, T::kTeams, max_blocks);
-  const size_t lds = (size_t)a.w.cols * sizeof(double);
+  const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
+                         : (size_t)a.w.cols * sizeof(double);
   if ((size_t)blocks * T::kTeams >= (size_t)items) {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false>), dim3(blocks), dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false, F32>), dim3(blocks), dim3(kBlock), lds, s, a);
   } else {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true>), dim3(blocks), dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true, F32>), dim3(blocks), dim3(kBlock), lds, s, a);
   }
   return hipGetLastError();
+}
+
+template <int FMT, int TL, int R, int KC, int PRO, int EPI>
+static hipError_t fused_t(hipStream_t s, const FusedArgs& a, int items, int max_blocks) {
+  if (a.f32) return fused_l<FMT, TL, R, KC, PRO, EPI, true>(s, a, items, max_blocks);
+  return fused_l<FMT, TL, R, KC, PRO, EPI, false>(s, a, items, max_blocks);
 }
 
 template <int FMT, int R, int PRO, int EPI>
@@ -408,6 +437,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
   uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
   uint16_t* vt = kc + c.key_elems;
   FusedArgs f{};
+  f.f32 = m.numerics == QH_NUMERICS_FAST;
   switch (role) {
     case QH_ROLE_QKV:
       f.eps = m.eps;
@@ -439,9 +469,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         a.heads = m.heads;
         a.kv_heads = m.kv_heads;
         a.max_slots = kDecodeSlots;
-        const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
-        hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, 1), dim3(kBlock),
-                           0, s, a);
+        return launch_attn_slots<kDecodeSlots>(s, a, 1, 1);
       } else {
         ExactArgs a{};
         a.q = c.q;
@@ -496,6 +524,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
 // The output head's matvec alone (final rmsnorm, lm_head, logits, block argmax partials).
 static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c) {
   FusedArgs f{};
+  f.f32 = m.numerics == QH_NUMERICS_FAST;
   f.eps = m.eps;
   f.w = m.lm_head;
   f.in = c.x;

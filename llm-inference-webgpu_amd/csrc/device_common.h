@@ -438,6 +438,218 @@ __device__ __forceinline__ void wtile_dot(const DMat& m, const WTile<FMT, R, KC>
   for (int i = 0; i < R; i++) acc[i] = team_sum<TL>(acc[i]);
 }
 
+// ------------------------------------------------- f32 matvec core (FAST) --
+// QH_NUMERICS_FAST sums every output in f32, as the reference's WebGPU kernels
+// do (weights f16 in storage, activations f32, f32 accumulation; README.md
+// "Precision is stated rather than inherited", src/gpu/kernels.js:33-79). The
+// activations are the same f32 values the exact path stages; only the sums
+// differ, by f32 rounding (~sqrt(n) * 2^-24 relative).
+//
+// Quantized chunks take the scale out of the sum: an int8 chunk contributes
+// sum((q+128) x) - 128 sum(x), an int4 chunk scale * (sum(level x) - zero sum(x)),
+// with the codes converted by one v_cvt_f32_ubyte each (int8 biased by an xor,
+// int4 even nibbles masked in place and odd ones masked as 16*level, rescaled by
+// the exact 1/16 once per chunk), so a weight costs one conversion and one f32
+// fma. sum(x) over each chunk (the "chunk sum") is computed once, while staging,
+// as a pairwise tree: ((x0+x1)+(x2+x3)) per 4-element group, then a butterfly
+// over the chunk's groups. A row's chunk contributions are added in ascending
+// chunk order per lane, then across the team by team_sum, so every path over a
+// matrix (decode tile, streamed prefill tile) sums one output in one order.
+//
+// Staged f32 layout (XLayoutF): 4-element group g of chunk c at float offset
+// 4*(g*nc + c) -- the team's lanes, each on its own chunk, read consecutive
+// 16-byte slots (ds_read_b128 without bank conflicts).
+struct XLayoutF {
+  int lw, nc;  // W = 1 << lw elements per chunk, nc chunks per row
+  __device__ __forceinline__ int pos(int i) const {
+    const int e = i & ((1 << lw) - 1);
+    return (((e >> 2) * nc + (i >> lw)) << 2) | (e & 3);
+  }
+};
+template <int FMT>
+__host__ __device__ inline XLayoutF chunk_layout_f(int nchunks) {
+  constexpr int lw = FMT == QH_FMT_F16 ? 3 : FMT == QH_FMT_INT8 ? 4 : 5;
+  return XLayoutF{lw, nchunks};
+}
+
+// Floats of LDS an f32-staged vector of `cols` values (a multiple of 4) takes: the
+// values, then one chunk sum per chunk, rounded up to whole 16-byte groups.
+__host__ __device__ inline int staged_f32_floats(int cols, int nchunks) { return cols + ((nchunks + 3) & ~3); }
+
+// The chunk sum over the G lanes (G = 4-element groups per chunk: int8 4, int4 8)
+// that hold one chunk's groups, from each lane's group sum; every lane of the G
+// ends with the same bits (each step adds a symmetric pair).
+template <int G>
+__device__ __forceinline__ float chunk_group_sum(float s4) {
+  static_assert(G == 4 || G == 8, "lanes per chunk");
+  s4 += dpp32<kDppQuadXor1>(s4);
+  s4 += dpp32<kDppQuadXor2>(s4);
+  if constexpr (G == 8) s4 += dpp32<kDppHalfMirror>(s4);
+  return s4;
+}
+
+// Stores 4-element group gi (value v) of an f32-staged vector and, for quantized
+// formats, its chunk's sum into sxs[gi / G]. Every lane of the wave must call it
+// together (the chunk sum is a cross-lane butterfly); `valid` false for lanes past
+// the vector, whose groups only complete chunks that do not exist.
+template <int FMT>
+__device__ __forceinline__ void stage_group_f32(v4f v, int gi, bool valid, float* xs, float* sxs,
+                                                XLayoutF lay) {
+  if (valid) *reinterpret_cast<v4f*>(xs + lay.pos(4 * gi)) = v;
+  if constexpr (FMT != QH_FMT_F16) {
+    constexpr int G = Fmt<FMT>::kW / 4;
+    float s4 = valid ? (v.x + v.y) + (v.z + v.w) : 0.f;
+    s4 = chunk_group_sum<G>(s4);
+    if (valid && (gi & (G - 1)) == 0) sxs[gi / G] = s4;
+  }
+}
+
+// acc[r] += the f32 dot of chunk row w[r] with the staged chunk at p (group g at
+// p + g*gs), for R rows element-major. s/z: int4 group scale and zero point of each
+// row (int8 takes its row scale after the team sum); sx the chunk sum.
+template <int FMT, int R>
+__device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* __restrict__ p, int gs,
+                                               const float (&s)[R], const float (&z)[R], float sx,
+                                               float (&acc)[R]) {
+  if constexpr (FMT == QH_FMT_F16) {
+    const v4f x0 = *reinterpret_cast<const v4f*>(p);
+    const v4f x1 = *reinterpret_cast<const v4f*>(p + gs);
+    const float xe[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r] = fmaf(f16_lo(w[r][k]), xe[2 * k], acc[r]);
+#pragma unroll
+      for (int r = 0; r < R; r++) acc[r] = fmaf(f16_hi(w[r][k]), xe[2 * k + 1], acc[r]);
+    }
+  } else if constexpr (FMT == QH_FMT_INT8) {
+    const float c0 = -128.f * sx;  // exact
+    float d[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) d[r] = c0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const v4f x = *reinterpret_cast<const v4f*>(p + k * gs);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t m = w[r][k] ^ 0x80808080u;  // q + 128 in every byte
+        d[r] = fmaf(ubyte<0>(m), x.x, d[r]);
+        d[r] = fmaf(ubyte<1>(m), x.y, d[r]);
+        d[r] = fmaf(ubyte<2>(m), x.z, d[r]);
+        d[r] = fmaf(ubyte<3>(m), x.w, d[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] += d[r];
+  } else {
+    float pe[R], po[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      pe[r] = -z[r] * sx;
+      po[r] = 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      // dword k holds elements 8k .. 8k+7: byte b = (element 8k+2b) | (element 8k+2b+1) << 4
+      const v4f xa = *reinterpret_cast<const v4f*>(p + (2 * k) * gs);
+      const v4f xb = *reinterpret_cast<const v4f*>(p + (2 * k + 1) * gs);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t lo = w[r][k] & 0x0F0F0F0Fu, hi = w[r][k] & 0xF0F0F0F0u;
+        pe[r] = fmaf(ubyte<0>(lo), xa.x, pe[r]);
+        po[r] = fmaf(ubyte<0>(hi), xa.y, po[r]);
+        pe[r] = fmaf(ubyte<1>(lo), xa.z, pe[r]);
+        po[r] = fmaf(ubyte<1>(hi), xa.w, po[r]);
+        pe[r] = fmaf(ubyte<2>(lo), xb.x, pe[r]);
+        po[r] = fmaf(ubyte<2>(hi), xb.y, po[r]);
+        pe[r] = fmaf(ubyte<3>(lo), xb.z, pe[r]);
+        po[r] = fmaf(ubyte<3>(hi), xb.w, po[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = fmaf(s[r], fmaf(po[r], 0.0625f, pe[r]), acc[r]);
+  }
+}
+
+// a * b rounded on its own: never fused into a multiply-add with the operation that
+// consumes it (HIP's __fmul_rn is a plain, contractible multiply).
+__device__ __forceinline__ float mul_rounded(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
+// The output of a team-summed f32 row: int8 applies the row scale, rounded before
+// any later add (the decode epilogue and the prefill's separate residual add see the
+// same value).
+template <int FMT>
+__device__ __forceinline__ float row_out_f32(float sum, float srow) {
+  if constexpr (FMT == QH_FMT_INT8) return mul_rounded(srow, sum);
+  else return sum;
+}
+
+// wtile_dot in f32: xs is staged by stage_group_f32 (values, then chunk sums at
+// xs + m.cols). Returns the team sums with the int8 row scale applied.
+template <int FMT, int R, int KC, int TL>
+__device__ __forceinline__ void wtile_dot_f32(const DMat& m, const WTile<FMT, R, KC>& t, const float* xs,
+                                              int tl, float (&acc)[R]) {
+  const float* sxs = xs + m.cols;
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = 0.f;
+#pragma unroll
+  for (int k = 0; k < KC; k++) {
+    const int c = tl + k * TL;
+    if (c < m.nchunks) {
+      const float sx = FMT == QH_FMT_F16 ? 0.f : sxs[c];
+      chunk_rows_f32<FMT, R>(t.w[k], xs + 4 * c, 4 * m.nchunks, t.s[k], t.z[k], sx, acc);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = row_out_f32<FMT>(team_sum<TL>(acc[i]), t.s[0][i]);
+}
+
+// mv_team in f32 over NB positions staged at xs + b*xstride (each a stage_group_f32
+// vector: values, then chunk sums at + m.cols).
+template <int FMT, int R, int NB, int TL>
+__device__ __forceinline__ void mv_team_f32(const DMat& m, const int (&rows)[R], const float* xs, int xstride,
+                                            int tl, float (&acc)[NB][R]) {
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+#pragma unroll
+    for (int i = 0; i < R; i++) acc[b][i] = 0.f;
+  const v4u* rp[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) rp[i] = reinterpret_cast<const v4u*>(m.data + (size_t)rows[i] * m.row_bytes);
+  float srow[R] = {};
+  if constexpr (FMT == QH_FMT_INT8) {
+#pragma unroll
+    for (int i = 0; i < R; i++) srow[i] = m.scales[rows[i]];
+  }
+  for (int c = tl; c < m.nchunks; c += TL) {
+    v4u w[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) w[i] = __builtin_nontemporal_load(&rp[i][c]);
+    float s[R] = {}, z[R] = {};
+    if constexpr (FMT == QH_FMT_INT4) {
+      const int g = c / m.cpg;
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        s[i] = m.scales[(size_t)rows[i] * m.gpr + g];
+        z[i] = m.zeros[(size_t)rows[i] * m.gpr + g];
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+      const float* xb = xs + (size_t)b * xstride;
+      const float sx = FMT == QH_FMT_F16 ? 0.f : xb[m.cols + c];
+      chunk_rows_f32<FMT, R>(w, xb + 4 * c, 4 * m.nchunks, s, z, sx, acc[b]);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+#pragma unroll
+    for (int i = 0; i < R; i++) acc[b][i] = row_out_f32<FMT>(team_sum<TL>(acc[b][i]), srow[i]);
+}
+
 // Team width of a matrix: 32 lanes when a row has at most 32 chunks, else 64.
 // It fixes which chunks a lane sums and the butterfly, so it is a function of
 // the shape alone and every path over a given matrix sums in one order.
@@ -543,6 +755,61 @@ __device__ __forceinline__ void stage_copy_finish(const StageIn& in, int n, doub
     }
   }
   __syncthreads();
+}
+
+// The staging above for the f32 core: the same f32 values (rmsnorm's statistic and
+// products still in f64), stored by stage_group_f32 with their chunk sums after
+// the `cols` values.
+template <int FMT>
+__device__ __forceinline__ void stage_rmsnorm_finish_f32(const StageIn& in, double eps, int cols, float* xs,
+                                                         double* red, XLayoutF lay) {
+  const int n4 = cols >> 2;
+  double ss = 0;
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    if (threadIdx.x + j * kBlock < n4) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) ss = fma((double)in.v[j][e], (double)in.v[j][e], ss);
+    }
+  }
+  ss = block_sum_f64(ss, red);
+  const double scale = 1.0 / sqrt(ss / cols + eps);
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    if (j * kBlock < n4) {  // uniform over the block
+      const int i = threadIdx.x + j * kBlock;
+      const bool valid = i < n4;
+      v4f v = {0.f, 0.f, 0.f, 0.f};
+      if (valid) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = (float)((double)in.v[j][e] * scale * (double)in.g[j][e]);
+      }
+      stage_group_f32<FMT>(v, i, valid, xs, xs + cols, lay);
+    }
+  }
+  __syncthreads();
+}
+
+template <int FMT>
+__device__ __forceinline__ void stage_copy_finish_f32(const StageIn& in, int n, float* xs, XLayoutF lay) {
+  const int n4 = n >> 2;
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    if (j * kBlock < n4) {
+      const int i = threadIdx.x + j * kBlock;
+      const bool valid = i < n4;
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      stage_group_f32<FMT>(valid ? in.v[j] : zero, i, valid, xs, xs + n, lay);
+    }
+  }
+  __syncthreads();
+}
+
+// silu(g) * u in f32, as the reference's WGSL SWIGLU evaluates it
+// (src/gpu/kernels.js:502-514): g / (1 + e^-g) * up, each operation rounded alone.
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+#pragma clang fp contract(off)
+  return g / (1.0f + expf(-g)) * u;
 }
 
 struct ArgPair {

@@ -72,13 +72,19 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge_rows(const float* __restr
   }
 }
 
-// h[t][j] = silu(g) * u over interleaved gate|up rows (g = gu[t][2j], u = gu[t][2j+1]), in
-// f64 as the decode step's SWIGLU epilogue (src/core/ops.js:81-91).
+// h[t][j] = silu(g) * u over interleaved gate|up rows (g = gu[t][2j], u = gu[t][2j+1]), as
+// the decode step's SWIGLU epilogue evaluates it: in f64 (src/core/ops.js:81-91), or in
+// f32 for fast numerics (F32).
+template <bool F32>
 __global__ void k_swiglu_pairs(const float* __restrict__ gu, float* __restrict__ h, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const double g = gu[2 * i], u = gu[2 * i + 1];
-  h[i] = (float)(g / (1.0 + exp(-g)) * u);
+  if constexpr (F32) {
+    h[i] = swiglu_f32(gu[2 * i], gu[2 * i + 1]);
+  } else {
+    const double g = gu[2 * i], u = gu[2 * i + 1];
+    h[i] = (float)(g / (1.0 + exp(-g)) * u);
+  }
 }
 
 // rows [seq][hidden] = bf16 embedding rows of tokens[past .. past+seq-1], widened exactly.
@@ -115,7 +121,7 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
   for (int L = 0; L < m.layers; L++) {
     const LayerDev& l = m.layers_host[L];
     for (const DMat* w : {&l.qkv, &l.o, &l.gu, &l.down}) {
-      scratch = std::max(scratch, matvec_x64_bytes(*w, (int)P));
+      if (m.numerics == QH_NUMERICS_EXACT) scratch = std::max(scratch, matvec_x64_bytes(*w, (int)P));
       if (matmul == QH_MATMUL_MFMA && w->format != QH_FMT_F16)
         scratch = std::max(scratch, matmul_prefill_scratch_bytes(*w, (int)P));
     }
@@ -124,10 +130,13 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
   return b;
 }
 
-static hipError_t matmul(hipStream_t s, int mode, const DMat& w, const float* x, const float* bias, float* y,
-                         int seq, const PrefillDev& p) {
+// The layer's matmul: MFMA (int8/int4 weights), or the batched matvec tiles summing as
+// the decode step does for the model's numerics.
+static hipError_t matmul(hipStream_t s, const ModelDev& m, int mode, const DMat& w, const float* x,
+                         const float* bias, float* y, int seq, const PrefillDev& p) {
   if (mode == QH_MATMUL_MFMA && w.format != QH_FMT_F16)
     return launch_matmul_prefill(s, w, x, bias, y, seq, p.scratch);
+  if (m.numerics == QH_NUMERICS_FAST) return launch_matvec_f32(s, w, x, bias, y, seq);
   return launch_matvec(s, w, x, bias, y, seq, static_cast<double*>(p.scratch));
 }
 
@@ -141,7 +150,7 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
     uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
     uint16_t* vt = kc + c.key_elems;
     if ((e = launch_rmsnorm(s, p.X, l.in_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
-    if ((e = matmul(s, mode, l.qkv, p.XN, l.qkv_bias, p.QKV, seq, p)) != hipSuccess) return e;
+    if ((e = matmul(s, m, mode, l.qkv, p.XN, l.qkv_bias, p.QKV, seq, p)) != hipSuccess) return e;
     const int items = (m.heads + m.kv_heads) * 32 + kvd;
     hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, p.Q, kc, vt, m.rope_cos,
                        m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
@@ -158,10 +167,7 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
       a.heads = m.heads;
       a.kv_heads = m.kv_heads;
       a.max_slots = kDecodeSlots;
-      const int waves = m.heads * kDecodeSlots, per_block = kBlock / kWave;
-      hipLaunchKernelGGL(k_attn_slots<kDecodeSlots>, dim3((waves + per_block - 1) / per_block, seq), dim3(kBlock),
-                         0, s, a);
-      if ((e = hipGetLastError()) != hipSuccess) return e;
+      if ((e = launch_attn_slots<kDecodeSlots>(s, a, seq, 1)) != hipSuccess) return e;
       hipLaunchKernelGGL(k_attn_merge_rows, dim3(seq), dim3(kBlock), 0, s, p.part, m.heads, p.ATT);
     } else {
       ExactArgs a{};
@@ -187,14 +193,17 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
       }
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = matmul(s, mode, l.o, p.ATT, nullptr, p.Y, seq, p)) != hipSuccess) return e;
+    if ((e = matmul(s, m, mode, l.o, p.ATT, nullptr, p.Y, seq, p)) != hipSuccess) return e;
     if ((e = launch_add(s, p.X, p.Y, (int)n)) != hipSuccess) return e;
     if ((e = launch_rmsnorm(s, p.X, l.post_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
-    if ((e = matmul(s, mode, l.gu, p.XN, nullptr, p.GU, seq, p)) != hipSuccess) return e;
+    if ((e = matmul(s, m, mode, l.gu, p.XN, nullptr, p.GU, seq, p)) != hipSuccess) return e;
     const size_t nh = (size_t)seq * f;
-    hipLaunchKernelGGL(k_swiglu_pairs, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, s, p.GU, p.H, nh);
+    if (m.numerics == QH_NUMERICS_FAST)
+      hipLaunchKernelGGL(k_swiglu_pairs<true>, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, s, p.GU, p.H, nh);
+    else
+      hipLaunchKernelGGL(k_swiglu_pairs<false>, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, s, p.GU, p.H, nh);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if ((e = matmul(s, mode, l.down, p.H, nullptr, p.Y, seq, p)) != hipSuccess) return e;
+    if ((e = matmul(s, m, mode, l.down, p.H, nullptr, p.Y, seq, p)) != hipSuccess) return e;
     if ((e = launch_add(s, p.X, p.Y, (int)n)) != hipSuccess) return e;
   }
   return hipSuccess;

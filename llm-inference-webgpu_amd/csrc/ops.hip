@@ -146,6 +146,112 @@ hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const flo
   return e;
 }
 
+// ------------------------------------------------------------ f32 matvec --
+// The fast-numerics matvec of the batched prefill: y[b, r] = f32 sum of row r with
+// position b's x (+ bias), summed by the f32 core exactly as the decode step's
+// fused launches sum it, so a prefill tile and the same position decoded alone give
+// the same bits. All NB staged positions (values + chunk sums) sit in LDS.
+template <int FMT, int R, int NB, int TL>
+__global__ __launch_bounds__(kBlock) void k_matvec_f32(DMat m, const float* __restrict__ x,
+                                                       const float* __restrict__ bias, float* __restrict__ y,
+                                                       int b_base) {
+  extern __shared__ double smem[];
+  float* xs = reinterpret_cast<float*>(smem);
+  const int b0 = b_base + blockIdx.y * NB;
+  const int per = staged_f32_floats(m.cols, m.nchunks);
+  const XLayoutF lay = chunk_layout_f<FMT>(m.nchunks);
+  const int n4 = m.cols >> 2;
+  // Groups of the NB positions in order; a chunk's groups are G consecutive lanes
+  // (G divides n4 and kBlock), so every position's chunk sums are butterflies inside
+  // one wave, and the trip count is the same for every lane.
+  for (int base = 0; base < NB * n4; base += kBlock) {
+    const int gi = base + threadIdx.x;
+    const bool valid = gi < NB * n4;
+    const int b = valid ? gi / n4 : 0, g = valid ? gi - b * n4 : 0;
+    v4f v = {0.f, 0.f, 0.f, 0.f};
+    if (valid) v = reinterpret_cast<const v4f*>(x + (size_t)(b0 + b) * m.cols)[g];
+    float* xb = xs + (size_t)b * per;
+    stage_group_f32<FMT>(v, g, valid, xb, xb + m.cols, lay);
+  }
+  __syncthreads();
+  using T = Teams<TL>;
+  const int row0 = (blockIdx.x * T::kTeams + T::team()) * R;
+  if (row0 >= m.rows) return;
+  int rows[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) rows[i] = min(row0 + i, m.rows - 1);
+  float acc[NB][R];
+  mv_team_f32<FMT, R, NB, TL>(m, rows, xs, per, T::lane(), acc);
+  if (T::lane() == 0) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const int r = row0 + i;
+        if (r >= m.rows) break;
+        y[(size_t)(b0 + b) * m.rows + r] = bias ? __fadd_rn(acc[b][i], bias[r]) : acc[b][i];
+      }
+    }
+  }
+}
+
+template <int NB>
+static bool f32_tile_fits(const DMat& m) {
+  return (size_t)NB * staged_f32_floats(m.cols, m.nchunks) * sizeof(float) <= kMatvecLdsBytes;
+}
+
+template <int FMT, int NB>
+static hipError_t matvec_f32_nb(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
+                                int b_base, int tiles) {
+  constexpr int R = 2;
+  const size_t lds = (size_t)NB * staged_f32_floats(m.cols, m.nchunks) * sizeof(float);
+  if (team_width(m.nchunks) == 32) {
+    const dim3 grid((m.rows + (kBlock / 32) * R - 1) / ((kBlock / 32) * R), tiles);
+    hipLaunchKernelGGL((k_matvec_f32<FMT, R, NB, 32>), grid, dim3(kBlock), lds, s, m, x, bias, y, b_base);
+  } else {
+    const dim3 grid((m.rows + (kBlock / 64) * R - 1) / ((kBlock / 64) * R), tiles);
+    hipLaunchKernelGGL((k_matvec_f32<FMT, R, NB, 64>), grid, dim3(kBlock), lds, s, m, x, bias, y, b_base);
+  }
+  return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t matvec_f32_fmt(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
+                                 int seq) {
+  // The widest tile of 8, 4, 2 or 1 positions whose staged vectors fit in LDS, then
+  // narrower tiles for the remainder.
+  hipError_t e = hipSuccess;
+  int done = 0;
+  if (seq >= 8 && f32_tile_fits<8>(m)) {
+    if ((e = matvec_f32_nb<FMT, 8>(s, m, x, bias, y, 0, seq / 8)) != hipSuccess) return e;
+    done = seq / 8 * 8;
+  }
+  if (seq - done >= 4 && f32_tile_fits<4>(m)) {
+    const int tiles = (seq - done) / 4;
+    if ((e = matvec_f32_nb<FMT, 4>(s, m, x, bias, y, done, tiles)) != hipSuccess) return e;
+    done += tiles * 4;
+  }
+  if (seq - done >= 2 && f32_tile_fits<2>(m)) {
+    const int tiles = (seq - done) / 2;
+    if ((e = matvec_f32_nb<FMT, 2>(s, m, x, bias, y, done, tiles)) != hipSuccess) return e;
+    done += tiles * 2;
+  }
+  if (seq - done >= 1) e = matvec_f32_nb<FMT, 1>(s, m, x, bias, y, done, seq - done);
+  return e;
+}
+
+bool matvec_f32_supported(const DMat& m) { return f32_tile_fits<1>(m) && m.cols % 4 == 0; }
+
+hipError_t launch_matvec_f32(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
+                             int seq) {
+  if (!matvec_f32_supported(m)) return hipErrorInvalidValue;
+  switch (m.format) {
+    case QH_FMT_F16: return matvec_f32_fmt<QH_FMT_F16>(s, m, x, bias, y, seq);
+    case QH_FMT_INT8: return matvec_f32_fmt<QH_FMT_INT8>(s, m, x, bias, y, seq);
+    default: return matvec_f32_fmt<QH_FMT_INT4>(s, m, x, bias, y, seq);
+  }
+}
+
 // ------------------------------------------- matvec with an f16 activation --
 // The isolated-matvec shape: x f16, int8 weights, one output
 // vector per matrix of a list. Codes are widened to exact f16 pairs and
@@ -365,10 +471,7 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
   a.heads = heads;
   a.kv_heads = kv_heads;
   a.max_slots = kOpSlots;
-  const int waves = heads * kOpSlots;
-  const int per_block = kBlock / kWave;
-  hipLaunchKernelGGL(k_attn_slots<kOpSlots>, dim3((waves + per_block - 1) / per_block, seq), dim3(kBlock), 0, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch_attn_slots<kOpSlots>(s, a, seq, 1);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
                      kOpSlots, (size_t)0);
@@ -389,9 +492,7 @@ template <int MAXS>
 static hipError_t list_t(hipStream_t s, SlotArgs a, int count, float* out) {
   a.max_slots = MAXS;
   a.list_part = (size_t)a.heads * MAXS * kPartStride;
-  const int waves = a.heads * MAXS, per_block = kBlock / kWave;
-  hipLaunchKernelGGL(k_attn_slots<MAXS>, dim3((waves + per_block - 1) / per_block, 1, count), dim3(kBlock), 0, s, a);
-  hipError_t e = hipGetLastError();
+  hipError_t e = launch_attn_slots<MAXS>(s, a, 1, count);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
                      a.list_part);

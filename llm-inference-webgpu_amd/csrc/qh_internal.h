@@ -82,6 +82,12 @@ namespace qh {
 hipError_t launch_matvec(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
                          int seq, double* x64_scratch = nullptr);
 size_t matvec_x64_bytes(const DMat& m, int seq);
+// The same product summed in f32 (fast numerics), as the decode step's fused launches
+// sum it in that mode. Needs cols % 4 == 0 and one staged position within 64 KiB of LDS
+// (matvec_f32_supported).
+hipError_t launch_matvec_f32(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
+                             int seq);
+bool matvec_f32_supported(const DMat& m);
 // The batched-prefill contraction on bf16 MFMA (int8 / int4 weights): y [M, rows] = x [M, cols] . W^T
 // (+ bias). `scratch` holds matmul_prefill_scratch_bytes(w, M) bytes.
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias, float* y,
