@@ -227,7 +227,8 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   if constexpr (F32) {
     float* xs = reinterpret_cast<float*>(smem);
     const XLayoutF lay = chunk_layout_f<FMT>(a.w.nchunks);
-    if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish_f32<FMT>(pin, a.eps, a.w.cols, xs, red, lay);
+    if constexpr (PRO == PRO_RMSNORM)
+      stage_rmsnorm_finish_f32<FMT>(pin, (float)a.eps, a.w.cols, xs, reinterpret_cast<float*>(red), lay);
     else if constexpr (PRO == PRO_COMBINE) stage_attn_combine_f32<FMT>(pin, a.heads, xs, lay, wl);
     else stage_copy_finish_f32<FMT>(pin, a.w.cols, xs, lay);
   } else {
@@ -295,23 +296,28 @@ __global__ __launch_bounds__(kBlock) void k_pick(const ArgPair* __restrict__ par
                                                  int vocab, float* __restrict__ x) {
   __shared__ ArgPair wred[kBlock / kWave];
   __shared__ int next;
+  // What does not depend on the argmax is read first, alongside the partials: the
+  // position, the forced length and the caller's token at the next position.
+  const int p = state[0], forced = state[1];
+  const bool caller = p + 1 < forced && p + 1 <= capacity;  // the next input is the caller's token
+  const int given = caller ? tokens[p + 1] : 0;
+  const float first = logits[0];
   float v = NAN;
   int i = 0x7fffffff;
   for (int b = threadIdx.x; b < nparts; b += kBlock) {
-    const ArgPair p = partials[b];
-    if (argmax_better(p.v, p.i, v, i)) {
-      v = p.v;
-      i = p.i;
+    const ArgPair q = partials[b];
+    if (argmax_better(q.v, q.i, v, i)) {
+      v = q.v;
+      i = q.i;
     }
   }
   argmax_block(v, i, wred);
   if (threadIdx.x == 0) {
-    const int tok = (logits[0] != logits[0]) ? 0 : i;
-    const int p = state[0];
+    const int tok = (first != first) ? 0 : i;
     if (p < capacity) pred[p] = tok;
-    if (p + 1 >= state[1] && p + 1 <= capacity) tokens[p + 1] = tok;
+    if (p + 1 >= forced && p + 1 <= capacity) tokens[p + 1] = tok;
     state[0] = p + 1;
-    int t = p + 1 <= capacity ? tokens[p + 1] : tok;
+    const int t = caller ? given : tok;
     next = (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
   }
   __syncthreads();

@@ -524,12 +524,15 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
     }
   } else if constexpr (FMT == QH_FMT_INT8) {
     const float c0 = -128.f * sx;  // exact
+    v4f xg[4];  // the chunk's activations, all read before any arithmetic
+#pragma unroll
+    for (int k = 0; k < 4; k++) xg[k] = *reinterpret_cast<const v4f*>(p + k * gs);
     float d[R];
 #pragma unroll
     for (int r = 0; r < R; r++) d[r] = c0;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      const v4f x = *reinterpret_cast<const v4f*>(p + k * gs);
+      const v4f x = xg[k];
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const uint32_t m = w[r][k] ^ 0x80808080u;  // q + 128 in every byte
@@ -548,11 +551,13 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
       pe[r] = -z[r] * sx;
       po[r] = 0.f;
     }
+    v4f xg[8];  // the chunk's activations, all read before any arithmetic
+#pragma unroll
+    for (int k = 0; k < 8; k++) xg[k] = *reinterpret_cast<const v4f*>(p + k * gs);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       // dword k holds elements 8k .. 8k+7: byte b = (element 8k+2b) | (element 8k+2b+1) << 4
-      const v4f xa = *reinterpret_cast<const v4f*>(p + (2 * k) * gs);
-      const v4f xb = *reinterpret_cast<const v4f*>(p + (2 * k + 1) * gs);
+      const v4f xa = xg[2 * k], xb = xg[2 * k + 1];
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const uint32_t lo = w[r][k] & 0x0F0F0F0Fu, hi = w[r][k] & 0xF0F0F0F0u;
@@ -757,33 +762,60 @@ __device__ __forceinline__ void stage_copy_finish(const StageIn& in, int n, doub
   __syncthreads();
 }
 
-// The staging above for the f32 core: the same f32 values (rmsnorm's statistic and
-// products still in f64), stored by stage_group_f32 with their chunk sums after
-// the `cols` values.
-template <int FMT>
-__device__ __forceinline__ void stage_rmsnorm_finish_f32(const StageIn& in, double eps, int cols, float* xs,
-                                                         double* red, XLayoutF lay) {
+// rmsnorm in f32 for fast numerics, the WGSL RMSNORM's arithmetic
+// (src/gpu/kernels.js:300-341): an f32 sum of squares, scale = inverseSqrt(sum / cols
+// + eps), y = x * scale * gain. Both the decode staging and the prefill's rmsnorm
+// launch evaluate it with the same thread-to-element map (StageIn), so they agree
+// bit for bit.
+//
+// Sum over the block in f32, fixed order; `red` (kBlock/kWave floats of LDS) must not
+// be reused before the caller's next barrier.
+__device__ __forceinline__ float block_sum_f32(float v, float* red) {
+  v = team_sum<64>(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < kBlock / kWave; w++) t += red[w];
+  return t;
+}
+
+__device__ __forceinline__ float rms_scale_f32(const StageIn& in, int cols, float eps, float* red) {
   const int n4 = cols >> 2;
-  double ss = 0;
+  float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < kStageVec; j++) {
     if (threadIdx.x + j * kBlock < n4) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) ss = fma((double)in.v[j][e], (double)in.v[j][e], ss);
+      for (int e = 0; e < 4; e++) ss = fmaf(in.v[j][e], in.v[j][e], ss);
     }
   }
-  ss = block_sum_f64(ss, red);
-  const double scale = 1.0 / sqrt(ss / cols + eps);
+  ss = block_sum_f32(ss, red);
+  return __builtin_amdgcn_rsqf(ss / (float)cols + eps);
+}
+
+__device__ __forceinline__ v4f rms_apply_f32(v4f v, float scale, v4f g) {
+  v4f y;
+#pragma unroll
+  for (int e = 0; e < 4; e++) y[e] = mul_rounded(mul_rounded(v[e], scale), g[e]);
+  return y;
+}
+
+// The staging above for the f32 core: the f32 rmsnorm, stored by stage_group_f32
+// with the chunk sums after the `cols` values.
+template <int FMT>
+__device__ __forceinline__ void stage_rmsnorm_finish_f32(const StageIn& in, float eps, int cols, float* xs,
+                                                         float* red, XLayoutF lay) {
+  const int n4 = cols >> 2;
+  const float scale = rms_scale_f32(in, cols, eps, red);
 #pragma unroll
   for (int j = 0; j < kStageVec; j++) {
     if (j * kBlock < n4) {  // uniform over the block
       const int i = threadIdx.x + j * kBlock;
       const bool valid = i < n4;
       v4f v = {0.f, 0.f, 0.f, 0.f};
-      if (valid) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = (float)((double)in.v[j][e] * scale * (double)in.g[j][e]);
-      }
+      if (valid) v = rms_apply_f32(in.v[j], scale, in.g[j]);
       stage_group_f32<FMT>(v, i, valid, xs, xs + cols, lay);
     }
   }

@@ -149,7 +149,7 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
     const LayerDev& l = m.layers_host[L];
     uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
     uint16_t* vt = kc + c.key_elems;
-    if ((e = launch_rmsnorm(s, p.X, l.in_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
+    if ((e = launch_rmsnorm(s, p.X, l.in_norm, p.XN, seq, d, m.eps, m.numerics == QH_NUMERICS_FAST)) != hipSuccess) return e;
     if ((e = matmul(s, m, mode, l.qkv, p.XN, l.qkv_bias, p.QKV, seq, p)) != hipSuccess) return e;
     const int items = (m.heads + m.kv_heads) * 32 + kvd;
     hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, p.Q, kc, vt, m.rope_cos,
@@ -195,7 +195,7 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if ((e = matmul(s, m, mode, l.o, p.ATT, nullptr, p.Y, seq, p)) != hipSuccess) return e;
     if ((e = launch_add(s, p.X, p.Y, (int)n)) != hipSuccess) return e;
-    if ((e = launch_rmsnorm(s, p.X, l.post_norm, p.XN, seq, d, m.eps)) != hipSuccess) return e;
+    if ((e = launch_rmsnorm(s, p.X, l.post_norm, p.XN, seq, d, m.eps, m.numerics == QH_NUMERICS_FAST)) != hipSuccess) return e;
     if ((e = matmul(s, m, mode, l.gu, p.XN, nullptr, p.GU, seq, p)) != hipSuccess) return e;
     const size_t nh = (size_t)seq * f;
     if (m.numerics == QH_NUMERICS_FAST)

@@ -356,13 +356,36 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float* __restrict__ x,
   for (int i = threadIdx.x; i < cols; i += kBlock) y[base + i] = (float)smem[i];
 }
 
+// The f32 rmsnorm of the fast decode step's staging, one row per block.
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_f32(const float* __restrict__ x,
+                                                        const float* __restrict__ gain,
+                                                        float* __restrict__ y, int cols, float eps) {
+  __shared__ float red[kBlock / kWave];
+  const size_t base = (size_t)blockIdx.x * cols;
+  StageIn in;
+  in.load(x + base, gain, cols);
+  const float scale = rms_scale_f32(in, cols, eps, red);
+  const int n4 = cols >> 2;
+  v4f* y4 = reinterpret_cast<v4f*>(y + base);
+#pragma unroll
+  for (int j = 0; j < kStageVec; j++) {
+    const int i = threadIdx.x + j * kBlock;
+    if (i < n4) y4[i] = rms_apply_f32(in.v[j], scale, in.g[j]);
+  }
+}
+
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
-                          int cols, double eps) {
+                          int cols, double eps, bool f32) {
   // The vector staging reads float4 groups: every row start and the gain 16-byte aligned.
   const int vec = (cols % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)gain % 16 == 0) &&
-                  cols <= kStageMax;
-  hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), cols * sizeof(double), s, x, gain, y,
-                     cols, eps, vec);
+                  ((uintptr_t)y % 16 == 0) && cols <= kStageMax;
+  if (f32) {
+    if (!vec) return hipErrorInvalidValue;  // model shapes always stage as float4 groups
+    hipLaunchKernelGGL(k_rmsnorm_f32, dim3(rows), dim3(kBlock), 0, s, x, gain, y, cols, (float)eps);
+  } else {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(rows), dim3(kBlock), cols * sizeof(double), s, x, gain, y,
+                       cols, eps, vec);
+  }
   return hipGetLastError();
 }
 

@@ -95,8 +95,10 @@ hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, c
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
+// f32: the fast numerics' f32 rmsnorm (needs cols % 4 == 0, cols <= 8192 and 16-byte
+// aligned rows); else the CPU path's f64 evaluation.
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, float* y, int rows,
-                          int cols, double eps);
+                          int cols, double eps, bool f32 = false);
 hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float* sin_t, int rows,
                        int heads, int head_dim, int base_pos);
 // Keys [kv_heads][capacity][head_dim]; values dimension-major [kv_heads][head_dim][vstride],
