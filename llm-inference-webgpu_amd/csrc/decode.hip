@@ -506,7 +506,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         f.in = c.part;
         f.heads = m.heads;
         f.state = c.state;
-        return fused<2, PRO_COMBINE, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
+        return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows);
       }
       f.in = c.attn;
       return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
