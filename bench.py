@@ -112,7 +112,7 @@ def attention_sweep(ctx, contexts=(128, 1024, 4096, 32768), heads=14, kv_heads=2
     rng = np.random.default_rng(3)
     for n_ctx in contexts:
         cap = n_ctx
-        vstride = (cap + 7) // 8 * 8
+        vstride = H.value_cache_bytes(cap, kv_heads) // (kv_heads * 64 * 2)
         k_elems, v_elems = kv_heads * cap * 64, kv_heads * 64 * vstride
         per = k_elems + v_elems
         copies = int(np.ceil((512 << 20) / (2 * per)))
@@ -209,6 +209,22 @@ def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
     return cpu, f"{match}/{steps}"
 
 
+def copy_calibration(mib, reps=5):
+    """qh_copy of `mib` MiB, `reps` times: per dispatch it reads and writes exactly mib MiB, the
+    scale for the FETCH_SIZE / WRITE_SIZE counters."""
+    ctx = H.GpuContext.create(0)
+    n = mib << 20
+    src, dst = ctx.empty(n, np.uint8), ctx.empty(n, np.uint8)
+    ctx.copy(src, 0, dst, 0, n)
+    ctx.done()
+    for _ in range(reps):
+        ctx.copy(src, 0, dst, 0, n)
+    ctx.done()
+    print(json.dumps({"copy_bytes": n, "launches": reps + 1, "kernel": "k_copy16"}), flush=True)
+    src.free(), dst.free()
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,6 +237,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--isolated", choices=["all", "none"], default="all",
                     help="the isolated config-2 matvec, config-3 attention and config-5 prefill lines")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run qh_copy over this many MiB, 5 times: the known-size kernel that the "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE passes are calibrated against")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
                     help="decode by hipGraph replay (default) or direct launches of the same "
                          "kernels (for profilers that do not follow graph launches)")
@@ -231,6 +250,10 @@ def main():
               "0.5B model is not sharded (see DESIGN.md for how it would be). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_mib:
+        copy_calibration(args.copy_mib)
+        return
 
     cfg = H.QWEN25_05B
     ctx = H.GpuContext.create(0)

@@ -80,6 +80,9 @@ int qh_free(qh_ctx* ctx, void* d_ptr);
 int qh_upload(qh_ctx* ctx, void* d_dst, const void* h_src, size_t bytes);
 int qh_download(qh_ctx* ctx, void* h_dst, const void* d_src, size_t bytes);
 int qh_memset(qh_ctx* ctx, void* d_dst, int value, size_t bytes);
+/* GpuContext.copy (device.js:168-175): bytes from d_src to d_dst (non-overlapping), a
+ * copy kernel on the context stream (so it can sit inside a captured graph). */
+int qh_copy(qh_ctx* ctx, void* d_dst, const void* d_src, size_t bytes);
 
 /* Device events on the context stream (GpuContext.timed, device.js:301-338). */
 typedef struct qh_event qh_event;
@@ -139,7 +142,7 @@ int qh_rope_tables(int32_t head_dim, double theta, int32_t positions, float* h_c
 /* The KV append (model.js:336-338): k, v f32 [seq, kv_heads*head_dim] written as f16 at
  * positions past .. past+seq-1. The key cache is position-major per head
  * [kv_heads, capacity, head_dim]; the value cache is dimension-major per head
- * [kv_heads, head_dim, vstride] with vstride = capacity rounded up to a multiple of 8
+ * [kv_heads, head_dim, vstride] with vstride = capacity rounded up to a multiple of 64
  * (qh_value_cache_bytes gives its size), the layout the attention kernels stream. */
 int qh_kv_append(qh_ctx* ctx, const float* d_k, const float* d_v, uint16_t* d_key_cache,
                  uint16_t* d_value_cache, int32_t capacity, int32_t kv_heads, int32_t head_dim,

@@ -5,7 +5,7 @@
 //
 // Cache layout, per kv head: keys position-major [capacity][64] (a position's
 // key is one 128-byte row, read whole by the lane that scores it) and values
-// dimension-major [64][vstride] with vstride = capacity rounded up to 8 (one
+// dimension-major [64][vstride] with vstride = capacity rounded up to 64 (one
 // dimension's values over positions are contiguous, so the lane that owns
 // output dimension d reads 8 positions in one 16-byte load).
 //
@@ -60,7 +60,7 @@ constexpr int kVChunk = 512;
 constexpr int kVRow = kVChunk + 8;   // f16 elements per staged row
 
 // buf[d][0..n8) = values of dimension d at positions p0 .. p0+n8-1, n8 = n rounded
-// up to 8 (the tail group stays inside the row: vstride is a multiple of 8 and
+// up to 8 (the tail group stays inside the row: vstride is a multiple of 64 and
 // p0 + n <= capacity). Thread t of nt loads NS 16-byte groups before storing any.
 template <int NS>
 __device__ __forceinline__ void stage_values(const uint16_t* __restrict__ vbase, int vstride, int p0,
@@ -428,7 +428,7 @@ __device__ __forceinline__ float team_max(float v) {
 // Loads chunk `c`: key row p0+lane and, for lane d, values of dimension d at
 // positions p0 .. p0+63 as eight 16-byte groups. Every load is unconditional and
 // in bounds -- rows past `lim` (the cache capacity) read row lim-1, groups past
-// it the group holding lim-1 (vstride >= lim rounded up to 8) -- so no load waits
+// it the group holding lim-1 (vstride >= lim rounded up to 64) -- so no load waits
 // on a branch; the caller masks what lies past the context.
 __device__ __forceinline__ void slot_load(const uint16_t* kb, const uint16_t* vrow, int c, int lim,
                                           int lane, v4u (&kr)[8], v4u (&vr)[8]) {
@@ -493,13 +493,33 @@ __device__ __forceinline__ void slot_chunk(const v4f (&q4)[kHeadDim / 4], const 
 // One wave per block: a slot's loads (the query, 64 key rows, 64 value runs) are
 // all issued up front, and with one wave per CU they are not queued behind three
 // other waves' in the CU's load pipeline. grid (heads * MAXS, seq, list entries).
+//
+// Block order is XCD-aware: workgroups are dealt to the 8 XCDs round-robin (block b
+// to XCD b % 8), and the query heads of a GQA group read the same key/value chunk,
+// so the blocks of one (kv head, slot) -- one per query head of the group -- take
+// indices congruent mod 8 and share that XCD's L2 instead of fetching the chunk
+// once per XCD. Any other dealing only costs traffic: the map is a bijection.
+template <int MAXS>
+__device__ __forceinline__ void slot_of_block(int b, int heads, int kv_heads, int& h, int& sl) {
+  const int pairs = kv_heads * MAXS, group = heads / kv_heads;
+  if (pairs % 8 == 0) {
+    const int x = b & 7, j = b >> 3;
+    const int p = (j / group) * 8 + x;  // (kv head, slot) pair, XCD x
+    h = (p / MAXS) * group + j % group;
+    sl = p % MAXS;
+  } else {
+    h = b / MAXS;
+    sl = b % MAXS;
+  }
+}
+
 template <int MAXS>
 static __global__ __launch_bounds__(kWave) void k_attn_slots(SlotArgs a) {
   __shared__ __attribute__((aligned(16))) float eb[kChunk];
   const int lane = threadIdx.x;
-  const int item = blockIdx.x;
   const int t = blockIdx.y;
-  const int h = item / MAXS, sl = item % MAXS;
+  int h, sl;
+  slot_of_block<MAXS>(blockIdx.x, a.heads, a.kv_heads, h, sl);
   if (h >= a.heads) return;
   const int g = h / (a.heads / a.kv_heads);
   const size_t z = blockIdx.z;

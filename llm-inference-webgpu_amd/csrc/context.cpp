@@ -190,6 +190,15 @@ int qh_memset(qh_ctx* ctx, void* d_dst, int value, size_t bytes) {
   return QH_OK;
 }
 
+int qh_copy(qh_ctx* ctx, void* d_dst, const void* d_src, size_t bytes) {
+  QH_CHECK(ctx && ((d_dst && d_src) || !bytes), QH_ERR_INVALID, "copy needs buffers");
+  const uintptr_t lo = (uintptr_t)d_dst, hi = (uintptr_t)d_src;
+  QH_CHECK(lo + bytes <= hi || hi + bytes <= lo, QH_ERR_INVALID, "copy ranges overlap");
+  if (!bytes) return QH_OK;
+  QH_HIP(qh::launch_copy(ctx->stream, d_dst, d_src, bytes));
+  return QH_OK;
+}
+
 int qh_event_create(qh_ctx* ctx, qh_event** out) {
   QH_CHECK(ctx && out, QH_ERR_INVALID, "event_create needs a context");
   qh_event* e = new qh_event();

@@ -35,7 +35,7 @@ struct ModelDev {
 
 struct CacheDev {
   int capacity;
-  int vstride;         // value row length: capacity rounded up to 8
+  int vstride;         // value row length: capacity rounded up to 64
   // Per layer: keys [kv_heads][capacity][64], then values [kv_heads][64][vstride], f16.
   uint16_t* kv;
   size_t layer_elems;  // f16 elements per layer (keys + values)

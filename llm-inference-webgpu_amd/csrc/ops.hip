@@ -3,6 +3,8 @@
 // attention (exact order and split-K), swiglu, residual add and argmax. Each
 // replaces one WGSL kernel of src/gpu/kernels.js; the decode step
 // (decode.hip) is built from the same device building blocks.
+#include <algorithm>
+
 #include "attention.h"
 #include "device_common.h"
 
@@ -565,6 +567,31 @@ hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n) {
 }
 hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n) {
   hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, s, x, delta, n);
+  return hipGetLastError();
+}
+
+// -------------------------------------------------------------------- copy --
+// A grid-stride copy: 16-byte vectors (both pointers 16-byte aligned) or bytes.
+__global__ void k_copy16(v4u* __restrict__ dst, const v4u* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+__global__ void k_copy8(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes) {
+  const bool vec = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0) && bytes % 16 == 0;
+  const size_t n = vec ? bytes / 16 : bytes;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + kBlock - 1) / kBlock, 8192);
+  if (vec) {
+    hipLaunchKernelGGL(k_copy16, dim3(blocks), dim3(kBlock), 0, s, static_cast<v4u*>(dst),
+                       static_cast<const v4u*>(src), n);
+  } else {
+    hipLaunchKernelGGL(k_copy8, dim3(blocks), dim3(kBlock), 0, s, static_cast<uint8_t*>(dst),
+                       static_cast<const uint8_t*>(src), n);
+  }
   return hipGetLastError();
 }
 

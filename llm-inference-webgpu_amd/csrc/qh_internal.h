@@ -47,8 +47,9 @@ int make_dmat(const qh_weight* w, DMat* out);
 int weights_per_chunk(int format);
 
 // Row length of the dimension-major value cache [kv_heads][head_dim][vstride]: capacity
-// rounded up to 8, so every row starts 16-byte aligned.
-__host__ __device__ inline int value_stride(int capacity) { return (capacity + 7) & ~7; }
+// rounded up to 64 positions (128 bytes), so every row, and every 64-position chunk of
+// a row that split-K attention reads, starts on a cache line.
+__host__ __device__ inline int value_stride(int capacity) { return (capacity + 63) & ~63; }
 // Exact attention scores 256 positions per block ("span").
 constexpr int kSpan = 256;
 __host__ __device__ inline int attn_spans(int ctx) { return (ctx + kSpan - 1) / kSpan; }
@@ -130,6 +131,9 @@ size_t attention_list_partials_floats(int count, int heads, int ctx);
 void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
 hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n);
+// dst[0, bytes) = src[0, bytes): 16-byte vector copies when both are 16-byte aligned,
+// bytes otherwise.
+hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
 // Argmax into d_out[0]; `partials` holds argmax_partials_bytes(n) bytes; *counter is zero
 // before the launch and left zero after it.
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, void* partials,

@@ -129,6 +129,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_close": [vp], "qh_describe": [vp, ctypes.c_char_p, sz], "qh_sync": [vp],
         "qh_alloc": [vp, sz, vp], "qh_free": [vp, vp], "qh_upload": [vp, vp, vp, sz],
         "qh_download": [vp, vp, vp, sz], "qh_memset": [vp, vp, ctypes.c_int, sz],
+        "qh_copy": [vp, vp, vp, sz],
         "qh_event_create": [vp, vp], "qh_event_record": [vp, vp],
         "qh_event_elapsed_ms": [vp, vp, vp], "qh_event_destroy": [vp],
         "qh_matvec": [vp, vp, vp, vp, vp, i32], "qh_matvec_xh": [vp, vp, vp, vp],
@@ -171,7 +172,7 @@ def _declare(lib: ctypes.CDLL) -> None:
 
 
 def value_cache_bytes(capacity: int, kv_heads: int, head_dim: int = 64) -> int:
-    """Bytes of a dimension-major value cache (rows of capacity rounded up to 8)."""
+    """Bytes of a dimension-major value cache (rows of capacity rounded up to 64)."""
     return int(load_library().qh_value_cache_bytes(capacity, kv_heads, head_dim))
 
 
@@ -379,6 +380,10 @@ class GpuContext:
 
     def download_into(self, out: np.ndarray, buf: DeviceBuffer, offset: int = 0) -> None:
         _check(self.lib.qh_download(self.handle, _ptr(out), buf.ptr + offset, out.nbytes))
+
+    def copy(self, src, src_offset: int, dst, dst_offset: int, nbytes: int) -> None:
+        """GpuContext.copy (device.js:168-175): a device copy kernel on the context stream."""
+        _check(self.lib.qh_copy(self.handle, dst.ptr + dst_offset, src.ptr + src_offset, nbytes))
 
     def done(self) -> None:
         _check(self.lib.qh_sync(self.handle))

@@ -275,12 +275,12 @@ def kv_setup(ctx, hip, capacity, ctx_len, seed, kv_heads=2):
 @pytest.mark.parametrize("capacity", [8, 13])
 def test_kv_append_rounds_to_f16_exactly(ctx, hip, capacity):
     # keys position-major [kv_heads, capacity, 64]; values dimension-major
-    # [kv_heads, 64, vstride] with vstride = capacity rounded up to 8
+    # [kv_heads, 64, vstride] with vstride = capacity rounded up to 64 (128-byte rows)
     kc, vc, kr, vr = kv_setup(ctx, hip, capacity, 5, 0)
     got = kc.read(np.uint16, 2 * capacity * 64).reshape(2, capacity, 64)[:, :5]
     want = O.f32_to_f16(kr).reshape(5, 2, 64).transpose(1, 0, 2)
     np.testing.assert_array_equal(got, want)
-    vstride = (capacity + 7) // 8 * 8
+    vstride = (capacity + 63) // 64 * 64
     assert hip.value_cache_bytes(capacity, 2) == 2 * 64 * vstride * 2
     got_v = vc.read(np.uint16, 2 * 64 * vstride).reshape(2, 64, vstride)[:, :, :5]
     want_v = O.f32_to_f16(vr).reshape(5, 2, 64).transpose(1, 2, 0)
@@ -319,7 +319,7 @@ def test_attention_list_matches_single_calls(ctx, hip, ctx_len):
     """The list form (config 3's rotation in one launch) gives each cache the single-cache
     split-K result within the kernel tolerance of the oracle."""
     heads, kv_heads, count, cap = 14, 2, 5, ctx_len + 3
-    vstride = (cap + 7) // 8 * 8
+    vstride = hip.value_cache_bytes(cap, kv_heads) // (kv_heads * 64 * 2)
     rng = np.random.default_rng(ctx_len)
     kel, vel = kv_heads * cap * 64, kv_heads * 64 * vstride
     keys = O.f32_to_f16(rng.standard_normal(count * kel).astype(np.float32))
@@ -415,6 +415,29 @@ def test_add_is_exact(ctx, hip):
     ctx.add(dx, dd, 896)
     np.testing.assert_array_equal(dx.read(count=896), x + d)
     free(dx, dd)
+
+
+@pytest.mark.parametrize("src_off,dst_off,n", [(0, 0, 1 << 20), (16, 48, 4096), (3, 5, 1001), (0, 0, 0),
+                                               (0, 0, 7)])
+def test_copy_moves_exactly_the_range(ctx, hip, src_off, dst_off, n):
+    """GpuContext.copy (device.js:168-175): bytes [src_off, +n) land at dst_off, nothing
+    around them changes (16-byte vector path when aligned, byte path otherwise)."""
+    rng = np.random.default_rng(9)
+    src = rng.integers(0, 256, size=n + 64, dtype=np.uint8)
+    dst = rng.integers(0, 256, size=n + 64, dtype=np.uint8)
+    ds, dd = ctx.upload(src), ctx.upload(dst)
+    ctx.copy(ds, src_off, dd, dst_off, n)
+    want = dst.copy()
+    want[dst_off:dst_off + n] = src[src_off:src_off + n]
+    np.testing.assert_array_equal(dd.read(np.uint8, n + 64), want)
+    free(ds, dd)
+
+
+def test_copy_rejects_overlap(ctx, hip):
+    d = ctx.upload(np.zeros(256, np.uint8))
+    with pytest.raises(hip.QwenHipError, match="overlap"):
+        ctx.copy(d, 0, d, 16, 64)
+    free(d)
 
 
 @pytest.mark.parametrize("case", ["random", "ties", "nan0", "nan_mid", "inf", "neg", "tiny", "all_nan"])
