@@ -25,6 +25,7 @@ Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16]
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -62,6 +63,23 @@ def role_bytes(cfg, ctx_len, group=128):
         "down": int4(d, ffn) + ffn * f + 2 * d * f,
         "head": V * d + V * f + 2 * d * f + V * f,
     }
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_int4_ctx1024_hbm_traffic.md")
+
+
+def measured_traffic(role, context):
+    """HBM bytes per launch of a decode role from the committed rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes (each scaled by a 64 MiB copy kernel's reading), taken at context 1024;
+    None for another context or without the profile."""
+    if context != 1024:
+        return None
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"```json\n(.*?)\n```", f.read(), re.S)
+        return json.loads(m.group(1))["bytes_per_launch"].get(role) if m else None
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def isolated_matvec(ctx, shapes, reps=5):
@@ -318,7 +336,8 @@ def main():
     achieved = kbytes / (kernel_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": None, "bytes_per_launch": kbytes, "us_per_launch": round(kernel_us, 3)}
+                "traffic": measured_traffic(dominant, args.context), "bytes_per_launch": kbytes,
+                "us_per_launch": round(kernel_us, 3)}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
     iso = attn = prefill = None

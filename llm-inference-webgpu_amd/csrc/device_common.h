@@ -3,12 +3,13 @@
 // row-team matvec core (streamed and register-prefetched forms), and
 // block-level staging helpers.
 //
-// Arithmetic follows the reference CPU path step for step (src/core/ops.js:
-// f32 storage, f64 accumulation). A weight is first dequantized to the f32 the
-// reference's loader would hold -- f32(q*scale), f32((level-zero)*scale), or the
-// f16 value -- and then multiplied into an f64 accumulator, so the only
-// difference from the CPU is the order of an f64 sum (~1e-16 relative), which
-// almost never survives the final rounding to f32.
+// Two arithmetics. The exact one follows the reference CPU path step for step
+// (src/core/ops.js: f32 storage, f64 accumulation): a weight is first
+// dequantized to the f32 the reference's loader would hold -- f32(q*scale),
+// f32((level-zero)*scale), or the f16 value -- and then multiplied into an f64
+// accumulator, so the only difference from the CPU is the order of an f64 sum
+// (~1e-16 relative), which almost never survives the final rounding to f32. The
+// fast one (the f32 core below) sums in f32 as the reference's WebGPU kernels do.
 //
 // The matvec core is shared by decode and the batched prefill path, so each
 // output row is summed in one order whatever the number of positions: lane-
