@@ -168,6 +168,14 @@ int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cac
                         int32_t seq, int32_t past, int32_t heads, int32_t kv_heads,
                         int32_t head_dim);
 
+/* As qh_attention on the matrix cores (the prefill's attention when the model's matmul mode is
+ * QH_MATMUL_MFMA): a flash attention whose q.k and p.v products run on f16 MFMA with q and p
+ * split into two f16 terms each, f32 accumulation, online softmax. Exact only to f32 rounding
+ * (~1e-6 of the output). */
+int qh_attention_mfma(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                      const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                      int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim);
+
 /* qh_attention_splitk for one query (position `past`) against `count` caches of the same shape
  * in one launch: key cache i at d_key_cache + i*key_stride, value cache i at d_value_cache +
  * i*value_stride (f16 elements); out [count][heads*head_dim]. How a working set of caches larger

@@ -584,6 +584,172 @@ static hipError_t launch_attn_slots(hipStream_t s, const SlotArgs& a, int seq, i
   return hipGetLastError();
 }
 
+// ------------------------------------------------ prefill on the matrix cores --
+// Causal GQA attention of `seq` queries (positions past .. past+seq-1) as a flash
+// attention on v_mfma_f32_16x16x32_f16: one wave per (query head, 16 queries), keys
+// in steps of 32 with an online softmax per query.
+//
+// Transposed products keep every operand where it is loaded: S^T = K Q^T (A = 16 key
+// rows of the position-major cache, 16 bytes per lane; B = the wave's queries), then
+// O^T += V^T P^T (A = 16 dimension rows of the dimension-major value cache; B = P^T).
+// In the D layout lane l holds keys 4*(l/16)+r of query l%16, which is exactly what
+// the B operand of the second product needs for query l%16 once the contraction
+// index is ordered (keys 4g..4g+3 of the first 16-key tile, then the same of the
+// second) -- the value operand is read in that order -- so P never leaves its
+// registers, and the softmax state of a query lives in the four lanes that share it.
+//
+// Precision: q (scaled by the exact 1/8) and p are each split into two f16 terms
+// whose sum is the f32 value to 2^-22, the f16 K/V are exact, products accumulate
+// in f32: the output agrees with the split-K f32 path to ~1e-6 (not to the bit).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kFlashQ = 16;  // queries per wave
+constexpr int kFlashK = 32;  // keys per step
+
+struct FlashArgs {
+  const float* q;        // [seq][heads*64], rotated
+  const uint16_t* kc;    // [kv_heads][capacity][64] f16
+  const uint16_t* vt;    // [kv_heads][64][vstride] f16
+  float* out;            // [seq][heads*64]
+  int past, seq, capacity, vstride, heads, kv_heads;
+};
+
+// x as hi + lo, two f16 values: hi = f16(x), lo = f16(x - hi) (x - hi is exact in f32).
+__device__ __forceinline__ _Float16 f16_hi_part(float x) { return (_Float16)x; }
+__device__ __forceinline__ _Float16 f16_lo_part(float x) { return (_Float16)(x - (float)(_Float16)x); }
+
+static __global__ __launch_bounds__(kWave) void k_flash_prefill(FlashArgs a) {
+  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y;
+  const int kvh = h / (a.heads / a.kv_heads);
+  const int t0 = blockIdx.x * kFlashQ;
+  const int tn = min(t0 + n, a.seq - 1);  // this lane's query; past the end, a copy of the last
+  const int qpos = a.past + tn;
+  const int kmax = a.past + min(t0 + kFlashQ - 1, a.seq - 1);  // the tile's last key
+
+  f16x8 qh[2], ql[2];  // B of S^T = K Q^T: query n, dims 32ks + 8g .. +7, times 1/8
+  const float* qr = a.q + ((size_t)tn * a.heads + h) * kHeadDim;
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    const v4f x0 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g);
+    const v4f x1 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float a0 = x0[e] * 0.125f, a1 = x1[e] * 0.125f;
+      qh[ks][e] = f16_hi_part(a0);
+      ql[ks][e] = f16_lo_part(a0);
+      qh[ks][4 + e] = f16_hi_part(a1);
+      ql[ks][4 + e] = f16_lo_part(a1);
+    }
+  }
+  const uint16_t* kb = a.kc + (size_t)kvh * a.capacity * kHeadDim;
+  const uint16_t* vb = a.vt + (size_t)kvh * kHeadDim * a.vstride;
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[4];  // O^T: dims 16dt + 4g + r of query n
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  for (int p0 = 0; p0 <= kmax; p0 += kFlashK) {
+    // Loads (in bounds: key rows clamped to the cache, value groups to the row).
+    f16x8 kf[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const uint16_t* kr = kb + (size_t)min(p0 + 16 * j + n, a.capacity - 1) * kHeadDim;
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) kf[j][ks] = *reinterpret_cast<const f16x8*>(kr + 32 * ks + 8 * g);
+    }
+    uint32_t vv[4][4];  // dim 16dt + n: keys p0+4g .. +3 (vv[dt][0..1]), p0+16+4g .. +3 (vv[dt][2..3])
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      const uint16_t* vr = vb + (size_t)(16 * dt + n) * a.vstride;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const uint2 w = *reinterpret_cast<const uint2*>(vr + min(p0 + 16 * j + 4 * g, a.vstride - 4));
+        vv[dt][2 * j] = w.x;
+        vv[dt][2 * j + 1] = w.y;
+      }
+    }
+    // S^T tiles: s[j][r] = score of key p0 + 16j + 4g + r for query n.
+    f32x4 s[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][ks], qh[ks], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][ks], ql[ks], acc, 0, 0, 0);
+      }
+      s[j] = acc;
+    }
+    // Online softmax for query n (causal mask by select: masked keys may hold any bits).
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        s[j][r] = p0 + 16 * j + 4 * g + r <= qpos ? s[j][r] : -INFINITY;
+        tmax = fmaxf(tmax, s[j][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);  // finite: key 0 is in every query's first step
+    const float alpha = expf(m - mn);  // 0 on the first step
+    float pv[2][4], psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        pv[j][r] = s[j][r] == -INFINITY ? 0.f : expf(s[j][r] - mn);
+        psum += pv[j][r];
+      }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l = fmaf(l, alpha, psum);
+    m = mn;
+    f16x8 ph, pl;  // B of O^T += V^T P^T, contraction order: keys 4g..4g+3, then 16+4g..16+4g+3
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      ph[r] = f16_hi_part(pv[0][r]);
+      pl[r] = f16_lo_part(pv[0][r]);
+      ph[4 + r] = f16_hi_part(pv[1][r]);
+      pl[4 + r] = f16_lo_part(pv[1][r]);
+    }
+    if (p0 + kFlashK - 1 > kmax) {
+      // Keys past the tile's last were never written for it: their values must be zeros.
+#pragma unroll
+      for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          const int k0 = p0 + 16 * (w >> 1) + 4 * g + 2 * (w & 1);  // keys of vv[dt][w]: k0, k0+1
+          const uint32_t keep = (k0 <= kmax ? 0x0000ffffu : 0u) | (k0 + 1 <= kmax ? 0xffff0000u : 0u);
+          vv[dt][w] &= keep;
+        }
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      f32x4 c = o[dt];
+#pragma unroll
+      for (int r = 0; r < 4; r++) c[r] *= alpha;
+      const f16x8 va = __builtin_bit_cast(f16x8, (v4u){vv[dt][0], vv[dt][1], vv[dt][2], vv[dt][3]});
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, c, 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, c, 0, 0, 0);
+    }
+  }
+  if (t0 + n < a.seq) {
+    float* dst = a.out + ((size_t)(t0 + n) * a.heads + h) * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+      const v4f r = {o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
+      *reinterpret_cast<v4f*>(dst + 16 * dt + 4 * g) = r;
+    }
+  }
+}
+
+static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a) {
+  hipLaunchKernelGGL(k_flash_prefill, dim3((a.seq + kFlashQ - 1) / kFlashQ, a.heads), dim3(kWave), 0, s, a);
+  return hipGetLastError();
+}
+
 // out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t) (and list
 // entry z, whose partials are list_part floats and output seq*heads*64 floats further on).
 [[maybe_unused]] static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __restrict__ part,

@@ -375,6 +375,17 @@ int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
   return QH_OK;
 }
 
+int qh_attention_mfma(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
+                      const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
+                      int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {
+  int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
+                           kv_heads, head_dim);
+  if (rc) return rc;
+  QH_HIP(qh::launch_attention_mfma(ctx->stream, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past,
+                                   heads, kv_heads));
+  return QH_OK;
+}
+
 int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
                         const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
                         int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim) {

@@ -5,8 +5,9 @@
 // (QH_MATMUL_MFMA, prefill.hip).
 //
 // Per layer, over all positions: rmsnorm -> q|k|v matmul + bias -> rope (f64) with
-// the f16 K/V append -> attention (the decode step's algorithm for the model's
-// numerics, one query per position) -> o matmul, residual add -> rmsnorm -> gate|up
+// the f16 K/V append -> attention (QH_MATMUL_BATCHED: the decode step's algorithm
+// for the model's numerics, one query per position; QH_MATMUL_MFMA: flash attention
+// on the matrix cores) -> o matmul, residual add -> rmsnorm -> gate|up
 // matmul -> swiglu -> down matmul, residual add. The last position's row then goes
 // through the decode step's own output head and pick.
 //
@@ -155,7 +156,21 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
     hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, p.Q, kc, vt, m.rope_cos,
                        m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (m.numerics == QH_NUMERICS_FAST) {
+    if (mode == QH_MATMUL_MFMA) {
+      // the matrix-core prefill: flash attention on MFMA (held to the MFMA tolerance)
+      FlashArgs a{};
+      a.q = p.Q;
+      a.kc = kc;
+      a.vt = vt;
+      a.out = p.ATT;
+      a.past = past;
+      a.seq = seq;
+      a.capacity = c.capacity;
+      a.vstride = c.vstride;
+      a.heads = m.heads;
+      a.kv_heads = m.kv_heads;
+      if ((e = launch_flash_prefill(s, a)) != hipSuccess) return e;
+    } else if (m.numerics == QH_NUMERICS_FAST) {
       SlotArgs a{};
       a.q = p.Q;
       a.kc = kc;

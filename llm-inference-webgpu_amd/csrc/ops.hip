@@ -503,6 +503,22 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
   return hipGetLastError();
 }
 
+hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
+                                 int capacity, float* out, int seq, int past, int heads, int kv_heads) {
+  FlashArgs a{};
+  a.q = q;
+  a.kc = kc;
+  a.vt = vt;
+  a.out = out;
+  a.past = past;
+  a.seq = seq;
+  a.capacity = capacity;
+  a.vstride = value_stride(capacity);
+  a.heads = heads;
+  a.kv_heads = kv_heads;
+  return launch_flash_prefill(s, a);
+}
+
 // Slots per head of the list operator: enough for one chunk per slot up to 64 slots.
 static int list_slots(int ctx) {
   const int n = attn_chunks(ctx);

@@ -120,6 +120,9 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
                                    const uint16_t* vt, int capacity, float* out, int seq, int past,
                                    int heads, int kv_heads, float* partials);
 size_t attention_partials_floats(int seq, int heads);
+// Flash attention on the matrix cores (f16 MFMA, q and p split in two f16 terms).
+hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
+                                 int capacity, float* out, int seq, int past, int heads, int kv_heads);
 // One query (position past) against `count` same-shape caches: key cache i at kc + i*list_k,
 // value cache i at vt + i*list_v (elements); out [count][heads*64]; `partials` holds
 // attention_list_partials_floats(count, heads, past + 1) floats.

@@ -140,6 +140,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_kv_append": [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32],
         "qh_attention": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_attention_splitk": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
+        "qh_attention_mfma": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
         "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32],
         "qh_attention_splitk_list": [vp, vp, vp, vp, sz, sz, i32, i32, vp, i32, i32, i32, i32],
@@ -437,8 +438,11 @@ class GpuContext:
                                      head_dim, past, seq))
 
     def attention(self, q, kc, vc, capacity, out, seq, past, heads, kv_heads, head_dim=64,
-                  splitk=False) -> None:
-        fn = self.lib.qh_attention_splitk if splitk else self.lib.qh_attention
+                  splitk=False, kind=None) -> None:
+        """kind: "exact" (qh_attention), "splitk" or "mfma"; `splitk` picks between the first two."""
+        kind = kind or ("splitk" if splitk else "exact")
+        fn = {"exact": self.lib.qh_attention, "splitk": self.lib.qh_attention_splitk,
+              "mfma": self.lib.qh_attention_mfma}[kind]
         _check(fn(self.handle, q.ptr, kc.ptr, vc.ptr, capacity, out.ptr, seq, past, heads, kv_heads,
                   head_dim))
 
