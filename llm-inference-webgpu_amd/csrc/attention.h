@@ -598,12 +598,23 @@ static hipError_t launch_attn_slots(hipStream_t s, const SlotArgs& a, int seq, i
 // second) -- the value operand is read in that order -- so P never leaves its
 // registers, and the softmax state of a query lives in the four lanes that share it.
 //
-// Precision: q (scaled by the exact 1/8) and p are each split into two f16 terms
+// Precision: q (scaled by 1/8 log2 e) and p are each split into two f16 terms
 // whose sum is the f32 value to 2^-22, the f16 K/V are exact, products accumulate
 // in f32: the output agrees with the split-K f32 path to ~1e-6 (not to the bit).
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kFlashQ = 16;  // queries per wave
+// q is scaled by 1/sqrt(64) * log2(e) once, so scores are in base-2 units and the softmax
+// weights are 2^(s - max) -- the same softmax.
+constexpr float kScoreLog2 = 0.125f * 1.44269504088896340736f;
+
+// 2^x for finite x <= 0 as v_exp_f32 of the fraction in [-0.5, 0.5] scaled by 2^rint(x):
+// the hardware exp2 is taken only where it is accurate (on the whole range its error
+// reached ~1e-5 of the attention output at short contexts).
+__device__ __forceinline__ float exp2_reduced(float x) {
+  const float n = __builtin_rintf(x);
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f(x - n), (int)n);
+}
 constexpr int kFlashK = 32;  // keys per step
 
 struct FlashArgs {
@@ -615,6 +626,13 @@ struct FlashArgs {
 };
 
 // x as hi + lo, two f16 values: hi = f16(x), lo = f16(x - hi) (x - hi is exact in f32).
+// x must be one materialized f32 value (f32_pinned): left as a product, the compiler
+// fuses it into both conversions (v_fma_mix*), rounding hi and lo from different values
+// whose halves need not sum to either.
+__device__ __forceinline__ float f32_pinned(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 __device__ __forceinline__ _Float16 f16_hi_part(float x) { return (_Float16)x; }
 __device__ __forceinline__ _Float16 f16_lo_part(float x) { return (_Float16)(x - (float)(_Float16)x); }
 
@@ -635,7 +653,7 @@ static __global__ __launch_bounds__(kWave) void k_flash_prefill(FlashArgs a) {
     const v4f x1 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g + 4);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const float a0 = x0[e] * 0.125f, a1 = x1[e] * 0.125f;
+      const float a0 = f32_pinned(x0[e] * kScoreLog2), a1 = f32_pinned(x1[e] * kScoreLog2);
       qh[ks][e] = f16_hi_part(a0);
       ql[ks][e] = f16_lo_part(a0);
       qh[ks][4 + e] = f16_hi_part(a1);
@@ -693,13 +711,13 @@ static __global__ __launch_bounds__(kWave) void k_flash_prefill(FlashArgs a) {
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
     const float mn = fmaxf(m, tmax);  // finite: key 0 is in every query's first step
-    const float alpha = expf(m - mn);  // 0 on the first step
+    const float alpha = m == -INFINITY ? 0.f : exp2_reduced(m - mn);  // 0 on the first step
     float pv[2][4], psum = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        pv[j][r] = s[j][r] == -INFINITY ? 0.f : expf(s[j][r] - mn);
+        pv[j][r] = s[j][r] == -INFINITY ? 0.f : exp2_reduced(s[j][r] - mn);
         psum += pv[j][r];
       }
     psum += __shfl_xor(psum, 16);
@@ -750,9 +768,192 @@ static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a)
   return hipGetLastError();
 }
 
+// ------------------------------------- one query, GQA group on the matrix cores --
+// The split-K slots of k_attn_slots for a single query, with a whole GQA group per
+// wave: the group's query heads are the columns of the MFMA products of the flash
+// kernel above (heads/kv_heads of the 16 used, the rest repeat head 0 and are
+// dropped), so each key/value position is read once for the group instead of once
+// per query head. A slot's chunks are walked in steps of 32 keys -- S^T for 2 tiles
+// of 16 keys (8 MFMAs), the online softmax per head column, O^T += V^T P^T (8
+// MFMAs) -- with the next step's loads issued before each step's arithmetic (two
+// 32-key buffers). Writes (m, l, o) slot partials in the layout of k_attn_slots, with
+// the maxima in base-2 units (merged by k_attn_combine<true>). q and p are split into
+// two f16 terms as in the flash kernel (~1e-6 of the output).
+struct GqaStep {
+  f16x8 k[2][2];     // keys 16j + n, dims 32ks + 8g .. +7
+  uint32_t v[4][4];  // dimension 16dt + n: keys 4g .. +3 (v[dt][0..1]), 16+4g .. +3 (v[dt][2..3])
+};
+
+// Step i of slot sl: 32 keys starting at p0 (chunk sl + (i/2)*MAXS, half i%2).
+template <int MAXS>
+__device__ __forceinline__ int gqa_p0(int sl, int i) {
+  return (sl + (i >> 1) * MAXS) * kChunk + (i & 1) * 32;
+}
+
+__device__ __forceinline__ void gqa_load(const uint16_t* kb, const uint16_t* vb, int p0, int capacity, int vstride,
+                                         int n, int g, GqaStep& d) {
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint16_t* kr = kb + (size_t)min(p0 + 16 * j + n, capacity - 1) * kHeadDim;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) d.k[j][ks] = *reinterpret_cast<const f16x8*>(kr + 32 * ks + 8 * g);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) {
+    const uint16_t* vr = vb + (size_t)(16 * dt + n) * vstride;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+      const uint2 w = *reinterpret_cast<const uint2*>(vr + min(p0 + 16 * hf + 4 * g, vstride - 4));
+      d.v[dt][2 * hf] = w.x;
+      d.v[dt][2 * hf + 1] = w.y;
+    }
+  }
+}
+
+__device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)[2], GqaStep& d, int p0, int ctx,
+                                         int g, float& m, float& l, f32x4 (&o)[4]) {
+  f32x4 s[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d.k[j][ks], qh[ks], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(d.k[j][ks], ql[ks], acc, 0, 0, 0);
+    }
+    s[j] = acc;
+  }
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      s[j][r] = p0 + 16 * j + 4 * g + r < ctx ? s[j][r] : -INFINITY;
+      tmax = fmaxf(tmax, s[j][r]);
+    }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+  const float mn = fmaxf(m, tmax);  // finite: every step a slot sums holds position p0 < ctx
+  const float alpha = m == -INFINITY ? 0.f : exp2_reduced(m - mn);
+  float pv[2][4], psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      pv[j][r] = s[j][r] == -INFINITY ? 0.f : exp2_reduced(s[j][r] - mn);
+      psum += pv[j][r];
+    }
+  psum += __shfl_xor(psum, 16);
+  psum += __shfl_xor(psum, 32);
+  l = fmaf(l, alpha, psum);
+  m = mn;
+  f16x8 ph, pl;  // contraction order: keys 4g .. 4g+3, then 16+4g .. 16+4g+3
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    ph[r] = f16_hi_part(pv[0][r]);
+    pl[r] = f16_lo_part(pv[0][r]);
+    ph[4 + r] = f16_hi_part(pv[1][r]);
+    pl[4 + r] = f16_lo_part(pv[1][r]);
+  }
+  if (p0 + 32 > ctx) {
+    // positions past the context may hold any bits: their values become zeros
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const int k0 = p0 + 16 * (w >> 1) + 4 * g + 2 * (w & 1);
+        d.v[dt][w] &= (k0 < ctx ? 0x0000ffffu : 0u) | (k0 + 1 < ctx ? 0xffff0000u : 0u);
+      }
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) {
+    f32x4 c = o[dt];
+#pragma unroll
+    for (int r = 0; r < 4; r++) c[r] *= alpha;
+    const f16x8 va = __builtin_bit_cast(f16x8, (v4u){d.v[dt][0], d.v[dt][1], d.v[dt][2], d.v[dt][3]});
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, c, 0, 0, 0);
+    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, c, 0, 0, 0);
+  }
+}
+
+// grid (kv_heads * MAXS, 1, list entries); SlotArgs as for k_attn_slots (one query).
+template <int MAXS>
+static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
+  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  const int group = a.heads / a.kv_heads;
+  const int kvh = blockIdx.x / MAXS, sl = blockIdx.x % MAXS;
+  const size_t z = blockIdx.z;
+  const int h = kvh * group + (n < group ? n : 0);
+  f16x8 qh[2], ql[2];
+  const float* qr = a.q + (size_t)h * kHeadDim;
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    const v4f x0 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g);
+    const v4f x1 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g + 4);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float a0 = f32_pinned(x0[e] * kScoreLog2), a1 = f32_pinned(x1[e] * kScoreLog2);
+      qh[ks][e] = f16_hi_part(a0);
+      ql[ks][e] = f16_lo_part(a0);
+      qh[ks][4 + e] = f16_hi_part(a1);
+      ql[ks][4 + e] = f16_lo_part(a1);
+    }
+  }
+  const uint16_t* kb = a.kc + z * a.list_k + (size_t)kvh * a.capacity * kHeadDim;
+  const uint16_t* vb = a.vt + z * a.list_v + (size_t)kvh * kHeadDim * a.vstride;
+  GqaStep A, B;
+  gqa_load(kb, vb, gqa_p0<MAXS>(sl, 0), a.capacity, a.vstride, n, g, A);  // in bounds whatever the position
+  const int pos = a.d_pos ? *a.d_pos : a.past;
+  if (pos >= a.capacity) return;  // the host keeps positions inside the cache
+  const int ctx = pos + 1, nch = attn_chunks(ctx);
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // Steps of this slot: two per chunk, but none that starts at or past the context.
+  int left = 0;
+  if (sl < nch) {
+    const int chunks = (nch - 1 - sl) / MAXS + 1;
+    const int last = sl + (chunks - 1) * MAXS;
+    left = 2 * chunks - (last * kChunk + 32 >= ctx ? 1 : 0);
+  }
+  int i = 0;
+  while (left > 0) {
+    if (left == 1) {
+      gqa_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+      break;
+    }
+    gqa_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, B);
+    __builtin_amdgcn_sched_barrier(0);  // the next step's loads before this step's arithmetic
+    gqa_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+    ++i;
+    if (--left == 1) {
+      gqa_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+      break;
+    }
+    gqa_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, A);
+    __builtin_amdgcn_sched_barrier(0);
+    gqa_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+    ++i;
+    --left;
+  }
+  if (n < group) {
+    float* dst = a.part + z * a.list_part + ((size_t)h * MAXS + sl) * kPartStride;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = (v4f)o[dt];
+    if (g == 0) {
+      dst[0] = m;
+      dst[1] = l;
+    }
+  }
+}
+
 // out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t) (and list
 // entry z, whose partials are list_part floats and output seq*heads*64 floats further on).
-[[maybe_unused]] static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __restrict__ part,
+// B2: the partials' maxima are in base-2 units (k_attn_gqa), so the slot weights are
+// 2^(m_s - M); else e^(m_s - M).
+template <bool B2>
+static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __restrict__ part,
                                                                float* __restrict__ out, int past,
                                                                int heads, int max_slots, size_t list_part) {
   const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
@@ -764,7 +965,8 @@ static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a)
   for (int s = 0; s < nslots; s++) M = fmaxf(M, p[(size_t)s * kPartStride]);
   float L = 0.f, A = 0.f;
   for (int s = 0; s < nslots; s++) {
-    const float w = expf(p[(size_t)s * kPartStride] - M);
+    const float ms = p[(size_t)s * kPartStride];
+    const float w = B2 ? (ms == -INFINITY ? 0.f : exp2_reduced(ms - M)) : expf(ms - M);
     L = fmaf(w, p[(size_t)s * kPartStride + 1], L);
     A = fmaf(w, p[(size_t)s * kPartStride + 4 + d], A);
   }

@@ -498,7 +498,7 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
   a.max_slots = kOpSlots;
   hipError_t e = launch_attn_slots<kOpSlots>(s, a, seq, 1);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_combine, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
+  hipLaunchKernelGGL(k_attn_combine<false>, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
                      kOpSlots, (size_t)0);
   return hipGetLastError();
 }
@@ -519,23 +519,27 @@ hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* 
   return launch_flash_prefill(s, a);
 }
 
-// Slots per head of the list operator: enough for one chunk per slot up to 64 slots.
+// Slots per head of the list operator: about four chunks per slot (a slot pipelines its
+// steps), up to 64 slots (the combine walks a head's slots in sequence).
 static int list_slots(int ctx) {
   const int n = attn_chunks(ctx);
-  return n <= 4 ? 4 : n <= 16 ? 16 : kOpSlots;
+  return n <= 16 ? 4 : n <= 64 ? 16 : kOpSlots;
 }
 
 size_t attention_list_partials_floats(int count, int heads, int ctx) {
   return (size_t)count * heads * list_slots(ctx) * kPartStride;
 }
 
+// The list runs the GQA-group MFMA form of the slots (one read of each K/V chunk per kv
+// head), then the slot combine.
 template <int MAXS>
 static hipError_t list_t(hipStream_t s, SlotArgs a, int count, float* out) {
   a.max_slots = MAXS;
   a.list_part = (size_t)a.heads * MAXS * kPartStride;
-  hipError_t e = launch_attn_slots<MAXS>(s, a, 1, count);
+  hipLaunchKernelGGL(k_attn_gqa<MAXS>, dim3(a.kv_heads * MAXS, 1, count), dim3(kWave), 0, s, a);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_combine, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
+  hipLaunchKernelGGL(k_attn_combine<true>, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
                      a.list_part);
   return hipGetLastError();
 }
