@@ -17,8 +17,9 @@ Also reported on the same JSON line:
   matvec_isolated  BASELINE config 2: int8 matvec with an f16 activation at the
                  five layer shapes, one list-driven launch over >= 512 MiB of
                  distinct matrices (larger than the 256 MB last-level cache)
-  cpu_baseline   the CPU oracle (a port of the reference's src/cpu path) timed on
-                 one host core over a bounded sample of the same workload
+  cpu_baseline   the reference's src/cpu path restated in JavaScript (oracle/cpu_model.js)
+                 timed under Node on one host core over a bounded sample of the same
+                 workload; cpu_baseline_c the C oracle on the same sample
 
 Usage: python bench.py [--gpus 1] [--steps 256] [--warmup 16]
 """
@@ -26,7 +27,9 @@ import argparse
 import json
 import os
 import re
+import subprocess
 import sys
+import tempfile
 import time
 
 import numpy as np
@@ -201,6 +204,40 @@ def prefill_bench(ctx, cfg, ckpt, seed, prompt_len=512, modes=("matvec", "batche
     return res
 
 
+def node_version():
+    try:
+        return subprocess.run(["node", "--version"], capture_output=True, text=True, check=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        return None
+
+
+def node_cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
+    """The reference CPU path in JavaScript (oracle/cpu_model.js: src/cpu/model.js restated for
+    Node 12, f32 storage, f64 sums) timed under Node on one thread: the int4-g128 layers and int8
+    head from the reference quantizer's arrays, dequantized once at load, the KV cache holding
+    the GPU run's context (the same f16 values), then `steps` greedy decode steps. Returns the
+    baseline record and the token match, or (None, None) without Node."""
+    version = node_version()
+    if version is None:
+        log("cpu baseline: node not found; skipped")
+        return None, None
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+
+    bits = O.js_cache_bits([cache.present(L) for L in range(cfg.layers)], context)
+    with tempfile.TemporaryDirectory() as d:
+        manifest = O.write_js_manifest(d, cfg, ckpt, scheme="int4", group=128, kv_f16=True, cache_bits=bits,
+                                       context=context, first=first, steps=steps)
+        res = O.run_js_model(manifest, timeout=900)
+    toks = res["tokens"]
+    match = sum(int(a == b) for a, b in zip(toks, gpu_tokens[:steps]))
+    cpu = {"value": round(steps / res["seconds"], 4), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"{steps} greedy decode steps at context {context}..{context + steps - 1} (KV cache "
+                     f"loaded from the GPU run), oracle/cpu_model.js under Node {version}, 1 thread, "
+                     f"{os.cpu_count()} host CPUs visible; {res['perStepSeconds']:.2f} s per token"}
+    return cpu, f"{match}/{steps}"
+
+
 def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
     """The oracle (a C port of the reference CPU path, f64 accumulation) on one core:
     its KV cache is loaded with the GPU cache's context (the same f16 values), then it
@@ -255,7 +292,7 @@ def main():
     ap.add_argument("--context", type=int, default=1024)
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--profile-steps", type=int, default=32)
-    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--isolated", choices=["all", "none"], default="all",
                     help="the isolated config-2 matvec, config-3 attention and config-5 prefill lines")
@@ -359,10 +396,16 @@ def main():
         attn = attention_sweep(ctx)
         prefill = prefill_bench(ctx, cfg, ckpt, args.seed)
 
-    cpu, match = (None, None)
+    cpu = match = cpu_c = match_c = None
     if not args.no_cpu:
-        cpu, match = cpu_baseline(cfg, ckpt, cache, first, tokens, args.cpu_steps, args.context)
-        log(f"cpu baseline: {cpu['value']} tok/s, greedy match {match}")
+        # The reference CPU path under Node (the baseline), and the C oracle beside it.
+        cpu, match = node_cpu_baseline(cfg, ckpt, cache, first, tokens, args.cpu_steps, args.context)
+        if cpu:
+            log(f"cpu baseline (node): {cpu['value']} tok/s, greedy match {match}")
+        cpu_c, match_c = cpu_baseline(cfg, ckpt, cache, first, tokens, args.cpu_steps, args.context)
+        log(f"cpu oracle (C): {cpu_c['value']} tok/s, greedy match {match_c}")
+        if cpu is None:
+            cpu, match = cpu_c, match_c
 
     line = {
         "metric": METRIC, "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1,
@@ -374,10 +417,12 @@ def main():
                    "global_batch": 1, "seq_len": args.context, "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_baseline_c": cpu_c,
         "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
         "per_kernel_us": per_kernel,
         "profile_tokens_match_timed": deterministic,
         "greedy_match_cpu_sample": match,
+        "greedy_match_cpu_c_sample": match_c,
         "matvec_isolated": iso,
         "attention_decode": attn,
         "prefill_512": prefill,

@@ -6,6 +6,7 @@ nothing in the product imports this module.
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 import subprocess
 
@@ -368,3 +369,74 @@ class OracleCache:
         if getattr(self, "h", None):
             lib().or_cache_free(self.h)
             self.h = None
+
+
+# ------------------------------------------- the CPU path under Node (cpu_model.js) --
+JS_MODEL = os.path.join(ROOT, "oracle", "cpu_model.js")
+
+
+def write_js_manifest(directory, cfg, ckpt, scheme="int4", group=128, kv_f16=True, cache_bits=None,
+                      context=0, first=0, steps=1):
+    """Files for oracle/cpu_model.js: the layer matrices as the quantizer's arrays (this
+    module's quantize_int4/int8, the reference quantizer restated), norms and biases f32,
+    the embedding's bf16 bits, the output head int8, and optionally a context of `context`
+    cache positions as f16 bits [layers][2][context][kv_dim]. Returns the manifest path."""
+    tensors = {}
+
+    def put(name, arr, dtype):
+        fn = name.replace("/", "_") + ".bin"
+        np.ascontiguousarray(arr).tofile(os.path.join(directory, fn))
+        tensors[name] = {"file": fn, "dtype": dtype, "length": int(np.asarray(arr).size)}
+
+    for name, bits in ckpt.items():
+        if name == "model.embed_tokens.weight":
+            put(name, bits, "u16")
+            q, s = quantize_int8(bf16_to_f32(bits))
+            put("lm_head.weight.q", q, "i8")
+            put("lm_head.weight.scales", s, "f32")
+        elif bits.ndim == 1:
+            put(name, bf16_to_f32(bits), "f32")
+        elif scheme == "int4":
+            q, s, z = quantize_int4(bf16_to_f32(bits), group)
+            put(name + ".q", q, "u8")
+            put(name + ".scales", s, "f32")
+            put(name + ".zeros", z, "f32")
+        else:
+            q, s = quantize_int8(bf16_to_f32(bits))
+            put(name + ".q", q, "i8")
+            put(name + ".scales", s, "f32")
+    cache = {"file": None, "length": 0}
+    if context:
+        fn = "cache.bin"
+        np.ascontiguousarray(cache_bits, np.uint16).tofile(os.path.join(directory, fn))
+        cache = {"file": fn, "length": int(context)}
+    manifest = {
+        "config": {"hidden": cfg.hidden, "intermediate": cfg.intermediate, "layers": cfg.layers,
+                   "heads": cfg.heads, "kvHeads": cfg.kv_heads, "headDim": cfg.head_dim,
+                   "vocab": cfg.vocab, "ropeTheta": cfg.rope_theta, "eps": cfg.eps},
+        "tensors": tensors, "scheme": scheme, "group": group, "kvF16": bool(kv_f16),
+        "cache": cache, "first": int(first), "steps": int(steps),
+    }
+    path = os.path.join(directory, "manifest.json")
+    with open(path, "w") as f:
+        json.dump(manifest, f)
+    return path
+
+
+def run_js_model(manifest, timeout=600):
+    """Runs oracle/cpu_model.js under Node on one thread; returns its JSON result."""
+    out = subprocess.run(["node", JS_MODEL, manifest], capture_output=True, text=True, timeout=timeout,
+                         check=True)
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+def js_cache_bits(presents, context):
+    """f16 bits [layers][2][context][kv_dim] from per-layer present() dicts ([kv_heads, n, 64]
+    f32 values that are f16 numbers)."""
+    out = []
+    for p in presents:
+        for kind in ("key", "value"):
+            a = np.asarray(p[kind])[:, :context]
+            out.append(np.ascontiguousarray(a.transpose(1, 0, 2).reshape(context, -1)).astype(np.float16)
+                       .view(np.uint16))
+    return np.stack(out)
