@@ -17,6 +17,8 @@ Also reported on the same JSON line:
   matvec_isolated  BASELINE config 2: int8 matvec with an f16 activation at the
                  five layer shapes, one list-driven launch over >= 512 MiB of
                  distinct matrices (larger than the 256 MB last-level cache)
+  loader         the load path's conversion kernels (bf16 checkpoint -> int8 / int4 / f16
+                 on the device) in GB/s, and the whole model load, host- vs device-converted
   cpu_baseline   the reference's src/cpu path restated in JavaScript (oracle/cpu_model.js)
                  timed under Node on one host core over a bounded sample of the same
                  workload; cpu_baseline_c the C oracle on the same sample
@@ -165,9 +167,7 @@ def prefill_bench(ctx, cfg, ckpt, seed, prompt_len=512, modes=("matvec", "batche
     """Config 5: time-to-first-token of a seeded prompt with int8 layers and head, through
     one decode step per position, the reference's 8-position tiles, and the MFMA contraction.
     A token's time covers the embedding gather, all layers, the head and the argmax readback."""
-    tensors = H.device_tensors(ckpt, cfg, "int8", 128, "int8")
-    model = H.GpuModel.load(ctx, tensors, cfg, maxPositions=prompt_len + 8)
-    del tensors
+    model = H.GpuModel.load_checkpoint(ctx, ckpt, cfg, "int8", 128, "int8", maxPositions=prompt_len + 8)
     prompt = H.synth_tokens(seed, "config5.prompt", cfg.vocab, prompt_len)
     res = {}
     logits = {}
@@ -268,6 +268,59 @@ def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
     return cpu, f"{match}/{steps}"
 
 
+def loader_bench(ctx, cfg, ckpt, reps=10):
+    """The loader's conversion kernels (qh_quantize) over bf16 checkpoint tensors resident in
+    HBM -- the output projection and every layer's gate|up and down matrices, each set as one
+    launch -- timed with HIP events on the library's stream over `reps` back-to-back launches;
+    algorithmic bytes = the bf16 source read once + the codes, scales and zero points written.
+    Then the whole model loaded both ways: host quantizer + upload, and device conversion."""
+    d, V = cfg.hidden, cfg.vocab
+    layers = range(cfg.layers)
+    gate_up = np.concatenate([ckpt[f"model.layers.{i}.mlp.{p}_proj.weight"] for i in layers for p in ("gate", "up")])
+    down = np.concatenate([ckpt[f"model.layers.{i}.mlp.down_proj.weight"] for i in layers])
+    embed = ckpt["model.embed_tokens.weight"]
+    cases = [("lm_head_int8", embed, H.FMT_INT8, 0), ("gate_up_int4", gate_up, H.FMT_INT4, 128),
+             ("down_int4", down, H.FMT_INT4, 128), ("lm_head_f16", embed, H.FMT_F16, 0)]
+    out = {}
+    for label, bits, fmt, group in cases:
+        rows, cols = bits.shape
+        n = rows * cols
+        src = ctx.upload(bits)
+        data, scales, zeros = ctx.quantize(src, H.FMT_BF16, rows, cols, fmt, group)   # warm
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.done()
+        ctx.record(e0)
+        for _ in range(reps):
+            ctx.quantize(src, H.FMT_BF16, rows, cols, fmt, group, data, scales, zeros)
+        ctx.record(e1)
+        us = ctx.elapsed_ms(e0, e1) * 1e3 / reps
+        ctx.destroy_event(e0), ctx.destroy_event(e1)
+        written = {H.FMT_INT8: n + 4 * rows, H.FMT_INT4: n // 2 + 8 * (n // max(group, 1)), H.FMT_F16: 2 * n}[fmt]
+        nbytes = 2 * n + written
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[label] = {"shape": [rows, cols], "us_per_launch": round(us, 1), "bytes_per_launch": nbytes,
+                      "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        log(f"convert {label} {rows}x{cols}: {us:.1f} us, {gbs:.0f} GB/s")
+        for b in (src, data, scales, zeros):
+            if b is not None:
+                b.free()
+    del gate_up, down
+    t0 = time.perf_counter()
+    tensors = H.device_tensors(ckpt, cfg, "int4", 128, "int8")
+    model = H.GpuModel.load(ctx, tensors, cfg, maxPositions=64)
+    host_s = time.perf_counter() - t0
+    model.destroy()
+    del tensors
+    t0 = time.perf_counter()
+    model = H.GpuModel.load_checkpoint(ctx, ckpt, cfg, "int4", 128, "int8", maxPositions=64)
+    device_s = time.perf_counter() - t0
+    model.destroy()
+    out["model_load_s"] = {"host_quantize_then_upload": round(host_s, 2), "device_convert": round(device_s, 2),
+                           "host_cpus": os.cpu_count()}
+    log(f"model load: host quantizer {host_s:.2f} s, device conversion {device_s:.2f} s")
+    return out
+
+
 def copy_calibration(mib, reps=5):
     """qh_copy of `mib` MiB, `reps` times: per dispatch it reads and writes exactly mib MiB, the
     scale for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -301,6 +354,8 @@ def main():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes are calibrated against")
     ap.add_argument("--prefill-only", choices=["all", "batched", "mfma"], default=None,
                     help="only the config-5 prefill (the named matmul modes), for profiling it alone")
+    ap.add_argument("--loader-only", action="store_true",
+                    help="only the loader's conversion kernels and the two whole-model loads")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
                     help="decode by hipGraph replay (default) or direct launches of the same "
                          "kernels (for profilers that do not follow graph launches)")
@@ -326,11 +381,13 @@ def main():
         print(json.dumps({"prefill_512": prefill_bench(ctx, cfg, ckpt, args.seed, modes=modes)}), flush=True)
         ctx.close()
         return
-    tensors = H.device_tensors(ckpt, cfg, "int4", 128, "int8")
+    if args.loader_only:
+        print(json.dumps({"loader": loader_bench(ctx, cfg, ckpt)}), flush=True)
+        ctx.close()
+        return
     extra = max(args.steps, args.warmup, args.profile_steps, args.cpu_steps) + 1
     capacity = args.context + extra
-    model = H.GpuModel.load(ctx, tensors, cfg, maxPositions=capacity)
-    del tensors
+    model = H.GpuModel.load_checkpoint(ctx, ckpt, cfg, "int4", 128, "int8", maxPositions=capacity)
     log(f"model ready in {time.perf_counter() - t0:.1f}s, {model.device_bytes / 1e6:.1f} MB on device")
 
     prompt = H.synth_tokens(args.seed, "config4.prompt", cfg.vocab, args.context)
@@ -388,13 +445,14 @@ def main():
                 "us_per_launch": round(kernel_us, 3)}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
-    iso = attn = prefill = None
+    iso = attn = prefill = loader = None
     if args.isolated == "all":
         d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
         iso = isolated_matvec(ctx, [("q_o", d, d), ("k_v", kv, d), ("gate_up", ffn, d),
                                     ("down", d, ffn), ("lm_head", V, d)])
         attn = attention_sweep(ctx)
         prefill = prefill_bench(ctx, cfg, ckpt, args.seed)
+        loader = loader_bench(ctx, cfg, ckpt)
 
     cpu = match = cpu_c = match_c = None
     if not args.no_cpu:
@@ -426,6 +484,7 @@ def main():
         "matvec_isolated": iso,
         "attention_decode": attn,
         "prefill_512": prefill,
+        "loader": loader,
         "prefill_s": round(prefill_s, 3),
     }
     print(json.dumps(line), flush=True)

@@ -199,6 +199,16 @@ int qh_quantize_int8(const float* h_w, int32_t rows, int32_t cols, int8_t* h_q,
                      float* h_scales);
 int qh_quantize_int4(const float* h_w, int32_t rows, int32_t cols, int32_t group,
                      uint8_t* h_q, float* h_scales, float* h_zeros);
+/* The same conversion on the device, for the loader (GpuModel.load's per-tensor upload,
+ * src/gpu/model.js:165-173: bf16ToF32Array, then quantizeInt8 / quantizeInt4 of
+ * src/core/quantize.js:36-132 or f32ToF16Array of src/core/dtype.js:81-113). d_src holds
+ * [rows, cols] values: src_format QH_FMT_BF16 (bits, widened exactly) or QH_FMT_F32. format
+ * QH_FMT_F32 | F16 | INT8 (d_scales [rows]) | INT4 (d_scales, d_zeros [rows * cols/group]; group
+ * even and dividing cols). Outputs as in qh_weight, bit-identical with qh_quantize_int8 /
+ * qh_quantize_int4 and the reference's f16 narrowing (NaN payloads included). Asynchronous on
+ * the context stream. */
+int qh_quantize(qh_ctx* ctx, int32_t src_format, const void* d_src, int32_t rows, int32_t cols,
+                int32_t format, int32_t group, void* d_data, float* d_scales, float* d_zeros);
 
 /* Seeded synthetic inputs (the reference has no random-init facility). Counter-based, so any
  * element can be generated independently and every platform produces the same bits.
@@ -261,6 +271,14 @@ int qh_model_set_matmul(qh_model* m, int32_t matmul);
 int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t rows,
                         int32_t cols, int32_t group, const void* h_data, const float* h_scales,
                         const float* h_zeros);
+/* As qh_model_set_tensor, from the checkpoint's own values: h_src holds [rows, cols] bf16 bits
+ * (src_format QH_FMT_BF16) or f32 values (QH_FMT_F32), uploaded in that width and converted to
+ * `format` on the device by qh_quantize's kernels -- GpuModel.load's per-tensor loop
+ * (src/gpu/model.js:165-181) with the widening, quantizing and narrowing moved off the host.
+ * The stored codes, scales and zero points equal those of qh_quantize_int8 / qh_quantize_int4
+ * on the widened values. The gather table takes bf16 values as they are. */
+int qh_model_load_tensor(qh_model* m, const char* name, int32_t src_format, int32_t rows,
+                         int32_t cols, const void* h_src, int32_t format, int32_t group);
 /* Checks that every tensor is present with its shape, builds the rope tables and the fused
  * device layouts. Afterwards the model is immutable. */
 int qh_model_finalize(qh_model* m);

@@ -199,6 +199,26 @@ int qh_copy(qh_ctx* ctx, void* d_dst, const void* d_src, size_t bytes) {
   return QH_OK;
 }
 
+int qh_quantize(qh_ctx* ctx, int32_t src_format, const void* d_src, int32_t rows, int32_t cols,
+                int32_t format, int32_t group, void* d_data, float* d_scales, float* d_zeros) {
+  QH_CHECK(ctx && d_src && d_data && rows >= 1 && cols >= 1, QH_ERR_INVALID,
+           "quantize needs a context, a non-empty source and an output");
+  QH_CHECK(src_format == QH_FMT_BF16 || src_format == QH_FMT_F32, QH_ERR_INVALID,
+           "quantize reads bf16 or f32 values (src_format %d)", src_format);
+  QH_CHECK(format == QH_FMT_F32 || format == QH_FMT_F16 || format == QH_FMT_INT8 || format == QH_FMT_INT4,
+           QH_ERR_INVALID, "quantize writes f32, f16, int8 or int4 (format %d)", format);
+  QH_CHECK(format != QH_FMT_INT8 || d_scales, QH_ERR_INVALID, "int8 needs a scale per row");
+  if (format == QH_FMT_INT4) {
+    QH_CHECK(d_scales && d_zeros, QH_ERR_INVALID, "int4 needs a scale and a zero point per group");
+    QH_CHECK(group >= 2, QH_ERR_RANGE, "groupSize must be an integer of at least 2, got %d", group);
+    QH_CHECK(cols % group == 0, QH_ERR_RANGE, "groupSize %d does not divide %d columns", group, cols);
+    QH_CHECK(group % 2 == 0, QH_ERR_INVALID, "groupSize %d must be even to pack a byte within a group", group);
+  }
+  QH_HIP(qh::launch_convert(ctx->stream, src_format == QH_FMT_BF16, d_src, rows, cols, format, group, d_data,
+                            d_scales, d_zeros));
+  return QH_OK;
+}
+
 int qh_event_create(qh_ctx* ctx, qh_event** out) {
   QH_CHECK(ctx && out, QH_ERR_INVALID, "event_create needs a context");
   qh_event* e = new qh_event();

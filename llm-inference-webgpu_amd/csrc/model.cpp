@@ -163,11 +163,13 @@ int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out) {
   return QH_OK;
 }
 
-int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t rows, int32_t cols,
-                        int32_t group, const void* h_data, const float* h_scales,
-                        const float* h_zeros) {
-  QH_CHECK(m && name && h_data, QH_ERR_INVALID, "set_tensor needs a model, a name and data");
+// The shape and formats a checkpoint name allows (src/core/config.js:88-119); a vector comes
+// back as [n, 1]. A matrix must also fit the kernels' layout rules (make_dmat).
+static int check_tensor(qh_model* m, const char* name, int32_t format, int32_t* rows_io, int32_t* cols_io,
+                        int32_t group) {
   QH_CHECK(!m->finalized, QH_ERR_STATE, "model is finalized; tensors are immutable");
+  int32_t& rows = *rows_io;
+  int32_t& cols = *cols_io;
   const qh_config& c = m->cfg;
   const int kv_dim = c.kv_heads * c.head_dim;
   const std::string n = name;
@@ -226,10 +228,27 @@ int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t r
       qh::DMat probe;
       int rc = qh::make_dmat(&w, &probe);
       if (rc) return fail(rc, "%s: %s", name, qh_last_error());
-      QH_CHECK(format == QH_FMT_F16 || h_scales, QH_ERR_INVALID, "%s needs scales", name);
-      QH_CHECK(format != QH_FMT_INT4 || h_zeros, QH_ERR_INVALID, "%s needs zero points", name);
     }
   }
+  return QH_OK;
+}
+
+// Keeps `s` as the tensor `name`, releasing an earlier upload of it.
+static void keep_staged(qh_model* m, const char* name, const Staged& s) {
+  auto it = m->staged.find(name);
+  if (it != m->staged.end()) free_staged(it->second);
+  m->staged[name] = s;
+}
+
+int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t rows, int32_t cols,
+                        int32_t group, const void* h_data, const float* h_scales,
+                        const float* h_zeros) {
+  QH_CHECK(m && name && h_data, QH_ERR_INVALID, "set_tensor needs a model, a name and data");
+  int rc = check_tensor(m, name, format, &rows, &cols, group);
+  if (rc) return rc;
+  QH_CHECK(!is_matrix_format(format) || format == QH_FMT_F16 || h_scales, QH_ERR_INVALID, "%s needs scales",
+           name);
+  QH_CHECK(format != QH_FMT_INT4 || h_zeros, QH_ERR_INVALID, "%s needs zero points", name);
   QH_HIP(hipSetDevice(m->ctx->device));
   Staged s;
   s.format = format;
@@ -256,9 +275,50 @@ int qh_model_set_tensor(qh_model* m, const char* name, int32_t format, int32_t r
     free_staged(s);
     return fail(QH_ERR_NOMEM, "uploading %s failed", name);
   }
-  auto it = m->staged.find(n);
-  if (it != m->staged.end()) free_staged(it->second);
-  m->staged[n] = s;
+  keep_staged(m, name, s);
+  return QH_OK;
+}
+
+int qh_model_load_tensor(qh_model* m, const char* name, int32_t src_format, int32_t rows, int32_t cols,
+                         const void* h_src, int32_t format, int32_t group) {
+  QH_CHECK(m && name && h_src, QH_ERR_INVALID, "load_tensor needs a model, a name and data");
+  QH_CHECK(src_format == QH_FMT_BF16 || src_format == QH_FMT_F32, QH_ERR_INVALID,
+           "%s: checkpoint values are bf16 or f32 (src_format %d)", name, src_format);
+  int rc = check_tensor(m, name, format, &rows, &cols, group);
+  if (rc) return rc;
+  // The gather table, or an f32 vector of an f32 checkpoint: nothing to convert.
+  if (format == src_format) return qh_model_set_tensor(m, name, format, rows, cols, group, h_src, nullptr, nullptr);
+  QH_CHECK(format != QH_FMT_BF16, QH_ERR_INVALID, "%s: the bf16 gather table takes bf16 values", name);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  Staged s;
+  s.format = format;
+  s.rows = rows;
+  s.cols = cols;
+  s.group = format == QH_FMT_INT4 ? group : 0;
+  const size_t nb = data_bytes(format, rows, cols);
+  const size_t ns = format == QH_FMT_INT8 ? (size_t)rows : format == QH_FMT_INT4 ? (size_t)rows * (cols / group) : 0;
+  const size_t src_bytes = data_bytes(src_format, rows, cols);
+  hipStream_t st = m->ctx->stream;
+  void* d_src = nullptr;
+  bool ok = hipMalloc(&d_src, src_bytes) == hipSuccess && hipMalloc(&s.data, nb) == hipSuccess;
+  if (ok && ns) ok = hipMalloc((void**)&s.scales, ns * 4) == hipSuccess;
+  if (ok && format == QH_FMT_INT4) ok = hipMalloc((void**)&s.zeros, ns * 4) == hipSuccess;
+  if (!ok) {
+    hipFree(d_src);
+    free_staged(s);
+    return fail(QH_ERR_NOMEM, "allocating %s failed", name);
+  }
+  // The borrowed host array is read before the synchronize below returns.
+  ok = hipMemcpyAsync(d_src, h_src, src_bytes, hipMemcpyHostToDevice, st) == hipSuccess &&
+       qh::launch_convert(st, src_format == QH_FMT_BF16, d_src, rows, cols, format, s.group, s.data, s.scales,
+                          s.zeros) == hipSuccess;
+  ok = hipStreamSynchronize(st) == hipSuccess && ok;
+  hipFree(d_src);
+  if (!ok) {
+    free_staged(s);
+    return fail(QH_ERR_DEVICE, "converting %s on the device failed", name);
+  }
+  keep_staged(m, name, s);
   return QH_OK;
 }
 

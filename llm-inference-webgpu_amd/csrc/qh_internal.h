@@ -137,6 +137,11 @@ hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n);
 // dst[0, bytes) = src[0, bytes): 16-byte vector copies when both are 16-byte aligned,
 // bytes otherwise.
 hipError_t launch_copy(hipStream_t s, void* dst, const void* src, size_t bytes);
+// [rows, cols] checkpoint values (bf16 bits when `bf16`, else f32) converted to `format`:
+// f32, f16, int8 (+ a scale per row) or int4 (+ a scale and zero per group; `group` even,
+// dividing cols), as the host quantizer writes them.
+hipError_t launch_convert(hipStream_t s, bool bf16, const void* src, int rows, int cols, int format,
+                          int group, void* data, float* scales, float* zeros);
 // Argmax into d_out[0]; `partials` holds argmax_partials_bytes(n) bytes; *counter is zero
 // before the launch and left zero after it.
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, void* partials,

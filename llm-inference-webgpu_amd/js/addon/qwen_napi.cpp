@@ -293,6 +293,28 @@ napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
   return nullptr;
 }
 
+// (model, name, srcFormat, rows, cols, data, format, group): the checkpoint's values converted
+// on the device.
+napi_value ModelLoadTensor(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  std::string name;
+  int32_t src_fmt, rows, cols, fmt, group;
+  void* data;
+  size_t bytes = 0;
+  if (!get_args(env, info, a, 8) || !to_handle(env, a.v[0], &m) || !to_str(env, a.v[1], &name) ||
+      !to_i32(env, a.v[2], &src_fmt) || !to_i32(env, a.v[3], &rows) || !to_i32(env, a.v[4], &cols) ||
+      !to_bytes(env, a.v[5], &data, &bytes) || !to_i32(env, a.v[6], &fmt) || !to_i32(env, a.v[7], &group))
+    return nullptr;
+  const size_t width = src_fmt == QH_FMT_BF16 ? 2 : 4;
+  if (rows < 1 || cols < 1 || bytes < (size_t)rows * cols * width) {
+    napi_throw_range_error(env, nullptr, "the data array is smaller than rows * cols values");
+    return nullptr;
+  }
+  QH_CALL(qh_model_load_tensor(m, name.c_str(), src_fmt, rows, cols, data, fmt, group));
+  return nullptr;
+}
+
 napi_value ModelFinalize(napi_env env, napi_callback_info info) {
   Args a;
   qh_model* m;
@@ -406,7 +428,8 @@ static napi_value Init(napi_env env, napi_value exports) {
              {"synthBf16", SynthBf16},     {"synthTokens", SynthTokens},
              {"quantizeInt8", QuantizeInt8}, {"quantizeInt4", QuantizeInt4},
              {"modelCreate", ModelCreate}, {"modelSetMode", ModelSetMode},
-             {"modelSetTensor", ModelSetTensor}, {"modelFinalize", ModelFinalize},
+             {"modelSetTensor", ModelSetTensor}, {"modelLoadTensor", ModelLoadTensor},
+             {"modelFinalize", ModelFinalize},
              {"modelFree", ModelFree},     {"cacheCreate", CacheCreate},
              {"cacheFree", CacheFree},     {"cacheLength", CacheLength},
              {"forward", Forward},         {"decode", Decode}};

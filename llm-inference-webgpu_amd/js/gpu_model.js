@@ -58,7 +58,7 @@ function f32ToF16Array(x) {
     const sign = (b >>> 16) & 0x8000;
     const exp = (b >>> 23) & 0xff;
     let mant = b & 0x7fffff;
-    if (exp === 0xff) { out[i] = sign | 0x7c00 | (mant ? 0x200 : 0); continue; }
+    if (exp === 0xff) { out[i] = sign | 0x7c00 | (mant ? (mant >>> 13) | 0x200 : 0); continue; }
     let e = exp - 127 + 15;
     if (e >= 0x1f) { out[i] = sign | 0x7c00; continue; }
     if (e <= 0) {
@@ -100,10 +100,13 @@ class GpuModel {
     this.maxPositions = maxPositions;
   }
 
-  // tensors: {name: {dtype: 'bf16', shape: [...], data: Uint16Array}} as a checkpoint reader
-  // returns them. opts: maxPositions (2048), quantize {scheme: 'int8'|'int4'|'f16', groupSize},
-  // headScheme (the output projection's format, default the layers'), matmul
-  // ('batched'|'matvec'|'mfma'), numerics ('fast'|'exact').
+  // tensors: {name: {dtype: 'bf16'|'f32', shape: [...], data: Uint16Array|Float32Array}} as a
+  // checkpoint reader returns them. opts: maxPositions (2048), quantize {scheme:
+  // 'int8'|'int4'|'f16', groupSize}, headScheme (the output projection's format, default the
+  // layers'), matmul ('batched'|'matvec'|'mfma'), numerics ('fast'|'exact'), convert ('device':
+  // each tensor uploaded in its checkpoint width and widened, quantized or narrowed by the
+  // library's kernels; 'host': converted here first, as the reference's loader does; both store
+  // the same bits).
   static load(ctx, tensors, config, opts) {
     opts = opts || {};
     const maxPositions = opts.maxPositions || 2048;
@@ -116,8 +119,26 @@ class GpuModel {
       addon.modelSetMode(handle, 'numerics', NUMERICS[opts.numerics || 'fast']);
       addon.modelSetMode(handle, 'matmul', MATMUL[opts.matmul || 'batched']);
       const names = Object.keys(tensors);
+      const onDevice = (opts.convert || 'device') === 'device';
+      if (!onDevice && opts.convert !== 'host') throw new Error('convert must be "device" or "host"');
       names.forEach(function (name, i) {
         const t = tensors[name];
+        if (t.dtype !== 'bf16' && t.dtype !== 'f32') throw new Error(name + ': dtype must be bf16 or f32');
+        if (onDevice) {
+          const src = t.dtype === 'bf16' ? FMT.bf16 : FMT.f32;
+          const rows = t.shape[0], cols = t.shape.length === 1 ? 1 : t.shape[1];
+          const load = function (as, fmt) {
+            addon.modelLoadTensor(handle, as, src, rows, cols, t.data, fmt, fmt === FMT.int4 ? group : 0);
+          };
+          if (name === 'model.embed_tokens.weight') {
+            load(name, FMT.bf16);
+            load('lm_head.weight', FMT[opts.headScheme || q.scheme]);
+          } else {
+            load(name, t.shape.length === 1 ? FMT.f32 : FMT[q.scheme]);
+          }
+          if (opts.onProgress) opts.onProgress(i + 1, names.length, name);
+          return;
+        }
         const w32 = t.dtype === 'bf16' ? bf16ToF32Array(t.data) : t.data;
         if (name === 'model.embed_tokens.weight') {
           addon.modelSetTensor(handle, name, FMT.bf16, t.shape[0], t.shape[1], 0, t.data, null, null);

@@ -147,11 +147,13 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
         "qh_quantize_int4": [vp, i32, i32, i32, vp, vp, vp],
+        "qh_quantize": [vp, i32, vp, i32, i32, i32, i32, vp, vp, vp],
         "qh_synth_f32": [u64, ctypes.c_char_p, f64, sz, sz, vp],
         "qh_synth_bf16": [u64, ctypes.c_char_p, f64, sz, sz, vp],
         "qh_synth_tokens": [u64, ctypes.c_char_p, i32, sz, vp],
         "qh_model_create": [vp, vp, vp],
         "qh_model_set_tensor": [vp, ctypes.c_char_p, i32, i32, i32, i32, vp, vp, vp],
+        "qh_model_load_tensor": [vp, ctypes.c_char_p, i32, i32, i32, vp, i32, i32],
         "qh_model_finalize": [vp], "qh_model_free": [vp], "qh_model_bytes": [vp, vp],
         "qh_model_set_numerics": [vp, i32], "qh_model_set_matmul": [vp, i32],
         "qh_cache_create": [vp, i32, vp], "qh_cache_free": [vp], "qh_cache_length": [vp, vp],
@@ -386,6 +388,24 @@ class GpuContext:
         """GpuContext.copy (device.js:168-175): a device copy kernel on the context stream."""
         _check(self.lib.qh_copy(self.handle, dst.ptr + dst_offset, src.ptr + src_offset, nbytes))
 
+    def quantize(self, src: DeviceBuffer, src_format: int, rows: int, cols: int, fmt: int,
+                 group: int = 0, data=None, scales=None, zeros=None):
+        """qh_quantize: [rows, cols] bf16 or f32 values on the device converted to `fmt`
+        (the loader's per-tensor conversion, src/gpu/model.js:165-173). Allocates the outputs
+        that are not given; returns (data, scales, zeros), absent ones None."""
+        n = rows * cols
+        nbytes = {FMT_F32: 4 * n, FMT_F16: 2 * n, FMT_INT8: n, FMT_INT4: n // 2}.get(fmt, 4)   # else rejected
+        per = rows if fmt == FMT_INT8 else rows * (cols // group) if fmt == FMT_INT4 and group > 0 else 0
+        if data is None:
+            data = self.empty(max(nbytes, 4), np.uint8)
+        if scales is None and per:
+            scales = self.empty(4 * per)
+        if zeros is None and fmt == FMT_INT4 and per:
+            zeros = self.empty(4 * per)
+        _check(self.lib.qh_quantize(self.handle, src_format, src.ptr, rows, cols, fmt, group, data.ptr,
+                                    scales.ptr if scales else None, zeros.ptr if zeros else None))
+        return data, scales, zeros
+
     def done(self) -> None:
         _check(self.lib.qh_sync(self.handle))
 
@@ -519,6 +539,60 @@ class GpuModel:
         matmul: how forward() runs several positions -- "batched" (8-position weight
         tiles, bitwise equal to decoding them one by one), "matvec" (one decode step per
         position) or "mfma" (bf16 matrix cores for int8/int4 weights)."""
+        def upload(lib, handle):
+            total = len(tensors)
+            for i, (name, (fmt, rows, cols, group, data, scales, zeros)) in enumerate(tensors.items()):
+                data = np.ascontiguousarray(data)
+                scales = None if scales is None else np.ascontiguousarray(scales, np.float32)
+                zeros = None if zeros is None else np.ascontiguousarray(zeros, np.float32)
+                _check(lib.qh_model_set_tensor(handle, name.encode(), fmt, rows, cols, group,
+                                               _ptr(data), _ptr(scales), _ptr(zeros)))
+                if onProgress:
+                    onProgress(i + 1, total, name)
+
+        return GpuModel._build(ctx, config, maxPositions, numerics, matmul, upload)
+
+    @staticmethod
+    def load_checkpoint(ctx: GpuContext, ckpt: dict, config: ModelConfig, scheme: str = "int4",
+                        group: int = 128, lm_head: str = "int8", maxPositions: int = 2048,
+                        onProgress=None, numerics: str = "fast",
+                        matmul: str = "batched") -> "GpuModel":
+        """GpuModel.load (src/gpu/model.js:147-207) from the checkpoint's own tensors
+        ({name: uint16 bf16 bits or float32 values}), each uploaded in its checkpoint width
+        and converted on the device (qh_model_load_tensor): layer matrices per `scheme`, the
+        tied embedding per `lm_head` as the output projection, the bf16 embedding as the
+        gather table, norms and biases f32. Stores the same bits as
+        load(ctx, device_tensors(ckpt, config, scheme, group, lm_head), config)."""
+        def src_of(a: np.ndarray):
+            if a.dtype == np.uint16:
+                return FMT_BF16, np.ascontiguousarray(a)
+            if a.dtype == np.float32:
+                return FMT_F32, np.ascontiguousarray(a)
+            raise ValueError(f"checkpoint tensors are bf16 bits (uint16) or float32, got {a.dtype}")
+
+        def upload(lib, handle):
+            jobs = []
+            for name, a in ckpt.items():
+                if name == "model.embed_tokens.weight":
+                    jobs.append((name, a, FMT_BF16))
+                    jobs.append(("lm_head.weight", a, FORMAT_OF[lm_head]))
+                elif a.ndim == 1:
+                    jobs.append((name, a, FMT_F32))
+                else:
+                    jobs.append((name, a, FORMAT_OF[scheme]))
+            for i, (name, a, fmt) in enumerate(jobs):
+                sf, src = src_of(a)
+                rows, cols = (a.shape[0], 1) if a.ndim == 1 else a.shape
+                _check(lib.qh_model_load_tensor(handle, name.encode(), sf, rows, cols, _ptr(src), fmt,
+                                                group if fmt == FMT_INT4 else 0))
+                if onProgress:
+                    onProgress(i + 1, len(jobs), name)
+
+        return GpuModel._build(ctx, config, maxPositions, numerics, matmul, upload)
+
+    @staticmethod
+    def _build(ctx: GpuContext, config: ModelConfig, maxPositions: int, numerics: str, matmul: str,
+               upload) -> "GpuModel":
         lib = ctx.lib
         h = ctypes.c_void_p()
         cc = config.c_config(maxPositions)
@@ -527,15 +601,7 @@ class GpuModel:
         try:
             _check(lib.qh_model_set_numerics(h.value, NUMERICS[numerics]))
             _check(lib.qh_model_set_matmul(h.value, MATMUL[matmul]))
-            total = len(tensors)
-            for i, (name, (fmt, rows, cols, group, data, scales, zeros)) in enumerate(tensors.items()):
-                data = np.ascontiguousarray(data)
-                scales = None if scales is None else np.ascontiguousarray(scales, np.float32)
-                zeros = None if zeros is None else np.ascontiguousarray(zeros, np.float32)
-                _check(lib.qh_model_set_tensor(h.value, name.encode(), fmt, rows, cols, group,
-                                               _ptr(data), _ptr(scales), _ptr(zeros)))
-                if onProgress:
-                    onProgress(i + 1, total, name)
+            upload(lib, h.value)
             _check(lib.qh_model_finalize(h.value))
         except Exception:
             lib.qh_model_free(h.value)

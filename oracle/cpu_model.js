@@ -48,7 +48,7 @@ function f32ToF16(x) {  // src/core/dtype.js:81-113, round to nearest even
   const sign = (b >>> 16) & 0x8000;
   const exp = (b >>> 23) & 0xff;
   let mant = b & 0x7fffff;
-  if (exp === 0xff) return sign | 0x7c00 | (mant ? 0x200 : 0);
+  if (exp === 0xff) return sign | 0x7c00 | (mant ? (mant >>> 13) | 0x200 : 0);
   const e = exp - 127 + 15;
   if (e >= 0x1f) return sign | 0x7c00;
   if (e <= 0) {

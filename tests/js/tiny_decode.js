@@ -1,19 +1,20 @@
 'use strict';
 // Drives a tiny Qwen2-shaped model through the Node-API driver: prompt logits, argmax and a
 // greedy decode, printed as JSON for tests/test_js_addon.py to compare with the Python binding.
-// Usage: node tiny_decode.js <scheme> <numerics> <matmul>
+// Usage: node tiny_decode.js <scheme> <numerics> <matmul> <convert: device|host>
 const path = require('path');
 const qh = require(path.join(__dirname, '..', '..', 'llm-inference-webgpu_amd', 'js', 'gpu_model.js'));
 
 const scheme = process.argv[2] || 'int4';
 const numerics = process.argv[3] || 'fast';
 const matmul = process.argv[4] || 'batched';
+const convert = process.argv[5] || 'device';
 const cfg = { hidden: 128, intermediate: 256, layers: 2, heads: 2, kvHeads: 1, vocab: 1000, ropeTheta: 1e6, eps: 1e-6 };
 const ctx = qh.GpuContext.create(0);
 const ckpt = qh.synthesizeCheckpoint(cfg, 3);
 const model = qh.GpuModel.load(ctx, ckpt, cfg, {
   maxPositions: 256, quantize: { scheme: scheme, groupSize: 128 }, headScheme: scheme === 'f16' ? 'f16' : 'int8',
-  numerics: numerics, matmul: matmul,
+  numerics: numerics, matmul: matmul, convert: convert,
 });
 const prompt = qh.synthTokens(3, 'prompt', cfg.vocab, 12);
 const cache = model.newCache(64);

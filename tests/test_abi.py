@@ -60,6 +60,27 @@ def test_product_int4_quantizer_matches_oracle(hip, rows, cols, group):
     np.testing.assert_array_equal(z.view(np.uint32), oz.view(np.uint32))
 
 
+def test_product_quantizers_match_oracle_on_special_values(hip):
+    rng = np.random.default_rng(7)
+    w = (rng.standard_normal((8, 256)) * 0.02).astype(np.float32)
+    w[0, ::5] = np.nan
+    w[1, 3], w[2, 200] = np.inf, -np.inf
+    w[3, :] = np.nan
+    w[4, :] = -0.0
+    w[5, :] = np.float32(1e-44) * np.sign(w[5, :])   # the f32 scale underflows, the f64 one does not
+    w[6, :8] = [0.0, -0.0, 1e-40, 3.4e38, -3.4e38, 65520.0, 2.0 ** -25, np.nan]
+    q, s = hip.quantize_int8(w)
+    oq, os_ = O.quantize_int8(w)
+    np.testing.assert_array_equal(q, oq)
+    np.testing.assert_array_equal(s.view(np.uint32), os_.view(np.uint32))
+    for group in (4, 32, 256):
+        q, s, z = hip.quantize_int4(w, group)
+        oq, os_, oz = O.quantize_int4(w, group)
+        np.testing.assert_array_equal(q, oq)
+        np.testing.assert_array_equal(s.view(np.uint32), os_.view(np.uint32))
+        np.testing.assert_array_equal(z.view(np.uint32), oz.view(np.uint32))
+
+
 def test_product_quantizer_tie_cases(hip):
     W = np.array([[127, 0.5, 2.5, -2.5, 63.5, -0.5, 1.49999, -126.5]], np.float32)
     q, _ = hip.quantize_int8(W)

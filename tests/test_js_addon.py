@@ -34,7 +34,7 @@ def addon_built():
 def test_addon_exports_the_driver_surface(addon_built):
     keys = json.loads(node("const a=require('./addon/qwen_napi.node'); console.log(JSON.stringify(Object.keys(a)))"))
     assert set(keys) == {"abiVersion", "open", "close", "describe", "synthBf16", "synthTokens", "quantizeInt8",
-                         "quantizeInt4", "modelCreate", "modelSetMode", "modelSetTensor", "modelFinalize",
+                         "quantizeInt4", "modelCreate", "modelSetMode", "modelSetTensor", "modelLoadTensor", "modelFinalize",
                          "modelFree", "cacheCreate", "cacheFree", "cacheLength", "forward", "decode"}
     assert node("console.log(require('./addon/qwen_napi.node').abiVersion())").strip() == "1"
 
@@ -77,10 +77,14 @@ def test_range_error_surfaces_as_js_range_error(addon_built):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("scheme,numerics,matmul", [("int4", "fast", "batched"), ("int8", "exact", "mfma"),
-                                                    ("f16", "fast", "matvec")])
-def test_js_driver_matches_python_binding(addon_built, ctx, hip, scheme, numerics, matmul):
-    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "tiny_decode.js"), scheme, numerics, matmul],
+@pytest.mark.parametrize("scheme,numerics,matmul,convert", [
+    ("int4", "fast", "batched", "device"), ("int4", "fast", "batched", "host"), ("int8", "exact", "mfma", "device"),
+    ("int8", "fast", "batched", "host"), ("f16", "fast", "matvec", "device"), ("f16", "exact", "batched", "host")])
+def test_js_driver_matches_python_binding(addon_built, ctx, hip, scheme, numerics, matmul, convert):
+    # The JS loader converts on the device or on the host; the Python side loads host-quantized
+    # tensors, so equal logits also show the two conversions store the same bits.
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "tiny_decode.js"), scheme, numerics, matmul,
+                        convert],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     js = json.loads(r.stdout)

@@ -196,3 +196,45 @@ def test_bits_per_weight():
     assert L.or_bits_per_weight(4, 896, 64) == 4 + 64 / 64
     assert 8 < L.or_bits_per_weight(8, 896, 0) < 8.1
     assert L.or_bits_per_weight(16, 0, 0) == 16
+
+
+# ------------------------------------------------------------ special values
+# What the reference's arithmetic gives non-finite inputs, worked by hand from its
+# JavaScript semantics: `m > peak` and `v < lo` skip NaN; Math.round(NaN) is NaN;
+# Math.min/Math.max propagate NaN; a typed-array store turns NaN into 0; Infinity * 0
+# and Infinity / Infinity are NaN; Math.max(0, -0) is +0.
+
+def test_int8_nan_is_skipped_by_the_peak_and_stored_as_zero():
+    q, s = O.quantize_int8(np.array([[np.nan, 0.5, -1.0, 0.0]], np.float32))
+    assert s[0] == np.float32(1 / 127)
+    np.testing.assert_array_equal(q[0], [0, 64, -127, 0])      # 63.5 rounds away to 64
+
+
+def test_int8_infinite_peak_gives_infinite_scale_and_zero_codes():
+    q, s = O.quantize_int8(np.array([[np.inf, 1.0, -3.0, 0.0], [np.nan] * 4], np.float32))
+    assert np.isposinf(s[0]) and s[1] == 0
+    np.testing.assert_array_equal(q, 0)
+
+
+def test_int4_nan_in_a_group():
+    # lo -15, hi 15: scale 2, zero round(7.5) = 8; 15 -> 7.5 -> 8 + 8 clamps to 15;
+    # -15 -> -7.5 -> -8 + 8 = 0; 0 -> 8; NaN -> 0.
+    q, s, z = O.quantize_int4(np.array([[np.nan, 15.0, -15.0, 0.0]], np.float32), 4)
+    assert s[0, 0] == 2 and z[0, 0] == 8
+    np.testing.assert_array_equal(q[0], [0xF0, 0x80])
+
+
+def test_int4_infinite_range():
+    # +inf: scale inf, zero round(-0/inf) = -0 -> Math.max(0, -0) = +0, inverse 0, levels 0.
+    # -inf: -lo/scale = inf/inf = NaN, so the zero point is NaN and every level NaN -> 0.
+    q, s, z = O.quantize_int4(np.array([[np.inf, 1.0, 0.0, 0.0, -np.inf, 1.0, 0.0, 0.0]], np.float32), 4)
+    assert np.isposinf(s[0, 0]) and z[0, 0] == 0 and not np.signbit(z[0, 0])
+    assert np.isposinf(s[0, 1]) and np.isnan(z[0, 1])
+    np.testing.assert_array_equal(q, 0)
+
+
+def test_int4_signed_zero_groups_have_zero_scale():
+    q, s, z = O.quantize_int4(np.array([[-0.0, 0.0, 0.0, -0.0, np.nan, np.nan, np.nan, np.nan]], np.float32), 4)
+    np.testing.assert_array_equal(s, 0)
+    np.testing.assert_array_equal(z, 0)
+    np.testing.assert_array_equal(q, 0)
