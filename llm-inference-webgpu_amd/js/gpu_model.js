@@ -10,6 +10,7 @@
 
 const path = require('path');
 const addon = require(path.join(__dirname, 'addon', 'qwen_napi.node'));
+const { Safetensors, parseConfig, expectedTensors, checkAgainst } = require('./safetensors.js');
 
 const FMT = { f32: 0, f16: 1, int8: 2, int4: 3, bf16: 4 };
 const NUMERICS = { fast: 0, exact: 1 };
@@ -100,8 +101,9 @@ class GpuModel {
     this.maxPositions = maxPositions;
   }
 
-  // tensors: {name: {dtype: 'bf16'|'f32', shape: [...], data: Uint16Array|Float32Array}} as a
-  // checkpoint reader returns them. opts: maxPositions (2048), quantize {scheme:
+  // tensors: a Safetensors checkpoint (./safetensors.js, src/gpu/model.js:147's `safetensors`), or
+  // {name: {dtype: 'bf16'|'f32', shape: [...], data: Uint16Array|Float32Array}}. config: the
+  // dimensions (parseConfig of config.json gives them). opts: maxPositions (2048), quantize {scheme:
   // 'int8'|'int4'|'f16', groupSize}, headScheme (the output projection's format, default the
   // layers'), matmul ('batched'|'matvec'|'mfma'), numerics ('fast'|'exact'), convert ('device':
   // each tensor uploaded in its checkpoint width and widened, quantized or narrowed by the
@@ -118,37 +120,48 @@ class GpuModel {
     try {
       addon.modelSetMode(handle, 'numerics', NUMERICS[opts.numerics || 'fast']);
       addon.modelSetMode(handle, 'matmul', MATMUL[opts.matmul || 'batched']);
-      const names = Object.keys(tensors);
+      // A checkpoint file (Safetensors) is checked against the config and read one tensor at
+      // a time; a dict of tensors is taken as given.
+      const file = typeof tensors.tensor === 'function' ? tensors : null;
+      if (file) checkAgainst(cfg, file);
+      const names = file ? Object.keys(expectedTensors(cfg)) : Object.keys(tensors);
+      const tied = names.indexOf('lm_head.weight') < 0;
+      const head = opts.headScheme || q.scheme;
       const onDevice = (opts.convert || 'device') === 'device';
       if (!onDevice && opts.convert !== 'host') throw new Error('convert must be "device" or "host"');
       names.forEach(function (name, i) {
-        const t = tensors[name];
+        const t = file ? file.tensor(name) : tensors[name];
         if (t.dtype !== 'bf16' && t.dtype !== 'f32') throw new Error(name + ': dtype must be bf16 or f32');
+        const embed = name === 'model.embed_tokens.weight';
+        if (embed && t.dtype !== 'bf16') throw new Error(name + ': the gather table is bf16, got ' + t.dtype);
+        const scheme = name === 'lm_head.weight' ? head : q.scheme;
         if (onDevice) {
           const src = t.dtype === 'bf16' ? FMT.bf16 : FMT.f32;
           const rows = t.shape[0], cols = t.shape.length === 1 ? 1 : t.shape[1];
           const load = function (as, fmt) {
             addon.modelLoadTensor(handle, as, src, rows, cols, t.data, fmt, fmt === FMT.int4 ? group : 0);
           };
-          if (name === 'model.embed_tokens.weight') {
+          if (embed) {
             load(name, FMT.bf16);
-            load('lm_head.weight', FMT[opts.headScheme || q.scheme]);
+            if (tied) load('lm_head.weight', FMT[head]);
           } else {
-            load(name, t.shape.length === 1 ? FMT.f32 : FMT[q.scheme]);
+            load(name, t.shape.length === 1 ? FMT.f32 : FMT[scheme]);
           }
           if (opts.onProgress) opts.onProgress(i + 1, names.length, name);
           return;
         }
         const w32 = t.dtype === 'bf16' ? bf16ToF32Array(t.data) : t.data;
-        if (name === 'model.embed_tokens.weight') {
+        if (embed) {
           addon.modelSetTensor(handle, name, FMT.bf16, t.shape[0], t.shape[1], 0, t.data, null, null);
-          const m = deviceMatrix(w32, t.shape[0], t.shape[1], opts.headScheme || q.scheme, group);
-          addon.modelSetTensor(handle, 'lm_head.weight', m.format, m.rows, m.cols, m.group, m.data,
-                               m.scales || null, m.zeros || null);
+          if (tied) {
+            const m = deviceMatrix(w32, t.shape[0], t.shape[1], head, group);
+            addon.modelSetTensor(handle, 'lm_head.weight', m.format, m.rows, m.cols, m.group, m.data,
+                                 m.scales || null, m.zeros || null);
+          }
         } else if (t.shape.length === 1) {
           addon.modelSetTensor(handle, name, FMT.f32, t.shape[0], 1, 0, w32, null, null);
         } else {
-          const m = deviceMatrix(w32, t.shape[0], t.shape[1], q.scheme, group);
+          const m = deviceMatrix(w32, t.shape[0], t.shape[1], scheme, group);
           addon.modelSetTensor(handle, name, m.format, m.rows, m.cols, m.group, m.data,
                                m.scales || null, m.zeros || null);
         }
@@ -192,23 +205,7 @@ class GpuModel {
 // from the library's counter-based generator, stream per tensor name.
 function synthesizeCheckpoint(config, seed, std) {
   std = std === undefined ? 0.02 : std;
-  const d = config.hidden, kv = config.kvHeads * (config.hidden / config.heads), f = config.intermediate;
-  const shapes = { 'model.embed_tokens.weight': [config.vocab, d], 'model.norm.weight': [d] };
-  for (let i = 0; i < config.layers; i++) {
-    const p = 'model.layers.' + i + '.';
-    shapes[p + 'input_layernorm.weight'] = [d];
-    shapes[p + 'post_attention_layernorm.weight'] = [d];
-    shapes[p + 'self_attn.q_proj.weight'] = [d, d];
-    shapes[p + 'self_attn.q_proj.bias'] = [d];
-    shapes[p + 'self_attn.k_proj.weight'] = [kv, d];
-    shapes[p + 'self_attn.k_proj.bias'] = [kv];
-    shapes[p + 'self_attn.v_proj.weight'] = [kv, d];
-    shapes[p + 'self_attn.v_proj.bias'] = [kv];
-    shapes[p + 'self_attn.o_proj.weight'] = [d, d];
-    shapes[p + 'mlp.gate_proj.weight'] = [f, d];
-    shapes[p + 'mlp.up_proj.weight'] = [f, d];
-    shapes[p + 'mlp.down_proj.weight'] = [d, f];
-  }
+  const shapes = expectedTensors(Object.assign({}, config, { tieWordEmbeddings: true }));
   const out = {};
   Object.keys(shapes).forEach(function (name) {
     const shape = shapes[name];
@@ -228,5 +225,5 @@ const QWEN25_05B = {
 
 module.exports = {
   GpuContext, GpuModel, GpuKVCache, synthesizeCheckpoint, synthTokens, bf16ToF32Array, f32ToF16Array,
-  QWEN25_05B, addon,
+  QWEN25_05B, addon, Safetensors, parseConfig,
 };

@@ -15,6 +15,7 @@ library is missing or no device is present, calls raise.
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 from dataclasses import dataclass
 
@@ -74,6 +75,76 @@ class ModelConfig:
     vocab: int = 151936
     rope_theta: float = 1e6
     eps: float = 1e-6
+    tie_word_embeddings: bool = True
+
+    REQUIRED = ("hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+                "num_key_value_heads", "vocab_size", "max_position_embeddings", "rope_theta",
+                "rms_norm_eps")
+
+    @staticmethod
+    def from_hf(raw) -> "ModelConfig":
+        """ModelConfig of src/core/config.js:16-80 from a config.json (text, path or dict):
+        the required numbers, and the architectures this engine refuses."""
+        if isinstance(raw, str):
+            raw = json.loads(open(raw).read() if os.path.exists(raw) else raw)
+        for key in ModelConfig.REQUIRED:
+            v = raw.get(key)
+            if isinstance(v, bool) or not isinstance(v, (int, float)) or not np.isfinite(v):
+                raise QwenHipError(QH_ERR_INVALID, f"config: {key} must be a finite number, got {json.dumps(v)}")
+        if raw.get("model_type") != "qwen2":
+            raise QwenHipError(QH_ERR_INVALID,
+                               f"config: only qwen2 is implemented, got {json.dumps(raw.get('model_type'))}")
+        if raw.get("hidden_act", "silu") != "silu":
+            raise QwenHipError(QH_ERR_INVALID,
+                               f"config: only the silu/SwiGLU MLP is implemented, got {raw.get('hidden_act')}")
+        if raw.get("use_sliding_window") is True:
+            raise QwenHipError(QH_ERR_INVALID, "config: sliding-window attention is not implemented")
+        d, h, kvh = raw["hidden_size"], raw["num_attention_heads"], raw["num_key_value_heads"]
+        if d % h:
+            raise QwenHipError(QH_ERR_INVALID,
+                               f"config: hidden_size {d} is not divisible by num_attention_heads {h}")
+        if h % kvh:
+            raise QwenHipError(QH_ERR_INVALID, f"config: num_attention_heads {h} is not divisible by "
+                                               f"num_key_value_heads {kvh}")
+        return ModelConfig(hidden=d, intermediate=raw["intermediate_size"], layers=raw["num_hidden_layers"],
+                           heads=h, kv_heads=kvh, vocab=raw["vocab_size"], rope_theta=float(raw["rope_theta"]),
+                           eps=float(raw["rms_norm_eps"]), tie_word_embeddings=raw.get("tie_word_embeddings") is True)
+
+    def expected_tensors(self) -> dict:
+        """Every tensor the architecture requires, with its shape (config.js:89-121)."""
+        d, kv, ffn = self.hidden, self.kv_dim, self.intermediate
+        shapes = {"model.embed_tokens.weight": (self.vocab, d), "model.norm.weight": (d,)}
+        for i in range(self.layers):
+            p = f"model.layers.{i}."
+            shapes.update({
+                p + "input_layernorm.weight": (d,), p + "post_attention_layernorm.weight": (d,),
+                p + "self_attn.q_proj.weight": (d, d), p + "self_attn.q_proj.bias": (d,),
+                p + "self_attn.k_proj.weight": (kv, d), p + "self_attn.k_proj.bias": (kv,),
+                p + "self_attn.v_proj.weight": (kv, d), p + "self_attn.v_proj.bias": (kv,),
+                p + "self_attn.o_proj.weight": (d, d),
+                p + "mlp.gate_proj.weight": (ffn, d), p + "mlp.up_proj.weight": (ffn, d),
+                p + "mlp.down_proj.weight": (d, ffn),
+            })
+        if not self.tie_word_embeddings:
+            shapes["lm_head.weight"] = (self.vocab, d)
+        return shapes
+
+    def check_against(self, st) -> int:
+        """checkAgainst (config.js:128-153): exactly the implied tensors, each with its shape."""
+        expected = self.expected_tensors()
+        problems = []
+        for name, shape in expected.items():
+            if not st.has(name):
+                problems.append(f"missing {name}")
+            elif tuple(st.info(name).shape) != tuple(shape):
+                problems.append(f"{name}: expected shape {list(shape)}, file has {list(st.info(name).shape)}")
+        problems += [f"unexpected tensor {n}" for n in st.names() if n not in expected]
+        if problems:
+            more = f"\n  ... and {len(problems) - 10} more" if len(problems) > 10 else ""
+            raise QwenHipError(QH_ERR_INVALID, f"weights do not match config ({len(problems)} problem"
+                                               f"{'' if len(problems) == 1 else 's'}):\n  "
+                               + "\n  ".join(problems[:10]) + more)
+        return len(expected)
 
     @property
     def head_dim(self) -> int:
@@ -589,6 +660,66 @@ class GpuModel:
                     onProgress(i + 1, len(jobs), name)
 
         return GpuModel._build(ctx, config, maxPositions, numerics, matmul, upload)
+
+    @staticmethod
+    def load_safetensors(ctx: GpuContext, path: str, config: ModelConfig | None = None, scheme: str = "int4",
+                         group: int = 128, lm_head: str = "int8", maxPositions: int = 2048, onProgress=None,
+                         numerics: str = "fast", matmul: str = "batched") -> "GpuModel":
+        """GpuModel.load (src/gpu/model.js:147-207) from a safetensors checkpoint. `path` is the
+        model file, or a directory holding model.safetensors and config.json (which then gives
+        `config`). The file is checked against the config first (checkAgainst,
+        src/core/config.js:128-153). Each tensor goes to the device from the read-only file
+        mapping as stored -- bf16 bits or f32 -- one at a time, and is converted there
+        (qh_model_load_tensor); an f16 tensor is widened exactly on the host first. The
+        embedding is the bf16 gather table and, for a tied model, also the output projection
+        in `lm_head` format; an untied checkpoint's lm_head.weight is used instead."""
+        import checkpoint
+
+        if os.path.isdir(path):
+            if config is None:
+                config = ModelConfig.from_hf(os.path.join(path, "config.json"))
+            path = os.path.join(path, "model.safetensors")
+        if config is None:
+            raise QwenHipError(QH_ERR_INVALID, "load_safetensors needs a config (or a directory with config.json)")
+        st = checkpoint.Safetensors.open(path)
+        config.check_against(st)
+
+        def upload(lib, handle):
+            jobs = []
+            for name, shape in config.expected_tensors().items():
+                if name == "model.embed_tokens.weight":
+                    jobs.append((name, name, FMT_BF16))
+                    if config.tie_word_embeddings:
+                        jobs.append(("lm_head.weight", name, FORMAT_OF[lm_head]))
+                elif name == "lm_head.weight":
+                    jobs.append((name, name, FORMAT_OF[lm_head]))
+                else:
+                    jobs.append((name, name, FMT_F32 if len(shape) == 1 else FORMAT_OF[scheme]))
+            for i, (as_name, name, fmt) in enumerate(jobs):
+                dtype = st.info(name).dtype
+                a = st.array(name)
+                if dtype == "BF16":
+                    sf, src = FMT_BF16, a
+                elif dtype == "F32":
+                    sf, src = FMT_F32, a
+                elif dtype == "F16":
+                    sf, src = FMT_F32, a.view(np.float16).astype(np.float32)
+                else:
+                    raise QwenHipError(QH_ERR_INVALID, f"{name}: dtype {dtype} is not a weight format")
+                if fmt == FMT_BF16 and sf != FMT_BF16:
+                    raise QwenHipError(QH_ERR_INVALID, f"{name}: the gather table is bf16 and the file holds "
+                                                       f"{dtype}")
+                rows, cols = (a.shape[0], 1) if a.ndim == 1 else a.shape
+                _check(lib.qh_model_load_tensor(handle, as_name.encode(), sf, rows, cols,
+                                                _ptr(np.ascontiguousarray(src)), fmt,
+                                                group if fmt == FMT_INT4 else 0))
+                if onProgress:
+                    onProgress(i + 1, len(jobs), as_name)
+
+        try:
+            return GpuModel._build(ctx, config, maxPositions, numerics, matmul, upload)
+        finally:
+            st.close()
 
     @staticmethod
     def _build(ctx: GpuContext, config: ModelConfig, maxPositions: int, numerics: str, matmul: str,
