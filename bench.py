@@ -268,6 +268,83 @@ def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
     return cpu, f"{match}/{steps}"
 
 
+def scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 32, 52, 64, 128, 256, 512, 1024), repeats=5,
+                  decode_steps=24, paths=("matvec", "batched", "mfma")):
+    """The same-session path comparison of web/scaling.html:40-194: time-to-logits of a prompt
+    through each matmul path (median/min/max of `repeats`, the path order rotated every repeat),
+    after a check at 52 tokens that the paths compute the same model (batched bit-identical to
+    matvec; MFMA within 1e-4 with the same argmax), then single-token forward steps after a
+    32-token prompt, the paths alternating step by step on caches of their own. int8 layers and
+    head (the MFMA path contracts int8/int4); the embedding rows come from the host as the page
+    gathers them, so each timing is of the forward pass alone."""
+    model = H.GpuModel.load_checkpoint(ctx, ckpt, cfg, "int8", 128, "int8", maxPositions=max(lengths) + 64)
+    d = cfg.hidden
+    longest = max(max(lengths), 32 + decode_steps) + 2
+    emb = ckpt["model.embed_tokens.weight"]
+    ids = (1000 + 7 * np.arange(longest)) % cfg.vocab                 # web/scaling.html:69
+    hidden = H.bf16_to_f32(emb[ids]).reshape(-1)
+
+    def prefill(path, seq):
+        model.set_matmul(path)
+        cache = model.newCache(seq + 2)
+        t0 = time.perf_counter()
+        out = model.forward(hidden[:seq * d], seq, cache)
+        ms = (time.perf_counter() - t0) * 1e3
+        cache.destroy()
+        return ms, out
+
+    for path in paths:                       # first use of every tile shape and code object
+        for seq in (1, 2, 4, 8, 64):
+            prefill(path, seq)
+    outs = {p: prefill(p, 52)[1] for p in paths}
+    m, b = outs["matvec"]["logits"], outs["batched"]["logits"]
+    agree = {"logits": int(m.size), "batched_differing": int(np.sum(m.view(np.uint32) != b.view(np.uint32))),
+             "argmax": {p: outs[p]["argmax"] for p in paths}}
+    if "mfma" in outs:
+        agree["mfma_max_relative"] = float(np.max(np.abs(outs["mfma"]["logits"].astype(np.float64) - m))
+                                           / np.max(np.abs(m)))
+    ok = agree["batched_differing"] == 0 and len(set(agree["argmax"].values())) == 1 and \
+        agree.get("mfma_max_relative", 0.0) < 1e-4
+    if not ok:
+        raise RuntimeError(f"paths disagree: {json.dumps(agree)}")
+
+    def summary(runs):
+        return {"median": round(float(np.median(runs)), 3), "min": round(min(runs), 3), "max": round(max(runs), 3)}
+
+    rows = []
+    for seq in lengths:
+        runs = {p: [] for p in paths}
+        for i in range(repeats):
+            for k in range(len(paths)):
+                p = paths[(k + i) % len(paths)]
+                runs[p].append(prefill(p, seq)[0])
+        row = {"seq": seq, **{p: summary(runs[p]) for p in paths}}
+        row["speedup_vs_matvec"] = {p: round(row["matvec"]["median"] / row[p]["median"], 2) for p in paths[1:]}
+        rows.append(row)
+        log(f"scaling prefill {seq}: " + ", ".join(f"{p} {row[p]['median']:.2f} ms" for p in paths))
+    caches = {}
+    for p in paths:
+        model.set_matmul(p)
+        caches[p] = model.newCache(32 + decode_steps + 2)
+        model.forward(hidden[:32 * d], 32, caches[p])
+    steps = {p: [] for p in paths}
+    for i in range(decode_steps):
+        row_x = hidden[(32 + i) * d:(33 + i) * d]
+        for k in range(len(paths)):
+            p = paths[(k + i) % len(paths)]
+            model.set_matmul(p)
+            t0 = time.perf_counter()
+            model.forward(row_x, 1, caches[p])
+            steps[p].append((time.perf_counter() - t0) * 1e3)
+    for c in caches.values():
+        c.destroy()
+    model.destroy()
+    decode = {p: {**summary(steps[p]), "tok_per_s": round(1e3 / float(np.median(steps[p])), 1)} for p in paths}
+    log(f"scaling decode step: " + ", ".join(f"{p} {decode[p]['median']:.3f} ms" for p in paths))
+    return {"agree": agree, "prefill": rows, "decode_after_32": decode, "repeats": repeats,
+            "weights": "int8 layers, int8 head", "timing": "wall clock around forward(), logits read back"}
+
+
 def loader_bench(ctx, cfg, ckpt, reps=10):
     """The loader's conversion kernels (qh_quantize) over bf16 checkpoint tensors resident in
     HBM -- the output projection and every layer's gate|up and down matrices, each set as one
@@ -354,6 +431,8 @@ def main():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE passes are calibrated against")
     ap.add_argument("--prefill-only", choices=["all", "batched", "mfma"], default=None,
                     help="only the config-5 prefill (the named matmul modes), for profiling it alone")
+    ap.add_argument("--scaling", action="store_true",
+                    help="only the same-session comparison of the matmul paths over prompt lengths")
     ap.add_argument("--loader-only", action="store_true",
                     help="only the loader's conversion kernels and the two whole-model loads")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
@@ -383,6 +462,10 @@ def main():
         return
     if args.loader_only:
         print(json.dumps({"loader": loader_bench(ctx, cfg, ckpt)}), flush=True)
+        ctx.close()
+        return
+    if args.scaling:
+        print(json.dumps({"scaling": scaling_bench(ctx, cfg, ckpt)}), flush=True)
         ctx.close()
         return
     extra = max(args.steps, args.warmup, args.profile_steps, args.cpu_steps) + 1

@@ -277,8 +277,9 @@ int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const f
   QH_CHECK(((uintptr_t)d_x & 15) == 0, QH_ERR_INVALID, "x must be 16-byte aligned");
   QH_CHECK(M >= 1, QH_ERR_INVALID, "M %d must be at least 1", M);
   void* tmp = nullptr;
-  QH_HIP(hipMallocAsync(&tmp, qh::matmul_prefill_scratch_bytes(m, M), ctx->stream));
-  hipError_t e = qh::launch_matmul_prefill(ctx->stream, m, d_x, d_bias, d_y, M, tmp);
+  const size_t scratch = qh::matmul_prefill_scratch_bytes(m, M);
+  QH_HIP(hipMallocAsync(&tmp, scratch, ctx->stream));
+  hipError_t e = qh::launch_matmul_prefill(ctx->stream, m, d_x, d_bias, d_y, M, tmp, scratch);
   QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
   return QH_OK;

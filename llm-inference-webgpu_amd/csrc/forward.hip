@@ -136,7 +136,7 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
 static hipError_t matmul(hipStream_t s, const ModelDev& m, int mode, const DMat& w, const float* x,
                          const float* bias, float* y, int seq, const PrefillDev& p) {
   if (mode == QH_MATMUL_MFMA && w.format != QH_FMT_F16)
-    return launch_matmul_prefill(s, w, x, bias, y, seq, p.scratch);
+    return launch_matmul_prefill(s, w, x, bias, y, seq, p.scratch, p.scratch_bytes);
   if (m.numerics == QH_NUMERICS_FAST) return launch_matvec_f32(s, w, x, bias, y, seq);
   return launch_matvec(s, w, x, bias, y, seq, static_cast<double*>(p.scratch));
 }

@@ -724,6 +724,7 @@ int ensure_prefill(qh_cache* c) {
   w.part = w.scores = p;
   w.counters = reinterpret_cast<int*>(static_cast<char*>(c->pw_mem) + fbytes);
   w.scratch = static_cast<char*>(c->pw_mem) + fbytes + cbytes;
+  w.scratch_bytes = b.scratch;
   return QH_OK;
 }
 

@@ -86,6 +86,7 @@ struct PrefillDev {
   float* scores;       // exact past kPLds: [P][heads][score_stride] + [P][heads][spans]
   int* counters;       // exact: [P][heads], zero between launches
   void* scratch;       // matmul scratch (f64 activations, MFMA splits)
+  size_t scratch_bytes;
 };
 struct PrefillBytes {
   size_t floats, counters, scratch;

@@ -235,7 +235,8 @@ static int gemm_steps_per_split(const DMat& w, int M) {
   return per;
 }
 
-size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
+// Scratch of one launch over exactly M rows: the activation terms, then the split partials.
+static size_t gemm_scratch_bytes(const DMat& w, int M) {
   const size_t split_bytes = (size_t)M * w.cols * kTerms * sizeof(uint16_t);
   const int steps = w.cols / kGK;
   const int per = gemm_steps_per_split(w, M);
@@ -244,8 +245,19 @@ size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
   return ((split_bytes + 255) & ~(size_t)255) + part;
 }
 
+// Scratch for every launch of 1..M rows. Not the M-row figure alone: below a 64-row tile
+// boundary there are fewer tiles and so more splits, and the partials of a smaller M can
+// outgrow M's own (896 x 896: 64 rows take 28 splits, 1792 partial rows; 66 rows take 14,
+// 924 partial rows).
+size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
+  size_t most = 0;
+  for (int m = 1; m <= M; m++) most = std::max(most, gemm_scratch_bytes(w, m));
+  return most;
+}
+
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias,
-                                 float* y, int M, void* scratch) {
+                                 float* y, int M, void* scratch, size_t scratch_bytes) {
+  if (M < 1 || gemm_scratch_bytes(w, M) > scratch_bytes) return hipErrorInvalidValue;
   const size_t nx = (size_t)M * w.cols;
   uint16_t* xt = static_cast<uint16_t*>(scratch);
   hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, s, x, xt, nx);

@@ -90,9 +90,11 @@ hipError_t launch_matvec_f32(hipStream_t s, const DMat& m, const float* x, const
                              int seq);
 bool matvec_f32_supported(const DMat& m);
 // The batched-prefill contraction on bf16 MFMA (int8 / int4 weights): y [M, rows] = x [M, cols] . W^T
-// (+ bias). `scratch` holds matmul_prefill_scratch_bytes(w, M) bytes.
+// (+ bias). `scratch` holds `scratch_bytes` bytes; a launch that needs more returns
+// hipErrorInvalidValue before any work. matmul_prefill_scratch_bytes(w, M) covers every
+// launch of up to M rows.
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias, float* y,
-                                 int M, void* scratch);
+                                 int M, void* scratch, size_t scratch_bytes);
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
@@ -103,7 +105,7 @@ hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* gain, floa
 hipError_t launch_rope(hipStream_t s, float* v, const float* cos_t, const float* sin_t, int rows,
                        int heads, int head_dim, int base_pos);
 // Keys [kv_heads][capacity][head_dim]; values dimension-major [kv_heads][head_dim][vstride],
-// vstride = capacity rounded up to a multiple of 8.
+// vstride = value_stride(capacity).
 hipError_t launch_kv_append(hipStream_t s, const float* k, const float* v, uint16_t* kc,
                             uint16_t* vt, int capacity, int kv_heads, int head_dim, int past,
                             int seq);

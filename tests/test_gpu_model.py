@@ -327,3 +327,26 @@ def test_config5_prefill_batched_and_mfma_match_oracle(ctx, hip, full_ckpt, nume
     for _, c in out.values():
         c.destroy()
     model.destroy()
+
+
+@pytest.mark.parametrize("capacity,seq", [(66, 64), (130, 64), (600, 65)])
+def test_mfma_prefill_shorter_than_its_workspace(ctx, hip, full_ckpt, capacity, seq):
+    """A cache's prefill workspace serves every prompt of up to min(capacity, 512) positions.
+    The MFMA contraction splits K more finely when a prompt has fewer 64-row tiles, so a
+    prompt shorter than the workspace can need more split partials than the workspace's own
+    length (capacity 66 or 130 with 64 positions, at the o-projection's 896 x 896); the
+    workspace is sized for the largest need over every length."""
+    cfg = hip.QWEN25_05B
+    model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int8", 128, "int8", maxPositions=capacity + 8)
+    prompt = hip.synth_tokens(6, "short.prompt", cfg.vocab, seq)
+    res = {}
+    for mode in ("batched", "mfma"):
+        model.set_matmul(mode)
+        cache = model.newCache(capacity)
+        res[mode] = model.forward_tokens(prompt, cache)
+        cache.destroy()
+    err = rel_err(res["mfma"]["logits"], res["batched"]["logits"])
+    print(f"mfma prefill {seq} positions, capacity {capacity}: logits rel {err:.2e} vs batched")
+    assert err <= MFMA_LOGIT_REL
+    assert res["mfma"]["argmax"] == res["batched"]["argmax"]
+    model.destroy()
