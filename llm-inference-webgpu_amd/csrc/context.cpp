@@ -273,6 +273,9 @@ int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const f
   QH_CHECK(m.format == QH_FMT_INT8 || m.format == QH_FMT_INT4, QH_ERR_INVALID,
            "the MFMA prefill takes int8 or int4 weights (format %d given)", m.format);
   QH_CHECK(m.cols % 32 == 0, QH_ERR_INVALID, "cols %d must be a multiple of 32", m.cols);
+  QH_CHECK(qh::matmul_prefill_supported(m), QH_ERR_INVALID,
+           "the MFMA prefill takes int8, or int4 in groups of a multiple of 64 columns, and at most "
+           "131072 columns (group %d, cols %d)", w->group, m.cols);
   QH_CHECK(d_x && d_y, QH_ERR_INVALID, "matmul needs x and y");
   QH_CHECK(((uintptr_t)d_x & 15) == 0, QH_ERR_INVALID, "x must be 16-byte aligned");
   QH_CHECK(M >= 1, QH_ERR_INVALID, "M %d must be at least 1", M);

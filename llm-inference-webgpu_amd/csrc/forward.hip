@@ -123,7 +123,7 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
     const LayerDev& l = m.layers_host[L];
     for (const DMat* w : {&l.qkv, &l.o, &l.gu, &l.down}) {
       if (m.numerics == QH_NUMERICS_EXACT) scratch = std::max(scratch, matvec_x64_bytes(*w, (int)P));
-      if (matmul == QH_MATMUL_MFMA && w->format != QH_FMT_F16)
+      if (matmul == QH_MATMUL_MFMA && matmul_prefill_supported(*w))
         scratch = std::max(scratch, matmul_prefill_scratch_bytes(*w, (int)P));
     }
   }
@@ -135,7 +135,7 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
 // the decode step does for the model's numerics.
 static hipError_t matmul(hipStream_t s, const ModelDev& m, int mode, const DMat& w, const float* x,
                          const float* bias, float* y, int seq, const PrefillDev& p) {
-  if (mode == QH_MATMUL_MFMA && w.format != QH_FMT_F16)
+  if (mode == QH_MATMUL_MFMA && matmul_prefill_supported(w))
     return launch_matmul_prefill(s, w, x, bias, y, seq, p.scratch, p.scratch_bytes);
   if (m.numerics == QH_NUMERICS_FAST) return launch_matvec_f32(s, w, x, bias, y, seq);
   return launch_matvec(s, w, x, bias, y, seq, static_cast<double*>(p.scratch));

@@ -4,209 +4,268 @@
 // GEMM: its prefill reads each weight once per <= 8 positions (batchedMatvec,
 // src/gpu/kernels.js:232-290); this is the M = 512 contraction that replaces it.
 //
-// Arithmetic. A weight code is an exact bf16: int8 q in [-127, 127], int4
-// (level - zero) in [-15, 15]. The activation is split into three bf16 terms
-// that sum to it exactly (x = t0 + t1 + t2: t0 = bf16(x), t1 = bf16(x - t0),
-// t2 = x - t0 - t1, each difference exact in f32 and the last one 8 significant
-// bits), and all three go through v_mfma_f32_16x16x32_bf16 into one f32
-// accumulator, so every product is exact and only the f32 accumulation rounds. The scale is
-// factored out of the code sum: per output column for int8, per 128-column group
-// for int4 (the group's partial sum is scaled into the running total). The
-// reference's own GPU path accumulates in f32 as well (kernels.js:56-76).
+// Arithmetic: integers on v_mfma_i32_16x16x64_i8. A weight code is already a small
+// integer: int8 q in [-127, 127], int4 (level - zero) in [-15, 15]. Each activation
+// row is made one too, once per call (k_digits): with s = max|x_row| / 127, every x
+// becomes the fixed-point integer X = rint(x * 2^16 / s), |X| <= 127 * 2^16, an
+// absolute error of at most s * 2^-17 = max|x_row| * 2^-17 / 127 (the row's largest
+// value keeps 24 significant bits, as in f32), stored as three balanced base-256
+// digits X = d0 + 256 d1 + 65536 d2, each an int8. The three digit planes go through
+// the int8 MFMA against the raw codes, so every product and every sum is exact in
+// int32 (|d q| <= 128 * 127, times at most 2^17 columns, stays below 2^31), and the
+// digits are recombined in f64 (S0 + 256 S1 + 65536 S2, exact) only at the end: for
+// int8 once per output, for int4 once per group, scaled by the group's scale into an
+// f64 running total. The output is that total times s * 2^-16 (and the int8 row
+// scale), rounded once to f32.
 //
-// Tiling. A block computes a 64 (positions) x 64 (weight rows) tile with four
-// waves of 32 x 32 (2 x 2 MFMA tiles of 16 x 16), stepping K by 32: each step the
-// block stages the three activation terms (64 x 32 bf16 each) and the weights,
-// widened to bf16 (64 x 32), in LDS rows padded by 16 bytes, while the next
-// step's global loads are already in flight in registers. Long K is split over
-// gridDim.z; partial tiles are summed in a fixed order by k_gemm_finish.
+// Tiling. A block of four waves computes 64 positions x 128 weight rows, each wave
+// owning 16 positions (1 x 8 MFMA tiles of 16 x 16), stepping K by 64. The weight tile
+// (128 x 64 codes, int4 expanded to int8) is staged in one of two LDS buffers, one
+// barrier per step; each lane loads its three digit fragments (16 bytes of its row per
+// digit) straight from global memory, three steps ahead. A step is 24 MFMAs per wave
+// against 8 LDS fragment reads and no per-element vector arithmetic for int8 weights.
+// Long K is split over gridDim.z; partial tiles are summed in a fixed order by
+// k_gemm_finish.
 #include <algorithm>
 
 #include "device_common.h"
 
 namespace qh {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kGM = 64, kGN = 64, kGK = 32;
-constexpr int kTerms = 3;       // bf16 terms of an activation
-constexpr int kGRow = kGK + 8;  // bf16 per LDS row: 64 bytes + 16 of padding
+constexpr int kGM = 64, kGN = 128, kGK = 64;
+constexpr int kDigits = 3;                    // base-256 digits of an activation
+constexpr int kGemmWaves = 4;                 // waves per block, 16 positions each
+constexpr int kGemmThreads = kGemmWaves * kWave;
+constexpr int kNT = kGN / 16;                 // 16-column MFMA tiles per wave
+constexpr int kGRow = kGK + 16;               // bytes per LDS row: 64 + 16 of padding
+constexpr int kStages = 3;                    // K steps of global loads in flight
 
-struct GemmArgs {
-  DMat w;                 // int8 | int4, rows = N, cols = K
-  const uint16_t* xt;     // bf16 [kTerms][M][K]: the activation's terms
-  float* out;             // splits == 1: Y [M][N]; else partials [splits][M][N]
-  const float* bias;      // [N] or NULL (splits == 1 only)
-  int M, N, K;
-  int steps_per_split;    // K steps (of 32) per gridDim.z slice
-};
+// K rounded up to whole steps: the digit planes are that wide, zeros past K.
+__host__ __device__ inline int padded_k(int K) { return (K + kGK - 1) / kGK * kGK; }
 
-__device__ __forceinline__ uint32_t bf16_bits_rne(float f) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;  // finite inputs
-}
+// ------------------------------------------------------------ activation digits --
+// The larger magnitude, NaN kept once met.
+__device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v != v) ? v : p; }
 
-// An exact small integer as bf16 bits (|v| < 256): the f32 has no low half.
-__device__ __forceinline__ uint32_t small_int_bf16(int v) {
-  return __builtin_bit_cast(uint32_t, (float)v) >> 16;
-}
-
-// The activation split: t0 = bf16(x), t1 = bf16(x - t0), t2 = bf16(x - t0 - t1) = x - t0 - t1.
-__global__ void k_split_bf16(const float* __restrict__ x, uint16_t* __restrict__ t, size_t n) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float r = x[i];
+// One block per row of X [M][K]: digits [kDigits][M][Kp] (int8) and the row factor
+// s * 2^-16 (f64; 0 for an all-zero row, whose digits are all zero).
+__global__ __launch_bounds__(kBlock) void k_digits(const float* __restrict__ x, int M, int K, int Kp,
+                                                   int8_t* __restrict__ digits, double* __restrict__ row_factor) {
+  __shared__ float red[kBlock / kWave];
+  const int m = blockIdx.x;
+  const float* row = x + (size_t)m * K;
+  float peak = 0.f;
+  for (int k = threadIdx.x; k < K; k += kBlock) peak = peak_of(peak, fabsf(row[k]));
+  for (int off = kWave / 2; off > 0; off >>= 1) peak = peak_of(peak, __shfl_xor(peak, off));
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = peak;
+  __syncthreads();
+  peak = 0.f;
 #pragma unroll
-  for (int k = 0; k < kTerms; k++) {
-    const uint32_t b = bf16_bits_rne(r);
-    t[(size_t)k * n + i] = (uint16_t)b;
-    r -= __builtin_bit_cast(float, b << 16);  // exact
+  for (int w = 0; w < kBlock / kWave; w++) peak = peak_of(peak, red[w]);
+  // A row holding an infinity or a NaN has no fixed-point form: its digits are zero and its
+  // factor NaN, so its outputs are NaN.
+  const bool finite = peak <= 3.402823466e38f;
+  const double s = (double)peak / 127.0;
+  const double inv = finite && peak > 0.f ? 65536.0 / s : 0.0;
+  if (threadIdx.x == 0) row_factor[m] = finite ? s / 65536.0 : (double)NAN;
+  const size_t plane = (size_t)M * Kp;
+  for (int k4 = 4 * threadIdx.x; k4 < Kp; k4 += 4 * kBlock) {
+    uint32_t w[kDigits] = {0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int k = k4 + e;
+      int v = k < K && inv != 0.0 ? (int)rint((double)row[k] * inv) : 0;  // |v| <= 127 * 2^16
+#pragma unroll
+      for (int d = 0; d < kDigits; d++) {
+        const int dig = (int)(int8_t)(uint8_t)(v & 0xff);  // balanced: [-128, 127]
+        w[d] |= (uint32_t)(uint8_t)dig << (8 * e);
+        v = (v - dig) >> 8;
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < kDigits; d++)
+      *reinterpret_cast<uint32_t*>(digits + d * plane + (size_t)m * Kp + k4) = w[d];
   }
 }
 
-// Weights of one K step for thread t: row n0 + t/4, columns k0 + 8*(t%4) .. +7,
-// as eight bf16 (packed in a v4u), int4 codes offset by the group's zero point.
+// ------------------------------------------------------------------ weight tile --
+// Thirty-two codes of one step for one thread: row n, columns k .. k+31, as int8.
 template <int FMT>
-struct WStep {
-  uint32_t raw[2];  // int8: 8 codes; int4: raw[0] = 8 nibbles
-  float zero;       // int4
+struct WRaw {
+  v4u q[2];  // int8: 32 codes; int4: q[0] = 32 nibbles
+  int zero;  // int4: the group's zero point
 };
 
 template <int FMT>
-__device__ __forceinline__ void wstep_load(const DMat& w, int n, int k, WStep<FMT>& s) {
+__device__ __forceinline__ void wraw_load(const DMat& w, int n, int k, int K, WRaw<FMT>& r) {
+  if (k >= K) {  // past K (a half step): zero codes
+    r.q[0] = r.q[1] = v4u{0, 0, 0, 0};
+    r.zero = 0;
+    return;
+  }
   const uint8_t* row = w.data + (size_t)n * w.row_bytes;
   if constexpr (FMT == QH_FMT_INT8) {
-    const uint2 v = *reinterpret_cast<const uint2*>(row + k);
-    s.raw[0] = v.x;
-    s.raw[1] = v.y;
+    r.q[0] = *reinterpret_cast<const v4u*>(row + k);
+    r.q[1] = *reinterpret_cast<const v4u*>(row + k + 16);
   } else {
-    s.raw[0] = *reinterpret_cast<const uint32_t*>(row + k / 2);
-    s.zero = w.zeros[(size_t)n * w.gpr + k / (w.cpg * 32)];
+    r.q[0] = *reinterpret_cast<const v4u*>(row + k / 2);
+    // an integer in [0, 15] (src/core/quantize.js:115)
+    r.zero = (int)w.zeros[(size_t)n * w.gpr + k / (w.cpg * 32)];
   }
 }
 
+// Bytewise a + b (mod 256 in each byte, no carry between bytes).
+__device__ __forceinline__ uint32_t add_bytes(uint32_t a, uint32_t b) {
+  return ((a & 0x7f7f7f7fu) + (b & 0x7f7f7f7fu)) ^ ((a ^ b) & 0x80808080u);
+}
+
+// The thirty-two codes as int8 bytes, in column order (int4: level - zero; the low
+// nibble of a byte is the even column).
 template <int FMT>
-__device__ __forceinline__ v4u wstep_widen(const WStep<FMT>& s) {
-  uint32_t b[8];
+__device__ __forceinline__ void wraw_bytes(const WRaw<FMT>& r, v4u (&o)[2]) {
   if constexpr (FMT == QH_FMT_INT8) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) b[e] = small_int_bf16((int)(int8_t)(uint8_t)(s.raw[e / 4] >> (8 * (e % 4))));
+    o[0] = r.q[0];
+    o[1] = r.q[1];
   } else {
-    const int z = (int)s.zero;  // an integer in [0, 15] (src/core/quantize.js:115)
+    const uint32_t nz = (uint32_t)((256 - r.zero) & 0xff) * 0x01010101u;  // -zero in every byte
+    uint32_t b[8];
+    const uint32_t src[4] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w};
 #pragma unroll
-    for (int e = 0; e < 8; e++) b[e] = small_int_bf16((int)((s.raw[0] >> (4 * e)) & 0xfu) - z);
+    for (int i = 0; i < 4; i++) {
+      const uint32_t lo = src[i] & 0x0f0f0f0fu, hi = (src[i] >> 4) & 0x0f0f0f0fu;  // even, odd columns
+      // interleave: bytes lo0 hi0 lo1 hi1 | lo2 hi2 lo3 hi3
+      b[2 * i] = add_bytes(__builtin_amdgcn_perm(hi, lo, 0x05010400u), nz);
+      b[2 * i + 1] = add_bytes(__builtin_amdgcn_perm(hi, lo, 0x07030602u), nz);
+    }
+    o[0] = v4u{b[0], b[1], b[2], b[3]};
+    o[1] = v4u{b[4], b[5], b[6], b[7]};
   }
-  return v4u{b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16), b[6] | (b[7] << 16)};
 }
 
+struct GemmArgs {
+  DMat w;                    // int8 | int4, rows = N, cols = K
+  const int8_t* digits;      // [kDigits][M][Kp]
+  const double* row_factor;  // [M]
+  float* out;                // splits == 1: Y [M][N]; else partials [splits][M][N]
+  const float* bias;         // [N] or NULL (splits == 1 only)
+  int M, N, K, Kp;
+  int steps_per_split;       // K steps (of 64) per gridDim.z slice
+};
+
 template <int FMT>
-__global__ __launch_bounds__(kBlock) void k_gemm(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[kTerms][kGM][kGRow];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[kGN][kGRow];
+__global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][kGN][kGRow];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
   const int s0 = blockIdx.z * a.steps_per_split;
-  const int s1 = min(s0 + a.steps_per_split, a.K / kGK);
+  const int s1 = min(s0 + a.steps_per_split, a.Kp / kGK);
+  const int fr = lane & 15, fg = lane >> 4;  // fragment row (or column) and 16-byte k group
+  const int mw = m0 + 16 * wave;             // this wave's first position
+  const bool active = mw < a.M;              // wave-uniform: rows past M are not computed
 
-  // Staging map: thread t owns row t/4 (of A and of B), columns 8*(t%4) .. +7.
-  const int sr = tid >> 2, sc = 8 * (tid & 3);
-  const size_t arow = (size_t)min(m0 + sr, a.M - 1) * a.K;  // rows past M: results discarded
-  const int brow = min(n0 + sr, a.N - 1);
+  // A fragments: this lane's row mw + fr (clamped; results past M are discarded), bytes
+  // 16*fg .. +15 of each step, one per digit plane.
+  const size_t plane = (size_t)a.M * a.Kp;
+  const int8_t* ar = a.digits + (size_t)min(mw + fr, a.M - 1) * a.Kp + 16 * fg;
+  // Weight staging: thread t stages row t/2 of the tile, columns 32*(t%2) .. +31.
+  const int br = tid >> 1, bk = 32 * (tid & 1);
+  const int brow = min(n0 + br, a.N - 1);
 
-  // Wave tile: rows wm*32 .. +31, columns wn*32 .. +31 of the block tile.
-  const int wm = wave >> 1, wn = wave & 1;
-  const int fr = lane & 15, fk = 8 * (lane >> 4);  // fragment row and k offset
-
-  f32x4 grp[2][2];
-  double acc[2][2][4];
+  v4i acc[kDigits][kNT];
+  double tot[kNT][4];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int j = 0; j < kNT; j++) {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int d = 0; d < kDigits; d++) acc[d][j] = v4i{0, 0, 0, 0};
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0;
-    }
-
-  // Column scales of this lane's output columns (int8: one per row of W).
-  float cs[2] = {1.f, 1.f};
-  if constexpr (FMT == QH_FMT_INT8) {
-#pragma unroll
-    for (int j = 0; j < 2; j++) cs[j] = a.w.scales[min(n0 + wn * 32 + 16 * j + fr, a.N - 1)];
+    for (int r = 0; r < 4; r++) tot[j][r] = 0.0;
   }
-  // K steps per f32 partial: an int4 group, else 128 columns.
-  const int group_steps = FMT == QH_FMT_INT4 ? a.w.cpg : 4;
+  // int4: steps per group (a group is a multiple of 64 columns on this path).
+  const int group_steps = FMT == QH_FMT_INT4 ? a.w.cpg / 2 : 1;
 
-  const size_t tstride = (size_t)a.M * a.K;  // elements between activation terms
-  v4u xa[kTerms];
-  WStep<FMT> ws;
-  if (s0 < s1) {
-    const int k = s0 * kGK + sc;
+  v4i xa[kStages][kDigits];
+  WRaw<FMT> wr[kStages];
+  auto issue = [&](int st, v4i (&x)[kDigits], WRaw<FMT>& w) {
+    const int k = st * kGK;
+    if (active) {
 #pragma unroll
-    for (int t = 0; t < kTerms; t++) xa[t] = *reinterpret_cast<const v4u*>(a.xt + t * tstride + arow + k);
-    wstep_load<FMT>(a.w, brow, k, ws);
-  }
-  for (int st = s0; st < s1; st++) {
-#pragma unroll
-    for (int t = 0; t < kTerms; t++) *reinterpret_cast<v4u*>(&As[t][sr][sc]) = xa[t];
-    *reinterpret_cast<v4u*>(&Bs[sr][sc]) = wstep_widen<FMT>(ws);
-    __syncthreads();
-    if (st + 1 < s1) {  // next step's loads in flight during this step's MFMAs
-      const int k = (st + 1) * kGK + sc;
-#pragma unroll
-      for (int t = 0; t < kTerms; t++) xa[t] = *reinterpret_cast<const v4u*>(a.xt + t * tstride + arow + k);
-      wstep_load<FMT>(a.w, brow, k, ws);
+      for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + d * plane + k);
     }
-    bf16x8 fa[kTerms][2], fb[2];
+    wraw_load<FMT>(a.w, brow, k + bk, a.K, w);
+  };
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+  for (int u = 0; u < kStages; u++)
+    if (s0 + u < s1) issue(s0 + u, xa[u], wr[u]);
+  for (int base = s0; base < s1; base += kStages) {
 #pragma unroll
-      for (int t = 0; t < kTerms; t++)
-        fa[t][i] = *reinterpret_cast<const bf16x8*>(&As[t][wm * 32 + 16 * i + fr][fk]);
-      fb[i] = *reinterpret_cast<const bf16x8*>(&Bs[wn * 32 + 16 * i + fr][fk]);
-    }
+    for (int u = 0; u < kStages; u++) {
+      const int st = base + u;
+      if (st >= s1) break;  // uniform over the block
+      const int buf = (st - s0) & 1;
+      {
+        v4u wb[2];
+        wraw_bytes<FMT>(wr[u], wb);
+        *reinterpret_cast<v4u*>(&Bs[buf][br][bk]) = wb[0];
+        *reinterpret_cast<v4u*>(&Bs[buf][br][bk + 16]) = wb[1];
+      }
+      v4i xd[kDigits];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int d = 0; d < kDigits; d++) xd[d] = xa[u][d];
+      if (st + kStages < s1) issue(st + kStages, xa[u], wr[u]);
+      // One barrier per step: Bs[buf] is complete, and every wave has finished reading it
+      // two steps ago (each wave reads a buffer before it arrives at the next barrier).
+      __syncthreads();
+      if (active) {
+        v4i fb[kNT];
 #pragma unroll
-      for (int j = 0; j < 2; j++)
+        for (int j = 0; j < kNT; j++) fb[j] = *reinterpret_cast<const v4i*>(&Bs[buf][16 * j + fr][16 * fg]);
 #pragma unroll
-        for (int t = 0; t < kTerms; t++)
-          grp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[t][i], fb[j], grp[i][j], 0, 0, 0);
-    if ((st + 1) % group_steps == 0 || st + 1 == s1) {  // fold the f32 partial into the f64 total
-      const int g = st / group_steps;
+        for (int d = 0; d < kDigits; d++)
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        double sg = 1.0;
+          for (int j = 0; j < kNT; j++)
+            acc[d][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xd[d], fb[j], acc[d][j], 0, 0, 0);
         if constexpr (FMT == QH_FMT_INT4) {
-          const int n = min(n0 + wn * 32 + 16 * j + fr, a.N - 1);
-          sg = a.w.scales[(size_t)n * a.w.gpr + g];
-        }
+          if ((st + 1) % group_steps == 0) {  // the group's exact sum, scaled into the total
+            const int g = st / group_steps;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+            for (int j = 0; j < kNT; j++) {
+              const double sg = a.w.scales[(size_t)min(n0 + 16 * j + fr, a.N - 1) * a.w.gpr + g];
 #pragma unroll
-          for (int r = 0; r < 4; r++) acc[i][j][r] += sg * (double)grp[i][j][r];
-          grp[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+              for (int r = 0; r < 4; r++)
+                tot[j][r] += sg * ((double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 +
+                                   (double)acc[0][j][r]);
+#pragma unroll
+              for (int d = 0; d < kDigits; d++) acc[d][j] = v4i{0, 0, 0, 0};
+            }
+          }
         }
       }
     }
-    __syncthreads();
   }
+  if (!active) return;
 
-  // D fragment: lane holds rows 4*(lane/16) .. +3 of column lane%16 of each tile.
+  // D fragment: lane holds rows 4*fg .. +3 of column fr of each tile.
   float* dst = a.out + (size_t)blockIdx.z * a.M * a.N;
+  double rf[4];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int n = n0 + wn * 32 + 16 * j + fr;
+  for (int r = 0; r < 4; r++) rf[r] = a.row_factor[min(mw + 4 * fg + r, a.M - 1)];
+#pragma unroll
+  for (int j = 0; j < kNT; j++) {
+    const int n = n0 + 16 * j + fr;
     if (n >= a.N) continue;
-    const float b = a.bias ? a.bias[n] : 0.f;
+    const double cs = FMT == QH_FMT_INT8 ? (double)a.w.scales[n] : 1.0;
+    const double b = a.bias ? (double)a.bias[n] : 0.0;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * 32 + 16 * i + 4 * (lane >> 4) + r;
-        if (m < a.M) dst[(size_t)m * a.N + n] = (float)(acc[i][j][r] * (double)cs[j] + (double)b);
-      }
+    for (int r = 0; r < 4; r++) {
+      const int m = mw + 4 * fg + r;
+      double v;
+      if constexpr (FMT == QH_FMT_INT8)
+        v = (double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 + (double)acc[0][j][r];
+      else
+        v = tot[j][r];
+      if (m < a.M) dst[(size_t)m * a.N + n] = (float)(v * rf[r] * cs + b);
     }
   }
 }
@@ -222,33 +281,41 @@ __global__ void k_gemm_finish(const float* __restrict__ part, int splits, const 
   y[i] = v + (bias ? bias[i % N] : 0.f);
 }
 
-// K steps per split: enough (M/64 x N/64 x splits) tiles to cover the chip twice,
-// int4 splits on group boundaries.
+// int8, or int4 in groups of a multiple of 64 columns (a step never spans two scales); K up
+// to 2^17 keeps every int32 sum exact.
+bool matmul_prefill_supported(const DMat& w) {
+  return (w.format == QH_FMT_INT8 || (w.format == QH_FMT_INT4 && w.cpg % 2 == 0)) && w.cols <= (1 << 17);
+}
+
+// K steps per split: as many splits as keep (M/64 x N/128 x splits) blocks within two per
+// CU, int4 splits on group boundaries.
 static int gemm_steps_per_split(const DMat& w, int M) {
-  const int steps = w.cols / kGK;
+  const int steps = padded_k(w.cols) / kGK;
   const int tiles = ((M + kGM - 1) / kGM) * ((w.rows + kGN - 1) / kGN);
-  const int unit = w.format == QH_FMT_INT4 ? w.cpg : 1;
-  int splits = (512 + tiles - 1) / tiles;
+  const int unit = w.format == QH_FMT_INT4 ? w.cpg / 2 : 1;
+  int splits = 512 / tiles;
   splits = std::max(1, std::min(splits, steps / unit));
   int per = (steps + splits - 1) / splits;
   per = (per + unit - 1) / unit * unit;
   return per;
 }
 
-// Scratch of one launch over exactly M rows: the activation terms, then the split partials.
+static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Scratch of one launch over exactly M rows: the digit planes, the row factors, and the
+// split partials.
 static size_t gemm_scratch_bytes(const DMat& w, int M) {
-  const size_t split_bytes = (size_t)M * w.cols * kTerms * sizeof(uint16_t);
-  const int steps = w.cols / kGK;
+  const int Kp = padded_k(w.cols);
+  const int steps = Kp / kGK;
   const int per = gemm_steps_per_split(w, M);
   const int splits = (steps + per - 1) / per;
   const size_t part = splits > 1 ? (size_t)splits * M * w.rows * sizeof(float) : 0;
-  return ((split_bytes + 255) & ~(size_t)255) + part;
+  return round256((size_t)kDigits * M * Kp) + round256((size_t)M * sizeof(double)) + part;
 }
 
 // Scratch for every launch of 1..M rows. Not the M-row figure alone: below a 64-row tile
 // boundary there are fewer tiles and so more splits, and the partials of a smaller M can
-// outgrow M's own (896 x 896: 64 rows take 28 splits, 1792 partial rows; 66 rows take 14,
-// 924 partial rows).
+// outgrow M's own.
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
   size_t most = 0;
   for (int m = 1; m <= M; m++) most = std::max(most, gemm_scratch_bytes(w, m));
@@ -257,29 +324,36 @@ size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
 
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias,
                                  float* y, int M, void* scratch, size_t scratch_bytes) {
-  if (M < 1 || gemm_scratch_bytes(w, M) > scratch_bytes) return hipErrorInvalidValue;
-  const size_t nx = (size_t)M * w.cols;
-  uint16_t* xt = static_cast<uint16_t*>(scratch);
-  hipLaunchKernelGGL(k_split_bf16, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, s, x, xt, nx);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int steps = w.cols / kGK;
+  if (M < 1 || !matmul_prefill_supported(w) || gemm_scratch_bytes(w, M) > scratch_bytes)
+    return hipErrorInvalidValue;
+  const int Kp = padded_k(w.cols);
+  const int steps = Kp / kGK;
   const int per = gemm_steps_per_split(w, M);
   const int splits = (steps + per - 1) / per;
-  float* part = reinterpret_cast<float*>(static_cast<char*>(scratch) + ((nx * kTerms * sizeof(uint16_t) + 255) & ~(size_t)255));
+  char* p = static_cast<char*>(scratch);
+  const size_t digit_bytes = round256((size_t)kDigits * M * Kp);
+  int8_t* digits = reinterpret_cast<int8_t*>(p);
+  double* row_factor = reinterpret_cast<double*>(p + digit_bytes);
+  float* part = reinterpret_cast<float*>(p + digit_bytes + round256((size_t)M * sizeof(double)));
+  hipLaunchKernelGGL(k_digits, dim3(M), dim3(kBlock), 0, s, x, M, w.cols, Kp, digits, row_factor);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   GemmArgs a{};
   a.w = w;
-  a.xt = xt;
+  a.digits = digits;
+  a.row_factor = row_factor;
   a.out = splits > 1 ? part : y;
   a.bias = splits > 1 ? nullptr : bias;
   a.M = M;
   a.N = w.rows;
   a.K = w.cols;
+  a.Kp = Kp;
   a.steps_per_split = per;
   const dim3 grid((w.rows + kGN - 1) / kGN, (M + kGM - 1) / kGM, splits);
-  if (w.format == QH_FMT_INT8) hipLaunchKernelGGL(k_gemm<QH_FMT_INT8>, grid, dim3(kBlock), 0, s, a);
-  else hipLaunchKernelGGL(k_gemm<QH_FMT_INT4>, grid, dim3(kBlock), 0, s, a);
-  if ((e = hipGetLastError()) != hipSuccess || splits == 1) return e;
+  if (w.format == QH_FMT_INT8) hipLaunchKernelGGL(k_gemm<QH_FMT_INT8>, grid, dim3(kGemmThreads), 0, s, a);
+  else hipLaunchKernelGGL(k_gemm<QH_FMT_INT4>, grid, dim3(kGemmThreads), 0, s, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
   const size_t total = (size_t)M * w.rows;
   hipLaunchKernelGGL(k_gemm_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, splits,
                      bias, y, M, w.rows);

@@ -96,6 +96,7 @@ bool matvec_f32_supported(const DMat& m);
 hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias, float* y,
                                  int M, void* scratch, size_t scratch_bytes);
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M);
+bool matmul_prefill_supported(const DMat& w);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
 // f32: the fast numerics' f32 rmsnorm (needs cols % 4 == 0, cols <= 8192 and 16-byte

@@ -149,7 +149,7 @@ def test_batched_matvec_equals_single_position_bitwise(ctx, hip, fmt, seq):
     free(wb, dX, db, dY, dy)
 
 
-MFMA_REL = KERNEL_REL   # bf16 MFMA over exact codes and an exact three-term bf16 split of x, f32 sums
+MFMA_REL = KERNEL_REL   # int8 MFMA: exact codes, x in 24-bit fixed point per row, exact int32 sums
 
 
 @pytest.mark.parametrize("fmt", ["int8", "int4"])
