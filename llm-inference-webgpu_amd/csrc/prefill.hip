@@ -6,7 +6,9 @@
 //
 // Arithmetic: integers on v_mfma_i32_16x16x64_i8. A weight code is already a small
 // integer: int8 q in [-127, 127], int4 (level - zero) in [-15, 15]. Each activation
-// row is made one too, once per call (k_digits): with s = max|x_row| / 127, every x
+// row is made one too, once per contraction by the row kernel that produces it (k_rows:
+// the previous contraction's split sum, residual add, rmsnorm or swiglu, then the
+// digits): with s = max|x_row| / 127, every x
 // becomes the fixed-point integer X = rint(x * 2^16 / s), |X| <= 127 * 2^16, an
 // absolute error of at most s * 2^-17 = max|x_row| * 2^-17 / 127 (the row's largest
 // value keeps 24 significant bits, as in f32), stored as three balanced base-256
@@ -49,45 +51,120 @@ __host__ __device__ inline int padded_k(int K) { return (K + kGK - 1) / kGK * kG
 // The larger magnitude, NaN kept once met.
 __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v != v) ? v : p; }
 
-// One block per row of X [M][K]: digits [kDigits][M][Kp] (int8) and the row factor
-// s * 2^-16 (f64; 0 for an all-zero row, whose digits are all zero).
-__global__ __launch_bounds__(kBlock) void k_digits(const float* __restrict__ x, int M, int K, int Kp,
-                                                   int8_t* __restrict__ digits, double* __restrict__ row_factor) {
+// One row kernel in front of every contraction (one block per row m, rows of n <= 8192
+// values): the row is the sum of `splits` partial rows (+ bias) -- a previous contraction's
+// split-K output, summed in the order k_gemm_finish sums it -- or, for ROW_SWIGLU,
+// silu(g) * u of such a row of interleaved gate|up pairs; optionally added into the
+// residual stream `resid` (f32, as the batched path's add); for ROW_RMSNORM normalized
+// as the f32 rmsnorm does; and, when `digits` is set, written as the digit planes of the
+// next contraction: s = max|y| / 127, X = rint(y * 2^16 / s) in three balanced base-256
+// digits [kDigits][M][Kp], zeros past n, and the row factor s * 2^-16 (NaN for a row
+// holding an infinity or a NaN, whose digits are zero).
+template <int OP>
+__global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   __shared__ float red[kBlock / kWave];
-  const int m = blockIdx.x;
-  const float* row = x + (size_t)m * K;
+  constexpr int kMaxVec = 8;  // float4 per thread: 8192 values
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const int n4 = a.n / 4;
+  const int in_len = OP == ROW_SWIGLU ? 2 * a.n : a.n;
+  const size_t plane_in = (size_t)a.M * in_len;
+  const float* in_row = a.in + (size_t)m * in_len;
+  v4f v[kMaxVec];
+#pragma unroll
+  for (int j = 0; j < kMaxVec; j++) {
+    const int i4 = tid + j * kBlock;
+    v[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (i4 >= n4) continue;
+    if constexpr (OP == ROW_SWIGLU) {
+      v4f g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0;
+      for (int sp = 0; sp < a.splits; sp++) {
+        g0 += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 8 * i4);
+        g1 += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 8 * i4 + 4);
+      }
+      if (a.bias) {
+        g0 += *reinterpret_cast<const v4f*>(a.bias + 8 * i4);
+        g1 += *reinterpret_cast<const v4f*>(a.bias + 8 * i4 + 4);
+      }
+      v[j] = v4f{swiglu_f32(g0[0], g0[1]), swiglu_f32(g0[2], g0[3]), swiglu_f32(g1[0], g1[1]),
+                 swiglu_f32(g1[2], g1[3])};
+    } else {
+      v4f x = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < a.splits; sp++) x += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 4 * i4);
+      if (a.bias) x += *reinterpret_cast<const v4f*>(a.bias + 4 * i4);
+      v[j] = x;
+    }
+    if (a.resid) {
+      v4f* r = reinterpret_cast<v4f*>(a.resid + (size_t)m * a.n + 4 * i4);
+      v[j] = *r + v[j];
+      *r = v[j];
+    }
+  }
+  if constexpr (OP == ROW_RMSNORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxVec; j++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) ss = fmaf(v[j][e], v[j][e], ss);
+    ss = block_sum_f32(ss, red);
+    const float scale = __builtin_amdgcn_rsqf(ss / (float)a.n + a.eps);
+    __syncthreads();  // red is reused below
+#pragma unroll
+    for (int j = 0; j < kMaxVec; j++) {
+      const int i4 = tid + j * kBlock;
+      if (i4 < n4) v[j] = rms_apply_f32(v[j], scale, *reinterpret_cast<const v4f*>(a.gain + 4 * i4));
+    }
+  }
+  if (!a.digits) return;
   float peak = 0.f;
-  for (int k = threadIdx.x; k < K; k += kBlock) peak = peak_of(peak, fabsf(row[k]));
+#pragma unroll
+  for (int j = 0; j < kMaxVec; j++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) peak = peak_of(peak, fabsf(v[j][e]));
   for (int off = kWave / 2; off > 0; off >>= 1) peak = peak_of(peak, __shfl_xor(peak, off));
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = peak;
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = peak;
   __syncthreads();
   peak = 0.f;
 #pragma unroll
   for (int w = 0; w < kBlock / kWave; w++) peak = peak_of(peak, red[w]);
-  // A row holding an infinity or a NaN has no fixed-point form: its digits are zero and its
-  // factor NaN, so its outputs are NaN.
   const bool finite = peak <= 3.402823466e38f;
   const double s = (double)peak / 127.0;
   const double inv = finite && peak > 0.f ? 65536.0 / s : 0.0;
-  if (threadIdx.x == 0) row_factor[m] = finite ? s / 65536.0 : (double)NAN;
-  const size_t plane = (size_t)M * Kp;
-  for (int k4 = 4 * threadIdx.x; k4 < Kp; k4 += 4 * kBlock) {
+  if (tid == 0) a.row_factor[m] = finite ? s / 65536.0 : (double)NAN;
+  const size_t plane = (size_t)a.M * a.Kp;
+  int8_t* drow = a.digits + (size_t)m * a.Kp;
+  for (int j = 0; 4 * (tid + j * kBlock) < a.Kp; j++) {
+    const int i4 = tid + j * kBlock;
     uint32_t w[kDigits] = {0, 0, 0};
+    if (i4 < n4 && inv != 0.0) {
+      v4f x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int k = k4 + e;
-      int v = k < K && inv != 0.0 ? (int)rint((double)row[k] * inv) : 0;  // |v| <= 127 * 2^16
+      for (int jj = 0; jj < kMaxVec; jj++)
+        if (jj == j) x = v[jj];
 #pragma unroll
-      for (int d = 0; d < kDigits; d++) {
-        const int dig = (int)(int8_t)(uint8_t)(v & 0xff);  // balanced: [-128, 127]
-        w[d] |= (uint32_t)(uint8_t)dig << (8 * e);
-        v = (v - dig) >> 8;
+      for (int e = 0; e < 4; e++) {
+        int q = (int)rint((double)x[e] * inv);  // |q| <= 127 * 2^16
+#pragma unroll
+        for (int d = 0; d < kDigits; d++) {
+          const int dig = (int)(int8_t)(uint8_t)(q & 0xff);  // balanced: [-128, 127]
+          w[d] |= (uint32_t)(uint8_t)dig << (8 * e);
+          q = (q - dig) >> 8;
+        }
       }
     }
 #pragma unroll
-    for (int d = 0; d < kDigits; d++)
-      *reinterpret_cast<uint32_t*>(digits + d * plane + (size_t)m * Kp + k4) = w[d];
+    for (int d = 0; d < kDigits; d++) *reinterpret_cast<uint32_t*>(drow + d * plane + 4 * i4) = w[d];
   }
+}
+
+hipError_t launch_rows(hipStream_t s, int op, const RowArgs& a) {
+  if (a.n % 4 || a.n > 8192 || (a.digits && a.Kp != padded_k(a.n))) return hipErrorInvalidValue;
+  switch (op) {
+    case ROW_PLAIN: hipLaunchKernelGGL(k_rows<ROW_PLAIN>, dim3(a.M), dim3(kBlock), 0, s, a); break;
+    case ROW_RMSNORM: hipLaunchKernelGGL(k_rows<ROW_RMSNORM>, dim3(a.M), dim3(kBlock), 0, s, a); break;
+    case ROW_SWIGLU: hipLaunchKernelGGL(k_rows<ROW_SWIGLU>, dim3(a.M), dim3(kBlock), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ weight tile --
@@ -300,44 +377,35 @@ static int gemm_steps_per_split(const DMat& w, int M) {
   return per;
 }
 
-static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
-
-// Scratch of one launch over exactly M rows: the digit planes, the row factors, and the
-// split partials.
-static size_t gemm_scratch_bytes(const DMat& w, int M) {
-  const int Kp = padded_k(w.cols);
-  const int steps = Kp / kGK;
+static int gemm_splits(const DMat& w, int M) {
+  const int steps = padded_k(w.cols) / kGK;
   const int per = gemm_steps_per_split(w, M);
-  const int splits = (steps + per - 1) / per;
-  const size_t part = splits > 1 ? (size_t)splits * M * w.rows * sizeof(float) : 0;
-  return round256((size_t)kDigits * M * Kp) + round256((size_t)M * sizeof(double)) + part;
+  return (steps + per - 1) / per;
 }
 
-// Scratch for every launch of 1..M rows. Not the M-row figure alone: below a 64-row tile
-// boundary there are fewer tiles and so more splits, and the partials of a smaller M can
-// outgrow M's own.
-size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
+static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+size_t digits_bytes(int M, int K) { return round256((size_t)kDigits * M * padded_k(K)); }
+int digits_width(int K) { return padded_k(K); }
+
+// Split partials of every launch of 1..M rows. Not the M-row figure alone: below a 64-row
+// tile boundary there are fewer tiles and so more splits, and the partials of a smaller M
+// can outgrow M's own.
+size_t gemm_partials_bytes(const DMat& w, int M) {
   size_t most = 0;
-  for (int m = 1; m <= M; m++) most = std::max(most, gemm_scratch_bytes(w, m));
+  for (int m = 1; m <= M; m++) {
+    const int splits = gemm_splits(w, m);
+    if (splits > 1) most = std::max(most, (size_t)splits * m * w.rows * sizeof(float));
+  }
   return most;
 }
 
-hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias,
-                                 float* y, int M, void* scratch, size_t scratch_bytes) {
-  if (M < 1 || !matmul_prefill_supported(w) || gemm_scratch_bytes(w, M) > scratch_bytes)
-    return hipErrorInvalidValue;
+hipError_t launch_gemm_digits(hipStream_t s, const DMat& w, const int8_t* digits, const double* row_factor, int M,
+                              const float* bias, float* y, float* part, size_t part_bytes, int* splits_out) {
+  if (M < 1 || !matmul_prefill_supported(w)) return hipErrorInvalidValue;
   const int Kp = padded_k(w.cols);
-  const int steps = Kp / kGK;
-  const int per = gemm_steps_per_split(w, M);
-  const int splits = (steps + per - 1) / per;
-  char* p = static_cast<char*>(scratch);
-  const size_t digit_bytes = round256((size_t)kDigits * M * Kp);
-  int8_t* digits = reinterpret_cast<int8_t*>(p);
-  double* row_factor = reinterpret_cast<double*>(p + digit_bytes);
-  float* part = reinterpret_cast<float*>(p + digit_bytes + round256((size_t)M * sizeof(double)));
-  hipLaunchKernelGGL(k_digits, dim3(M), dim3(kBlock), 0, s, x, M, w.cols, Kp, digits, row_factor);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  const int splits = gemm_splits(w, M);
+  if (splits > 1 && (size_t)splits * M * w.rows * sizeof(float) > part_bytes) return hipErrorInvalidValue;
   GemmArgs a{};
   a.w = w;
   a.digits = digits;
@@ -348,11 +416,38 @@ hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, c
   a.N = w.rows;
   a.K = w.cols;
   a.Kp = Kp;
-  a.steps_per_split = per;
+  a.steps_per_split = gemm_steps_per_split(w, M);
   const dim3 grid((w.rows + kGN - 1) / kGN, (M + kGM - 1) / kGM, splits);
   if (w.format == QH_FMT_INT8) hipLaunchKernelGGL(k_gemm<QH_FMT_INT8>, grid, dim3(kGemmThreads), 0, s, a);
   else hipLaunchKernelGGL(k_gemm<QH_FMT_INT4>, grid, dim3(kGemmThreads), 0, s, a);
-  e = hipGetLastError();
+  *splits_out = splits;
+  return hipGetLastError();
+}
+
+// The whole standalone contraction: the row kernel's digits of x, the GEMM, the split sum.
+size_t matmul_prefill_scratch_bytes(const DMat& w, int M) {
+  return digits_bytes(M, w.cols) + round256((size_t)M * sizeof(double)) + gemm_partials_bytes(w, M);
+}
+
+hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, const float* bias,
+                                 float* y, int M, void* scratch, size_t scratch_bytes) {
+  if (M < 1 || !matmul_prefill_supported(w) || w.cols > 8192 || matmul_prefill_scratch_bytes(w, M) > scratch_bytes)
+    return hipErrorInvalidValue;
+  char* p = static_cast<char*>(scratch);
+  const size_t db = digits_bytes(M, w.cols), rb = round256((size_t)M * sizeof(double));
+  RowArgs r{};
+  r.in = x;
+  r.splits = 1;
+  r.M = M;
+  r.n = w.cols;
+  r.Kp = padded_k(w.cols);
+  r.digits = reinterpret_cast<int8_t*>(p);
+  r.row_factor = reinterpret_cast<double*>(p + db);
+  hipError_t e = launch_rows(s, ROW_PLAIN, r);
+  if (e != hipSuccess) return e;
+  float* part = reinterpret_cast<float*>(p + db + rb);
+  int splits = 1;
+  e = launch_gemm_digits(s, w, r.digits, r.row_factor, M, bias, y, part, scratch_bytes - db - rb, &splits);
   if (e != hipSuccess || splits == 1) return e;
   const size_t total = (size_t)M * w.rows;
   hipLaunchKernelGGL(k_gemm_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, splits,

@@ -97,6 +97,33 @@ hipError_t launch_matmul_prefill(hipStream_t s, const DMat& w, const float* x, c
                                  int M, void* scratch, size_t scratch_bytes);
 size_t matmul_prefill_scratch_bytes(const DMat& w, int M);
 bool matmul_prefill_supported(const DMat& w);
+// The pieces of that contraction, for callers that fuse its input and output rows.
+// Row kernel: row m = sum of `splits` partial rows [splits][M][in_len] (+ bias); for
+// ROW_SWIGLU silu(g)*u of interleaved gate|up pairs (in_len = 2n), else in_len = n; added
+// into `resid` [M][n] when set; ROW_RMSNORM then normalizes it (f32, `gain`, `eps`); when
+// `digits` is set it is written as the contraction's input: digit planes
+// [3][M][Kp = digits_width(n)] and row factors [M] (f64). n % 4 == 0, n <= 8192.
+enum { ROW_PLAIN = 0, ROW_RMSNORM = 1, ROW_SWIGLU = 2 };
+struct RowArgs {
+  const float* in;
+  int splits;
+  const float* bias;
+  float* resid;
+  const float* gain;
+  float eps;
+  int M, n, Kp;
+  int8_t* digits;
+  double* row_factor;
+};
+hipError_t launch_rows(hipStream_t s, int op, const RowArgs& a);
+size_t digits_bytes(int M, int K);
+int digits_width(int K);
+// y [M][N] = W x (+ bias) from digit planes; when the launch splits K, `part` receives the
+// splits' partial rows [splits][M][N] without the bias and *splits_out says how many
+// (gemm_partials_bytes(w, M) bytes cover every M up to the argument).
+hipError_t launch_gemm_digits(hipStream_t s, const DMat& w, const int8_t* digits, const double* row_factor, int M,
+                              const float* bias, float* y, float* part, size_t part_bytes, int* splits_out);
+size_t gemm_partials_bytes(const DMat& w, int M);
 hipError_t launch_matvec_xh_list(hipStream_t s, const DMat& m, int count, size_t data_stride,
                                  size_t scale_stride, const uint16_t* x, size_t x_stride, float* y);
 // f32: the fast numerics' f32 rmsnorm (needs cols % 4 == 0, cols <= 8192 and 16-byte
