@@ -29,6 +29,7 @@
 // Long K is split over gridDim.z; partial tiles are summed in a fixed order by
 // k_gemm_finish.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.h"
 
@@ -264,63 +265,72 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
 
   v4i xa[kStages][kDigits];
   WRaw<FMT> wr[kStages];
+  // Loads are unconditional, so the register sets rotate in place and no wait covers more
+  // than the step being consumed: a step past the split's last re-reads that last one
+  // (never used), and waves past M read the clamped row.
   auto issue = [&](int st, v4i (&x)[kDigits], WRaw<FMT>& w) {
-    const int k = st * kGK;
-    if (active) {
+    const int k = min(st, s1 - 1) * kGK;
 #pragma unroll
-      for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + d * plane + k);
-    }
+    for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + d * plane + k);
     wraw_load<FMT>(a.w, brow, k + bk, a.K, w);
   };
 #pragma unroll
-  for (int u = 0; u < kStages; u++)
-    if (s0 + u < s1) issue(s0 + u, xa[u], wr[u]);
-  for (int base = s0; base < s1; base += kStages) {
+  for (int u = 0; u < kStages; u++) issue(s0 + u, xa[u], wr[u]);
+  // One K step from register set U; the loop below runs whole groups of kStages steps (no
+  // exit inside a group, so every set is reloaded in place) and then the remainder.
+  auto step = [&](auto U, int st) {
+    constexpr int u = decltype(U)::value;
+    const int buf = (st - s0) & 1;
+    {
+      v4u wb[2];
+      wraw_bytes<FMT>(wr[u], wb);
+      *reinterpret_cast<v4u*>(&Bs[buf][br][bk]) = wb[0];
+      *reinterpret_cast<v4u*>(&Bs[buf][br][bk + 16]) = wb[1];
+    }
+    // One barrier per step: Bs[buf] is complete, and every wave has finished reading it
+    // two steps ago (each wave reads a buffer before it arrives at the next barrier).
+    __syncthreads();
+    if (active) {
+      v4i fb[kNT];
 #pragma unroll
-    for (int u = 0; u < kStages; u++) {
-      const int st = base + u;
-      if (st >= s1) break;  // uniform over the block
-      const int buf = (st - s0) & 1;
-      {
-        v4u wb[2];
-        wraw_bytes<FMT>(wr[u], wb);
-        *reinterpret_cast<v4u*>(&Bs[buf][br][bk]) = wb[0];
-        *reinterpret_cast<v4u*>(&Bs[buf][br][bk + 16]) = wb[1];
-      }
-      v4i xd[kDigits];
+      for (int j = 0; j < kNT; j++) fb[j] = *reinterpret_cast<const v4i*>(&Bs[buf][16 * j + fr][16 * fg]);
 #pragma unroll
-      for (int d = 0; d < kDigits; d++) xd[d] = xa[u][d];
-      if (st + kStages < s1) issue(st + kStages, xa[u], wr[u]);
-      // One barrier per step: Bs[buf] is complete, and every wave has finished reading it
-      // two steps ago (each wave reads a buffer before it arrives at the next barrier).
-      __syncthreads();
-      if (active) {
-        v4i fb[kNT];
+      for (int d = 0; d < kDigits; d++)
 #pragma unroll
-        for (int j = 0; j < kNT; j++) fb[j] = *reinterpret_cast<const v4i*>(&Bs[buf][16 * j + fr][16 * fg]);
+        for (int j = 0; j < kNT; j++)
+          acc[d][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u][d], fb[j], acc[d][j], 0, 0, 0);
+      if constexpr (FMT == QH_FMT_INT4) {
+        if ((st + 1) % group_steps == 0) {  // the group's exact sum, scaled into the total
+          const int g = st / group_steps;
 #pragma unroll
-        for (int d = 0; d < kDigits; d++)
+          for (int j = 0; j < kNT; j++) {
+            const double sg = a.w.scales[(size_t)min(n0 + 16 * j + fr, a.N - 1) * a.w.gpr + g];
 #pragma unroll
-          for (int j = 0; j < kNT; j++)
-            acc[d][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xd[d], fb[j], acc[d][j], 0, 0, 0);
-        if constexpr (FMT == QH_FMT_INT4) {
-          if ((st + 1) % group_steps == 0) {  // the group's exact sum, scaled into the total
-            const int g = st / group_steps;
+            for (int r = 0; r < 4; r++)
+              tot[j][r] += sg * ((double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 +
+                                 (double)acc[0][j][r]);
 #pragma unroll
-            for (int j = 0; j < kNT; j++) {
-              const double sg = a.w.scales[(size_t)min(n0 + 16 * j + fr, a.N - 1) * a.w.gpr + g];
-#pragma unroll
-              for (int r = 0; r < 4; r++)
-                tot[j][r] += sg * ((double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 +
-                                   (double)acc[0][j][r]);
-#pragma unroll
-              for (int d = 0; d < kDigits; d++) acc[d][j] = v4i{0, 0, 0, 0};
-            }
+            for (int d = 0; d < kDigits; d++) acc[d][j] = v4i{0, 0, 0, 0};
           }
         }
       }
     }
+    // The set's next loads, issued once its digits are in the MFMAs: they land in the same
+    // registers kStages steps ahead of their use.
+    issue(st + kStages, xa[u], wr[u]);
+  };
+  static_assert(kStages == 3, "the group below is written out for three register sets");
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  int st = s0;
+  for (; st + kStages <= s1; st += kStages) {
+    step(S0{}, st);
+    step(S1{}, st + 1);
+    step(S2{}, st + 2);
   }
+  if (st < s1) step(S0{}, st);
+  if (st + 1 < s1) step(S1{}, st + 1);
   if (!active) return;
 
   // D fragment: lane holds rows 4*fg .. +3 of column fr of each tile.
