@@ -586,17 +586,19 @@ static hipError_t launch_attn_slots(hipStream_t s, const SlotArgs& a, int seq, i
 
 // ------------------------------------------------ prefill on the matrix cores --
 // Causal GQA attention of `seq` queries (positions past .. past+seq-1) as a flash
-// attention on v_mfma_f32_16x16x32_f16: one wave per (query head, 16 queries), keys
-// in steps of 32 with an online softmax per query.
+// attention on v_mfma_f32_16x16x32_f16: one block per (query head, 16 queries), keys
+// in steps of 32 with an online softmax per query, the steps spread over the block's
+// waves and their states merged at the end.
 //
 // Transposed products keep every operand where it is loaded: S^T = K Q^T (A = 16 key
 // rows of the position-major cache, 16 bytes per lane; B = the wave's queries), then
 // O^T += V^T P^T (A = 16 dimension rows of the dimension-major value cache; B = P^T).
-// In the D layout lane l holds keys 4*(l/16)+r of query l%16, which is exactly what
-// the B operand of the second product needs for query l%16 once the contraction
-// index is ordered (keys 4g..4g+3 of the first 16-key tile, then the same of the
-// second) -- the value operand is read in that order -- so P never leaves its
-// registers, and the softmax state of a query lives in the four lanes that share it.
+// In the D layout lane l holds rows 4*(l/16)+r of query l%16; with the key rows of
+// the two 16-key tiles interleaved (KvStep below) those are keys 8*(l/16) .. +7 over
+// both tiles, exactly the B operand of the second product for query l%16 with the
+// contraction in key order -- the value operand is one 16-byte run of a dimension row
+// -- so P never leaves its registers, and the softmax state of a query lives in the
+// four lanes that share it.
 //
 // Precision: q (scaled by 1/8 log2 e) and p are each split into two f16 terms
 // whose sum is the f32 value to 2^-22, the f16 K/V are exact, products accumulate
@@ -636,182 +638,41 @@ __device__ __forceinline__ float f32_pinned(float x) {
 __device__ __forceinline__ _Float16 f16_hi_part(float x) { return (_Float16)x; }
 __device__ __forceinline__ _Float16 f16_lo_part(float x) { return (_Float16)(x - (float)(_Float16)x); }
 
-static __global__ __launch_bounds__(kWave) void k_flash_prefill(FlashArgs a) {
-  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y;
-  const int kvh = h / (a.heads / a.kv_heads);
-  const int t0 = blockIdx.x * kFlashQ;
-  const int tn = min(t0 + n, a.seq - 1);  // this lane's query; past the end, a copy of the last
-  const int qpos = a.past + tn;
-  const int kmax = a.past + min(t0 + kFlashQ - 1, a.seq - 1);  // the tile's last key
-
-  f16x8 qh[2], ql[2];  // B of S^T = K Q^T: query n, dims 32ks + 8g .. +7, times 1/8
-  const float* qr = a.q + ((size_t)tn * a.heads + h) * kHeadDim;
-#pragma unroll
-  for (int ks = 0; ks < 2; ks++) {
-    const v4f x0 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g);
-    const v4f x1 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g + 4);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const float a0 = f32_pinned(x0[e] * kScoreLog2), a1 = f32_pinned(x1[e] * kScoreLog2);
-      qh[ks][e] = f16_hi_part(a0);
-      ql[ks][e] = f16_lo_part(a0);
-      qh[ks][4 + e] = f16_hi_part(a1);
-      ql[ks][4 + e] = f16_lo_part(a1);
-    }
-  }
-  const uint16_t* kb = a.kc + (size_t)kvh * a.capacity * kHeadDim;
-  const uint16_t* vb = a.vt + (size_t)kvh * kHeadDim * a.vstride;
-  float m = -INFINITY, l = 0.f;
-  f32x4 o[4];  // O^T: dims 16dt + 4g + r of query n
-#pragma unroll
-  for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  for (int p0 = 0; p0 <= kmax; p0 += kFlashK) {
-    // Loads (in bounds: key rows clamped to the cache, value groups to the row).
-    f16x8 kf[2][2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const uint16_t* kr = kb + (size_t)min(p0 + 16 * j + n, a.capacity - 1) * kHeadDim;
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) kf[j][ks] = *reinterpret_cast<const f16x8*>(kr + 32 * ks + 8 * g);
-    }
-    uint32_t vv[4][4];  // dim 16dt + n: keys p0+4g .. +3 (vv[dt][0..1]), p0+16+4g .. +3 (vv[dt][2..3])
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) {
-      const uint16_t* vr = vb + (size_t)(16 * dt + n) * a.vstride;
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const uint2 w = *reinterpret_cast<const uint2*>(vr + min(p0 + 16 * j + 4 * g, a.vstride - 4));
-        vv[dt][2 * j] = w.x;
-        vv[dt][2 * j + 1] = w.y;
-      }
-    }
-    // S^T tiles: s[j][r] = score of key p0 + 16j + 4g + r for query n.
-    f32x4 s[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][ks], qh[ks], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[j][ks], ql[ks], acc, 0, 0, 0);
-      }
-      s[j] = acc;
-    }
-    // Online softmax for query n (causal mask by select: masked keys may hold any bits).
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        s[j][r] = p0 + 16 * j + 4 * g + r <= qpos ? s[j][r] : -INFINITY;
-        tmax = fmaxf(tmax, s[j][r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m, tmax);  // finite: key 0 is in every query's first step
-    const float alpha = m == -INFINITY ? 0.f : exp2_reduced(m - mn);  // 0 on the first step
-    float pv[2][4], psum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        pv[j][r] = s[j][r] == -INFINITY ? 0.f : exp2_reduced(s[j][r] - mn);
-        psum += pv[j][r];
-      }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
-    l = fmaf(l, alpha, psum);
-    m = mn;
-    f16x8 ph, pl;  // B of O^T += V^T P^T, contraction order: keys 4g..4g+3, then 16+4g..16+4g+3
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      ph[r] = f16_hi_part(pv[0][r]);
-      pl[r] = f16_lo_part(pv[0][r]);
-      ph[4 + r] = f16_hi_part(pv[1][r]);
-      pl[4 + r] = f16_lo_part(pv[1][r]);
-    }
-    if (p0 + kFlashK - 1 > kmax) {
-      // Keys past the tile's last were never written for it: their values must be zeros.
-#pragma unroll
-      for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-          const int k0 = p0 + 16 * (w >> 1) + 4 * g + 2 * (w & 1);  // keys of vv[dt][w]: k0, k0+1
-          const uint32_t keep = (k0 <= kmax ? 0x0000ffffu : 0u) | (k0 + 1 <= kmax ? 0xffff0000u : 0u);
-          vv[dt][w] &= keep;
-        }
-    }
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) {
-      f32x4 c = o[dt];
-#pragma unroll
-      for (int r = 0; r < 4; r++) c[r] *= alpha;
-      const f16x8 va = __builtin_bit_cast(f16x8, (v4u){vv[dt][0], vv[dt][1], vv[dt][2], vv[dt][3]});
-      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, c, 0, 0, 0);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, c, 0, 0, 0);
-    }
-  }
-  if (t0 + n < a.seq) {
-    float* dst = a.out + ((size_t)(t0 + n) * a.heads + h) * kHeadDim;
-#pragma unroll
-    for (int dt = 0; dt < 4; dt++) {
-      const v4f r = {o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
-      *reinterpret_cast<v4f*>(dst + 16 * dt + 4 * g) = r;
-    }
-  }
-}
-
-static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a) {
-  hipLaunchKernelGGL(k_flash_prefill, dim3((a.seq + kFlashQ - 1) / kFlashQ, a.heads), dim3(kWave), 0, s, a);
-  return hipGetLastError();
-}
-
-// ------------------------------------- one query, GQA group on the matrix cores --
-// The split-K slots of k_attn_slots for a single query, with a whole GQA group per
-// wave: the group's query heads are the columns of the MFMA products of the flash
-// kernel above (heads/kv_heads of the 16 used, the rest repeat head 0 and are
-// dropped), so each key/value position is read once for the group instead of once
-// per query head. A slot's chunks are walked in steps of 32 keys -- S^T for 2 tiles
-// of 16 keys (8 MFMAs), the online softmax per head column, O^T += V^T P^T (8
-// MFMAs) -- with the next step's loads issued before each step's arithmetic (two
-// 32-key buffers). Writes (m, l, o) slot partials in the layout of k_attn_slots, with
-// the maxima in base-2 units (merged by k_attn_combine<true>). q and p are split into
-// two f16 terms as in the flash kernel (~1e-6 of the output).
-struct GqaStep {
-  f16x8 k[2][2];     // keys 16j + n, dims 32ks + 8g .. +7
-  uint32_t v[4][4];  // dimension 16dt + n: keys 4g .. +3 (v[dt][0..1]), 16+4g .. +3 (v[dt][2..3])
+// One step of 32 keys (p0 .. p0+31) for 16 query columns, shared by the flash and the
+// GQA kernels: S^T = K Q^T over two 16-key tiles (8 MFMAs), the online softmax per
+// query column, O^T += V^T P^T (8 MFMAs). The loads of a step go into a KvStep so a
+// caller can issue the next step's loads before this step's arithmetic.
+//
+// Key order: row n of 16-key tile j holds key 8*(n/4) + 4j + n%4, so the score tile's D
+// layout gives lane (n, g) keys 8g + 4j + r, and the eight P values of the lane are keys
+// 8g .. 8g+7 in order -- the value operand of dimension 16dt + n is then one 16-byte
+// run of its row (the contraction order is the same permutation for both operands).
+struct KvStep {
+  f16x8 k[2][2];  // key 8*(n/4) + 4j + n%4, dims 32ks + 8g .. +7
+  v4u v[4];       // dimension 16dt + n: keys 8g .. 8g+7
 };
 
-// Step i of slot sl: 32 keys starting at p0 (chunk sl + (i/2)*MAXS, half i%2).
-template <int MAXS>
-__device__ __forceinline__ int gqa_p0(int sl, int i) {
-  return (sl + (i >> 1) * MAXS) * kChunk + (i & 1) * 32;
-}
+__device__ __forceinline__ int kv_key_row(int j, int n) { return 8 * (n >> 2) + 4 * j + (n & 3); }
 
-__device__ __forceinline__ void gqa_load(const uint16_t* kb, const uint16_t* vb, int p0, int capacity, int vstride,
-                                         int n, int g, GqaStep& d) {
+// In bounds for every p0 >= 0: key rows are clamped to the cache, value runs to the row.
+__device__ __forceinline__ void kv_load(const uint16_t* kb, const uint16_t* vb, int p0, int capacity, int vstride,
+                                        int n, int g, KvStep& d) {
 #pragma unroll
   for (int j = 0; j < 2; j++) {
-    const uint16_t* kr = kb + (size_t)min(p0 + 16 * j + n, capacity - 1) * kHeadDim;
+    const uint16_t* kr = kb + (size_t)min(p0 + kv_key_row(j, n), capacity - 1) * kHeadDim;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) d.k[j][ks] = *reinterpret_cast<const f16x8*>(kr + 32 * ks + 8 * g);
   }
 #pragma unroll
-  for (int dt = 0; dt < 4; dt++) {
-    const uint16_t* vr = vb + (size_t)(16 * dt + n) * vstride;
-#pragma unroll
-    for (int hf = 0; hf < 2; hf++) {
-      const uint2 w = *reinterpret_cast<const uint2*>(vr + min(p0 + 16 * hf + 4 * g, vstride - 4));
-      d.v[dt][2 * hf] = w.x;
-      d.v[dt][2 * hf + 1] = w.y;
-    }
-  }
+  for (int dt = 0; dt < 4; dt++)
+    d.v[dt] = *reinterpret_cast<const v4u*>(vb + (size_t)(16 * dt + n) * vstride + min(p0 + 8 * g, vstride - 8));
 }
 
-__device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)[2], GqaStep& d, int p0, int ctx,
-                                         int g, float& m, float& l, f32x4 (&o)[4]) {
+// Scores of keys >= slim (this lane's query column) are masked; values of keys >= vlim
+// (uniform: keys never written for this launch may hold any bits) become zeros. A query
+// column whose keys are all masked so far keeps m = -inf, l = 0 and o = 0 exactly.
+__device__ __forceinline__ void kv_step(const f16x8 (&qh)[2], const f16x8 (&ql)[2], KvStep& d, int p0, int slim,
+                                        int vlim, int g, float& m, float& l, f32x4 (&o)[4]) {
   f32x4 s[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
@@ -828,13 +689,13 @@ __device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)
   for (int j = 0; j < 2; j++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      s[j][r] = p0 + 16 * j + 4 * g + r < ctx ? s[j][r] : -INFINITY;
+      s[j][r] = p0 + 8 * g + 4 * j + r < slim ? s[j][r] : -INFINITY;
       tmax = fmaxf(tmax, s[j][r]);
     }
   tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-  const float mn = fmaxf(m, tmax);  // finite: every step a slot sums holds position p0 < ctx
-  const float alpha = m == -INFINITY ? 0.f : exp2_reduced(m - mn);
+  const float mn = fmaxf(m, tmax);
+  const float alpha = m == -INFINITY ? 0.f : exp2_reduced(m - mn);  // m finite: mn finite too
   float pv[2][4], psum = 0.f;
 #pragma unroll
   for (int j = 0; j < 2; j++)
@@ -847,7 +708,7 @@ __device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)
   psum += __shfl_xor(psum, 32);
   l = fmaf(l, alpha, psum);
   m = mn;
-  f16x8 ph, pl;  // contraction order: keys 4g .. 4g+3, then 16+4g .. 16+4g+3
+  f16x8 ph, pl;  // contraction order: keys 8g .. 8g+7
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     ph[r] = f16_hi_part(pv[0][r]);
@@ -855,14 +716,13 @@ __device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)
     ph[4 + r] = f16_hi_part(pv[1][r]);
     pl[4 + r] = f16_lo_part(pv[1][r]);
   }
-  if (p0 + 32 > ctx) {
-    // positions past the context may hold any bits: their values become zeros
+  if (p0 + 32 > vlim) {
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
       for (int w = 0; w < 4; w++) {
-        const int k0 = p0 + 16 * (w >> 1) + 4 * g + 2 * (w & 1);
-        d.v[dt][w] &= (k0 < ctx ? 0x0000ffffu : 0u) | (k0 + 1 < ctx ? 0xffff0000u : 0u);
+        const int k0 = p0 + 8 * g + 2 * w;  // keys of d.v[dt][w]: k0, k0+1
+        d.v[dt][w] &= (k0 < vlim ? 0x0000ffffu : 0u) | (k0 + 1 < vlim ? 0xffff0000u : 0u);
       }
   }
 #pragma unroll
@@ -870,22 +730,15 @@ __device__ __forceinline__ void gqa_step(const f16x8 (&qh)[2], const f16x8 (&ql)
     f32x4 c = o[dt];
 #pragma unroll
     for (int r = 0; r < 4; r++) c[r] *= alpha;
-    const f16x8 va = __builtin_bit_cast(f16x8, (v4u){d.v[dt][0], d.v[dt][1], d.v[dt][2], d.v[dt][3]});
+    const f16x8 va = __builtin_bit_cast(f16x8, d.v[dt]);
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, c, 0, 0, 0);
     o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, c, 0, 0, 0);
   }
 }
 
-// grid (kv_heads * MAXS, 1, list entries); SlotArgs as for k_attn_slots (one query).
-template <int MAXS>
-static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
-  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
-  const int group = a.heads / a.kv_heads;
-  const int kvh = blockIdx.x / MAXS, sl = blockIdx.x % MAXS;
-  const size_t z = blockIdx.z;
-  const int h = kvh * group + (n < group ? n : 0);
-  f16x8 qh[2], ql[2];
-  const float* qr = a.q + (size_t)h * kHeadDim;
+// q split into hi + lo f16 terms, scaled to base-2 score units: B of S^T = K Q^T for
+// query column n, dims 32ks + 8g .. +7 (qr: the query's 64 floats).
+__device__ __forceinline__ void load_query_split(const float* qr, int g, f16x8 (&qh)[2], f16x8 (&ql)[2]) {
 #pragma unroll
   for (int ks = 0; ks < 2; ks++) {
     const v4f x0 = *reinterpret_cast<const v4f*>(qr + 32 * ks + 8 * g);
@@ -899,10 +752,128 @@ static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
       ql[ks][4 + e] = f16_lo_part(a1);
     }
   }
+}
+
+// A (query head, 16 queries) tile is one block of kFlashWaves waves: key step i (keys
+// 32i .. 32i+31, up to the tile's last key) goes to wave i % kFlashWaves, which walks its
+// steps with the next one's loads in flight (two KvStep buffers); the waves' (m, l, o)
+// states then merge through LDS in wave order. Step i lands on the same wave whatever
+// the tile, and a key a query does not see adds exact zeros, so a query's output does
+// not depend on the other queries of its tile.
+constexpr int kFlashWaves = 4;
+
+static __global__ __launch_bounds__(kWave * kFlashWaves) void k_flash_prefill(FlashArgs a) {
+  __shared__ v4f sh_o[kFlashWaves][4][kWave];
+  __shared__ float sh_m[kFlashWaves][kFlashQ], sh_l[kFlashWaves][kFlashQ];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, n = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y;
+  const int kvh = h / (a.heads / a.kv_heads);
+  const int t0 = blockIdx.x * kFlashQ;
+  const int tn = min(t0 + n, a.seq - 1);  // this lane's query; past the end, a copy of the last
+  const int qpos = a.past + tn;
+  const int kmax = a.past + min(t0 + kFlashQ - 1, a.seq - 1);  // the tile's last key
+
+  f16x8 qh[2], ql[2];
+  load_query_split(a.q + ((size_t)tn * a.heads + h) * kHeadDim, g, qh, ql);
+  const uint16_t* kb = a.kc + (size_t)kvh * a.capacity * kHeadDim;
+  const uint16_t* vb = a.vt + (size_t)kvh * kHeadDim * a.vstride;
+  float m = -INFINITY, l = 0.f;
+  f32x4 o[4];  // O^T: dims 16dt + 4g + r of query n
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  constexpr int kStride = kFlashWaves * kFlashK;
+  const int steps = kmax / kFlashK + 1;
+  int left = (steps - w + kFlashWaves - 1) / kFlashWaves;  // steps w, w + kFlashWaves, ...
+  int p0 = w * kFlashK;
+  KvStep A, B;
+  kv_load(kb, vb, p0, a.capacity, a.vstride, n, g, A);
+  while (left > 0) {
+    if (left == 1) {
+      kv_step(qh, ql, A, p0, qpos + 1, kmax + 1, g, m, l, o);
+      break;
+    }
+    kv_load(kb, vb, p0 + kStride, a.capacity, a.vstride, n, g, B);
+    __builtin_amdgcn_sched_barrier(0);  // the next step's loads before this step's arithmetic
+    kv_step(qh, ql, A, p0, qpos + 1, kmax + 1, g, m, l, o);
+    p0 += kStride;
+    if (--left == 1) {
+      kv_step(qh, ql, B, p0, qpos + 1, kmax + 1, g, m, l, o);
+      break;
+    }
+    kv_load(kb, vb, p0 + kStride, a.capacity, a.vstride, n, g, A);
+    __builtin_amdgcn_sched_barrier(0);
+    kv_step(qh, ql, B, p0, qpos + 1, kmax + 1, g, m, l, o);
+    p0 += kStride;
+    --left;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) sh_o[w][dt][lane] = (v4f)o[dt];
+  if (g == 0) {
+    sh_m[w][n] = m;
+    sh_l[w][n] = l;
+  }
+  __syncthreads();
+  // Merge: wave dt writes dims 16dt + 4g .. +3 of query n (wave 0 always holds key 0).
+  for (int dt = w; dt < 4; dt += kFlashWaves) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < kFlashWaves; v++) mx = fmaxf(mx, sh_m[v][n]);
+    float lt = 0.f;
+    v4f ot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < kFlashWaves; v++) {
+      const float mv = sh_m[v][n];
+      const float wt = mv == -INFINITY ? 0.f : exp2_reduced(mv - mx);
+      lt = fmaf(sh_l[v][n], wt, lt);
+      const v4f ov = sh_o[v][dt][lane];
+#pragma unroll
+      for (int r = 0; r < 4; r++) ot[r] = fmaf(ov[r], wt, ot[r]);
+    }
+    if (t0 + n < a.seq) {
+      const v4f r = {ot[0] / lt, ot[1] / lt, ot[2] / lt, ot[3] / lt};
+      *reinterpret_cast<v4f*>(a.out + ((size_t)(t0 + n) * a.heads + h) * kHeadDim + 16 * dt + 4 * g) = r;
+    }
+  }
+}
+
+static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a) {
+  hipLaunchKernelGGL(k_flash_prefill, dim3((a.seq + kFlashQ - 1) / kFlashQ, a.heads), dim3(kWave * kFlashWaves), 0,
+                     s, a);
+  return hipGetLastError();
+}
+
+// ------------------------------------- one query, GQA group on the matrix cores --
+// The split-K slots of k_attn_slots for a single query, with a whole GQA group per
+// wave: the group's query heads are the columns of the MFMA products of the flash
+// kernel above (heads/kv_heads of the 16 used, the rest repeat head 0 and are
+// dropped), so each key/value position is read once for the group instead of once
+// per query head. A slot's chunks are walked in steps of 32 keys -- S^T for 2 tiles
+// of 16 keys (8 MFMAs), the online softmax per head column, O^T += V^T P^T (8
+// MFMAs) -- with the next step's loads issued before each step's arithmetic (two
+// 32-key buffers). Writes (m, l, o) slot partials in the layout of k_attn_slots, with
+// the maxima in base-2 units (merged by k_attn_combine<true>). q and p are split into
+// two f16 terms as in the flash kernel (~1e-6 of the output).
+// Step i of slot sl: 32 keys starting at p0 (chunk sl + (i/2)*MAXS, half i%2).
+template <int MAXS>
+__device__ __forceinline__ int gqa_p0(int sl, int i) {
+  return (sl + (i >> 1) * MAXS) * kChunk + (i & 1) * 32;
+}
+
+// grid (kv_heads * MAXS, 1, list entries); SlotArgs as for k_attn_slots (one query).
+template <int MAXS>
+static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
+  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  const int group = a.heads / a.kv_heads;
+  const int kvh = blockIdx.x / MAXS, sl = blockIdx.x % MAXS;
+  const size_t z = blockIdx.z;
+  const int h = kvh * group + (n < group ? n : 0);
+  f16x8 qh[2], ql[2];
+  load_query_split(a.q + (size_t)h * kHeadDim, g, qh, ql);
   const uint16_t* kb = a.kc + z * a.list_k + (size_t)kvh * a.capacity * kHeadDim;
   const uint16_t* vb = a.vt + z * a.list_v + (size_t)kvh * kHeadDim * a.vstride;
-  GqaStep A, B;
-  gqa_load(kb, vb, gqa_p0<MAXS>(sl, 0), a.capacity, a.vstride, n, g, A);  // in bounds whatever the position
+  KvStep A, B;
+  kv_load(kb, vb, gqa_p0<MAXS>(sl, 0), a.capacity, a.vstride, n, g, A);  // in bounds whatever the position
   const int pos = a.d_pos ? *a.d_pos : a.past;
   if (pos >= a.capacity) return;  // the host keeps positions inside the cache
   const int ctx = pos + 1, nch = attn_chunks(ctx);
@@ -920,20 +891,20 @@ static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
   int i = 0;
   while (left > 0) {
     if (left == 1) {
-      gqa_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+      kv_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
       break;
     }
-    gqa_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, B);
+    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, B);
     __builtin_amdgcn_sched_barrier(0);  // the next step's loads before this step's arithmetic
-    gqa_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+    kv_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
     ++i;
     if (--left == 1) {
-      gqa_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+      kv_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
       break;
     }
-    gqa_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, A);
+    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, A);
     __builtin_amdgcn_sched_barrier(0);
-    gqa_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, g, m, l, o);
+    kv_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
     ++i;
     --left;
   }
