@@ -30,6 +30,7 @@
 // k_gemm_finish.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "device_common.h"
 
@@ -176,21 +177,22 @@ struct WRaw {
   int zero;  // int4: the group's zero point
 };
 
+// Past K (the second half of a last 64-column step) the thread loads columns K - 32 ..
+// K - 1 again: the digit planes are zeros there, so those codes add nothing. Every thread
+// loads, with nothing done to the registers until their step: a branch around the loads,
+// or a select right after them, would make the waits before each step cover the loads
+// of the steps prefetched behind it as well.
 template <int FMT>
 __device__ __forceinline__ void wraw_load(const DMat& w, int n, int k, int K, WRaw<FMT>& r) {
-  if (k >= K) {  // past K (a half step): zero codes
-    r.q[0] = r.q[1] = v4u{0, 0, 0, 0};
-    r.zero = 0;
-    return;
-  }
+  const int kk = min(k, K - 32);
   const uint8_t* row = w.data + (size_t)n * w.row_bytes;
   if constexpr (FMT == QH_FMT_INT8) {
-    r.q[0] = *reinterpret_cast<const v4u*>(row + k);
-    r.q[1] = *reinterpret_cast<const v4u*>(row + k + 16);
+    r.q[0] = *reinterpret_cast<const v4u*>(row + kk);
+    r.q[1] = *reinterpret_cast<const v4u*>(row + kk + 16);
   } else {
-    r.q[0] = *reinterpret_cast<const v4u*>(row + k / 2);
+    r.q[0] = *reinterpret_cast<const v4u*>(row + kk / 2);
     // an integer in [0, 15] (src/core/quantize.js:115)
-    r.zero = (int)w.zeros[(size_t)n * w.gpr + k / (w.cpg * 32)];
+    r.zero = (int)w.zeros[(size_t)n * w.gpr + kk / (w.cpg * 32)];
   }
 }
 
@@ -231,6 +233,13 @@ struct GemmArgs {
   int M, N, K, Kp;
   int steps_per_split;       // K steps (of 64) per gridDim.z slice
 };
+
+// Steps st + U of a group, each from register set U (a compile-time index, so the sets
+// stay in registers), up to step s1.
+template <typename F, int... U>
+__device__ __forceinline__ void step_group(F& step, int st, int s1, std::integer_sequence<int, U...>) {
+  ((st + U < s1 ? (step(std::integral_constant<int, U>{}, st + U), 0) : 0), ...);
+}
 
 template <int FMT>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
@@ -319,18 +328,9 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
     // registers kStages steps ahead of their use.
     issue(st + kStages, xa[u], wr[u]);
   };
-  static_assert(kStages == 3, "the group below is written out for three register sets");
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
   int st = s0;
-  for (; st + kStages <= s1; st += kStages) {
-    step(S0{}, st);
-    step(S1{}, st + 1);
-    step(S2{}, st + 2);
-  }
-  if (st < s1) step(S0{}, st);
-  if (st + 1 < s1) step(S1{}, st + 1);
+  for (; st + kStages <= s1; st += kStages) step_group(step, st, s1, std::make_integer_sequence<int, kStages>{});
+  step_group(step, st, s1, std::make_integer_sequence<int, kStages - 1>{});
   if (!active) return;
 
   // D fragment: lane holds rows 4*fg .. +3 of column fr of each tile.
