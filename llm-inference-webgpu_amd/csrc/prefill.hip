@@ -173,8 +173,9 @@ hipError_t launch_rows(hipStream_t s, int op, const RowArgs& a) {
 // Thirty-two codes of one step for one thread: row n, columns k .. k+31, as int8.
 template <int FMT>
 struct WRaw {
-  v4u q[2];  // int8: 32 codes; int4: q[0] = 32 nibbles
-  int zero;  // int4: the group's zero point
+  v4u q[2];     // int8: 32 codes; int4: q[0] = 32 nibbles
+  float zero;   // int4: the group's zero point
+  float scale;  // int4: the step's group scale of weight row n0 + tid % 128
 };
 
 // Past K (the second half of a last 64-column step) the thread loads columns K - 32 ..
@@ -191,8 +192,7 @@ __device__ __forceinline__ void wraw_load(const DMat& w, int n, int k, int K, WR
     r.q[1] = *reinterpret_cast<const v4u*>(row + kk + 16);
   } else {
     r.q[0] = *reinterpret_cast<const v4u*>(row + kk / 2);
-    // an integer in [0, 15] (src/core/quantize.js:115)
-    r.zero = (int)w.zeros[(size_t)n * w.gpr + kk / (w.cpg * 32)];
+    r.zero = w.zeros[(size_t)n * w.gpr + kk / (w.cpg * 32)];
   }
 }
 
@@ -209,7 +209,8 @@ __device__ __forceinline__ void wraw_bytes(const WRaw<FMT>& r, v4u (&o)[2]) {
     o[0] = r.q[0];
     o[1] = r.q[1];
   } else {
-    const uint32_t nz = (uint32_t)((256 - r.zero) & 0xff) * 0x01010101u;  // -zero in every byte
+    // the zero point is an integer in [0, 15] (src/core/quantize.js:115)
+    const uint32_t nz = (uint32_t)((256 - (int)r.zero) & 0xff) * 0x01010101u;  // -zero in every byte
     uint32_t b[8];
     const uint32_t src[4] = {r.q[0].x, r.q[0].y, r.q[0].z, r.q[0].w};
 #pragma unroll
@@ -244,6 +245,7 @@ __device__ __forceinline__ void step_group(F& step, int st, int s1, std::integer
 template <int FMT>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t Bs[2][kGN][kGRow];
+  __shared__ float Ss[2][kGN];  // int4: the step's group scales of the tile's weight rows
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
   const int m0 = blockIdx.y * kGM, n0 = blockIdx.x * kGN;
   const int s0 = blockIdx.z * a.steps_per_split;
@@ -282,6 +284,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
 #pragma unroll
     for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + d * plane + k);
     wraw_load<FMT>(a.w, brow, k + bk, a.K, w);
+    if constexpr (FMT == QH_FMT_INT4)
+      w.scale = a.w.scales[(size_t)min(n0 + (tid & (kGN - 1)), a.N - 1) * a.w.gpr + min(st, s1 - 1) / group_steps];
   };
 #pragma unroll
   for (int u = 0; u < kStages; u++) issue(s0 + u, xa[u], wr[u]);
@@ -295,6 +299,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
       wraw_bytes<FMT>(wr[u], wb);
       *reinterpret_cast<v4u*>(&Bs[buf][br][bk]) = wb[0];
       *reinterpret_cast<v4u*>(&Bs[buf][br][bk + 16]) = wb[1];
+      if constexpr (FMT == QH_FMT_INT4)
+        if (tid < kGN) Ss[buf][tid] = wr[u].scale;
     }
     // One barrier per step: Bs[buf] is complete, and every wave has finished reading it
     // two steps ago (each wave reads a buffer before it arrives at the next barrier).
@@ -310,10 +316,9 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
           acc[d][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u][d], fb[j], acc[d][j], 0, 0, 0);
       if constexpr (FMT == QH_FMT_INT4) {
         if ((st + 1) % group_steps == 0) {  // the group's exact sum, scaled into the total
-          const int g = st / group_steps;
 #pragma unroll
           for (int j = 0; j < kNT; j++) {
-            const double sg = a.w.scales[(size_t)min(n0 + 16 * j + fr, a.N - 1) * a.w.gpr + g];
+            const double sg = Ss[buf][16 * j + fr];
 #pragma unroll
             for (int r = 0; r < 4; r++)
               tot[j][r] += sg * ((double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 +
