@@ -23,8 +23,8 @@
 // Tiling. A block of four waves computes 64 positions x 128 weight rows, each wave
 // owning 16 positions (1 x 8 MFMA tiles of 16 x 16), stepping K by 64. The weight tile
 // (128 x 64 codes, int4 expanded to int8) is staged in one of two LDS buffers, one
-// barrier per step; each lane loads its three digit fragments (16 bytes of its row per
-// digit) straight from global memory, three steps ahead. A step is 24 MFMAs per wave
+// barrier per step; each wave loads its three digit fragments (one contiguous 1 KB run
+// per digit in the step-major digit layout) straight from global memory, three steps ahead. A step is 24 MFMAs per wave
 // against 8 LDS fragment reads and no per-element vector arithmetic for int8 weights.
 // Long K is split over gridDim.z; partial tiles are summed in a fixed order by
 // k_gemm_finish.
@@ -49,6 +49,17 @@ constexpr int kStages = 3;                    // K steps of global loads in flig
 // K rounded up to whole steps: the digit planes are that wide, zeros past K.
 __host__ __device__ inline int padded_k(int K) { return (K + kGK - 1) / kGK * kGK; }
 
+// Digit planes, step-major: for each K step of 64 columns, the three digits, each M rows
+// rounded up to whole 16-row tiles (Mp); within a tile the 16-byte runs are in MFMA lane
+// order -- run g (columns 16g .. 16g+15 of the step) of row r at (16 g + r) * 16 -- so a
+// wave's fragment of one digit for one step is one contiguous 1 KB load, lane l taking row
+// l % 16, columns 16 (l / 16) .. +15. Rows past M within the last tile are never written
+// (only outputs of those rows read them, and those are dropped).
+__host__ __device__ inline int digit_rows(int M) { return (M + 15) & ~15; }
+__host__ __device__ inline size_t digit_offset(int Mp, int step, int d, int m, int b) {
+  return ((size_t)(step * kDigits + d) * Mp + (m & ~15)) * kGK + (b >> 4) * 256 + (m & 15) * 16 + (b & 15);
+}
+
 // ------------------------------------------------------------ activation digits --
 // The larger magnitude, NaN kept once met.
 __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v != v) ? v : p; }
@@ -60,8 +71,8 @@ __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v 
 // residual stream `resid` (f32, as the batched path's add); for ROW_RMSNORM normalized
 // as the f32 rmsnorm does; and, when `digits` is set, written as the digit planes of the
 // next contraction: s = max|y| / 127, X = rint(y * 2^16 / s) in three balanced base-256
-// digits [kDigits][M][Kp], zeros past n, and the row factor s * 2^-16 (NaN for a row
-// holding an infinity or a NaN, whose digits are zero).
+// digits (step-major, digit_offset), zeros past n, and the row factor s * 2^-16 (NaN for a
+// row holding an infinity or a NaN, whose digits are zero).
 template <int OP>
 __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   __shared__ float red[kBlock / kWave];
@@ -132,8 +143,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   const double s = (double)peak / 127.0;
   const double inv = finite && peak > 0.f ? 65536.0 / s : 0.0;
   if (tid == 0) a.row_factor[m] = finite ? s / 65536.0 : (double)NAN;
-  const size_t plane = (size_t)a.M * a.Kp;
-  int8_t* drow = a.digits + (size_t)m * a.Kp;
+  const int Mp = digit_rows(a.M);
   for (int j = 0; 4 * (tid + j * kBlock) < a.Kp; j++) {
     const int i4 = tid + j * kBlock;
     uint32_t w[kDigits] = {0, 0, 0};
@@ -154,7 +164,8 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
       }
     }
 #pragma unroll
-    for (int d = 0; d < kDigits; d++) *reinterpret_cast<uint32_t*>(drow + d * plane + 4 * i4) = w[d];
+    for (int d = 0; d < kDigits; d++)
+      *reinterpret_cast<uint32_t*>(a.digits + digit_offset(Mp, i4 >> 4, d, m, (4 * i4) & (kGK - 1))) = w[d];
   }
 }
 
@@ -227,7 +238,7 @@ __device__ __forceinline__ void wraw_bytes(const WRaw<FMT>& r, v4u (&o)[2]) {
 
 struct GemmArgs {
   DMat w;                    // int8 | int4, rows = N, cols = K
-  const int8_t* digits;      // [kDigits][M][Kp]
+  const int8_t* digits;      // step-major digit planes (digit_offset), Kp columns
   const double* row_factor;  // [M]
   float* out;                // splits == 1: Y [M][N]; else partials [splits][M][N]
   const float* bias;         // [N] or NULL (splits == 1 only)
@@ -254,10 +265,11 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
   const int mw = m0 + 16 * wave;             // this wave's first position
   const bool active = mw < a.M;              // wave-uniform: rows past M are not computed
 
-  // A fragments: this lane's row mw + fr (clamped; results past M are discarded), bytes
-  // 16*fg .. +15 of each step, one per digit plane.
-  const size_t plane = (size_t)a.M * a.Kp;
-  const int8_t* ar = a.digits + (size_t)min(mw + fr, a.M - 1) * a.Kp + 16 * fg;
+  // A fragments: this wave's 16-row tile (clamped to the last; results past M are
+  // discarded), lane row fr, bytes 16*fg .. +15 of each step, one 1 KB load per digit.
+  const int Mp = digit_rows(a.M);
+  const int8_t* ar = a.digits + (size_t)min(mw, Mp - 16) * kGK + 16 * lane;
+  const size_t dplane = (size_t)Mp * kGK;  // one digit of one step
   // Weight staging: thread t stages row t/2 of the tile, columns 32*(t%2) .. +31.
   const int br = tid >> 1, bk = 32 * (tid & 1);
   const int brow = min(n0 + br, a.N - 1);
@@ -282,7 +294,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
   auto issue = [&](int st, v4i (&x)[kDigits], WRaw<FMT>& w) {
     const int k = min(st, s1 - 1) * kGK;
 #pragma unroll
-    for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + d * plane + k);
+    for (int d = 0; d < kDigits; d++) x[d] = *reinterpret_cast<const v4i*>(ar + (size_t)(k / kGK * kDigits + d) * dplane);
     wraw_load<FMT>(a.w, brow, k + bk, a.K, w);
     if constexpr (FMT == QH_FMT_INT4)
       w.scale = a.w.scales[(size_t)min(n0 + (tid & (kGN - 1)), a.N - 1) * a.w.gpr + min(st, s1 - 1) / group_steps];
@@ -400,7 +412,7 @@ static int gemm_splits(const DMat& w, int M) {
 
 static size_t round256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-size_t digits_bytes(int M, int K) { return round256((size_t)kDigits * M * padded_k(K)); }
+size_t digits_bytes(int M, int K) { return round256((size_t)kDigits * digit_rows(M) * padded_k(K)); }
 int digits_width(int K) { return padded_k(K); }
 
 // Split partials of every launch of 1..M rows. Not the M-row figure alone: below a 64-row

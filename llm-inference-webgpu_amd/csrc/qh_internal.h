@@ -101,8 +101,9 @@ bool matmul_prefill_supported(const DMat& w);
 // Row kernel: row m = sum of `splits` partial rows [splits][M][in_len] (+ bias); for
 // ROW_SWIGLU silu(g)*u of interleaved gate|up pairs (in_len = 2n), else in_len = n; added
 // into `resid` [M][n] when set; ROW_RMSNORM then normalizes it (f32, `gain`, `eps`); when
-// `digits` is set it is written as the contraction's input: digit planes
-// [3][M][Kp = digits_width(n)] and row factors [M] (f64). n % 4 == 0, n <= 8192.
+// `digits` is set it is written as the contraction's input: digit planes (step-major,
+// M rounded up to 16-row tiles, Kp = digits_width(n) columns; digits_bytes) and row
+// factors [M] (f64). n % 4 == 0, n <= 8192.
 enum { ROW_PLAIN = 0, ROW_RMSNORM = 1, ROW_SWIGLU = 2 };
 struct RowArgs {
   const float* in;
