@@ -508,7 +508,7 @@ class GpuContext:
                                   y.ptr, seq))
 
     def matmul_prefill(self, w: Weight, x: DeviceBuffer, bias, y: DeviceBuffer, M: int) -> None:
-        """y [M, rows] = x [M, cols] . W^T (+ bias) on bf16 MFMA (int8 / int4 weights)."""
+        """y [M, rows] = x [M, cols] . W^T (+ bias) on the int8 matrix cores (int8 / int4 weights)."""
         _check(self.lib.qh_matmul_prefill(self.handle, ctypes.byref(w), x.ptr,
                                           bias.ptr if bias else None, y.ptr, M))
 
