@@ -176,6 +176,23 @@ def test_matmul_prefill_matches_oracle(ctx, hip, fmt, M, rows, cols):
     free(wb, dX, db, dY)
 
 
+@pytest.mark.parametrize("M,rows,cols", [(5, 130, 32), (33, 200, 96), (70, 300, 1056)])
+def test_matmul_prefill_half_last_step(ctx, hip, M, rows, cols):
+    """int8 with K = 64 k + 32: the last K step's second half lies past the row (its weight
+    loads re-read the row's last columns against zero digits), with ragged M and N and, at
+    1056 columns, K split over many slices."""
+    rng = np.random.default_rng(M + rows + cols)
+    w32 = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    X = rng.standard_normal((M, cols)).astype(np.float32)
+    W, wb, deq = upload_weight(ctx, hip, w32, "int8")
+    dX, dY = ctx.upload(X), ctx.empty(M * rows * 4)
+    ctx.matmul_prefill(W, dX, None, dY, M)
+    got = dY.read(count=M * rows).reshape(M, rows)
+    worst = max(rel_err(got[t], O.matvec(deq, X[t], rows, cols, None)) for t in range(M))
+    assert worst <= MFMA_REL
+    free(wb, dX, dY)
+
+
 def test_matmul_prefill_rejects_f16_and_ragged_k(ctx, hip):
     rng = np.random.default_rng(0)
     W, wb, _ = upload_weight(ctx, hip, (rng.standard_normal((64, 896)) * 0.02).astype(np.float32), "f16")
