@@ -391,13 +391,15 @@ bool matmul_prefill_supported(const DMat& w) {
   return (w.format == QH_FMT_INT8 || (w.format == QH_FMT_INT4 && w.cpg % 2 == 0)) && w.cols <= (1 << 17);
 }
 
-// K steps per split: as many splits as keep (M/64 x N/128 x splits) blocks within two per
-// CU, int4 splits on group boundaries.
+// K steps per split: as many splits as keep (M/64 x N/128 x splits) blocks within one per
+// CU, int4 splits on group boundaries. A CU holding two blocks runs each at well under half
+// speed (its L2 load rate is the bound), and every split adds an M x N partial that the
+// consumer row kernel reads back: 512-token prefill 3.6 ms at two blocks per CU, 3.4 ms at one.
 static int gemm_steps_per_split(const DMat& w, int M) {
   const int steps = padded_k(w.cols) / kGK;
   const int tiles = ((M + kGM - 1) / kGM) * ((w.rows + kGN - 1) / kGN);
   const int unit = w.format == QH_FMT_INT4 ? w.cpg / 2 : 1;
-  int splits = 512 / tiles;
+  int splits = 256 / tiles;
   splits = std::max(1, std::min(splits, steps / unit));
   int per = (steps + splits - 1) / splits;
   per = (per + unit - 1) / unit * unit;
