@@ -109,8 +109,10 @@ struct qh_cache {
   qh::CacheDev dev{};
   int length = 0;
   std::vector<void*> allocs;
-  hipGraph_t graph = nullptr;
+  hipGraph_t graph = nullptr;          // one carried decode step
   hipGraphExec_t exec = nullptr;
+  hipGraph_t graph_run = nullptr;      // kGraphRun carried steps back to back
+  hipGraphExec_t exec_run = nullptr;
   bool use_graph = true;  // false: decode enqueues every kernel directly
   bool busy = false;
   int pending_start = 0, pending_steps = 0;
@@ -606,6 +608,8 @@ int qh_cache_free(qh_cache* c) {
   hipStreamSynchronize(c->m->ctx->stream);
   if (c->exec) hipGraphExecDestroy(c->exec);
   if (c->graph) hipGraphDestroy(c->graph);
+  if (c->exec_run) hipGraphExecDestroy(c->exec_run);
+  if (c->graph_run) hipGraphDestroy(c->graph_run);
   for (void* p : c->allocs) hipFree(p);
   hipFree(c->d_hidden);
   if (c->pw_mem) hipFree(c->pw_mem);
@@ -831,6 +835,8 @@ int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t se
   return finish_forward(c, seq, h_logits, h_argmax);
 }
 
+constexpr int kGraphRun = 8;  // decode steps per replayed run graph
+
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps) {
   QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode needs a model and its cache");
   QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
@@ -841,26 +847,39 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   if (rc) return rc;
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
-  if (c->use_graph && !c->exec) {
+  // Carried steps are identical launches (position and tokens live on the device), so a
+  // graph of kGraphRun of them replays runs of steps with one launch each.
+  auto capture = [&](int n, hipGraph_t* graph, hipGraphExec_t* exec) -> int {
     QH_HIP(hipStreamSynchronize(s));
     QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-    hipError_t e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n && e == hipSuccess; i++) e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(s, &g);
     QH_HIP(e);
     QH_HIP(e2);
-    c->graph = g;
-    QH_HIP(hipGraphInstantiate(&c->exec, c->graph, nullptr, nullptr, 0));
-  }
+    *graph = g;
+    QH_HIP(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+    return QH_OK;
+  };
+  if (c->use_graph && !c->exec && (rc = capture(1, &c->graph, &c->exec))) return rc;
+  if (c->use_graph && steps >= kGraphRun && !c->exec_run && (rc = capture(kGraphRun, &c->graph_run, &c->exec_run)))
+    return rc;
   c->h_pinned[3] = first_token;
   QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s));
   if ((rc = set_state(c, c->length, c->length + 1))) return rc;
   // Each replayed step starts from the row its predecessor's pick gathered; the
   // first starts from this gather.
   QH_HIP(qh::enqueue_gather(s, m->dev, c->dev));
-  for (int i = 0; i < steps; i++) {
+  for (int i = 0; i < steps;) {
+    if (c->use_graph && steps - i >= kGraphRun) {
+      QH_HIP(hipGraphLaunch(c->exec_run, s));
+      i += kGraphRun;
+      continue;
+    }
     if (c->use_graph) QH_HIP(hipGraphLaunch(c->exec, s));
     else QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true));
+    i++;
   }
   c->busy = true;
   c->pending_start = c->length;

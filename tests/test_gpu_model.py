@@ -79,9 +79,12 @@ def test_graph_replay_equals_direct_steps(hip, tiny_model):
     c1, c2 = model.newCache(32), model.newCache(32)
     first = model.forward_tokens(prompt, c1)["argmax"]
     assert model.forward_tokens(prompt, c2)["argmax"] == first
-    graph = model.decode(c1, first, 10)
+    # runs of 8 steps replay as one graph launch, the rest step by step; the second call
+    # reuses the captured graphs
+    graph = list(model.decode(c1, first, 10))
+    graph += list(model.decode(c1, graph[-1], 9))
     direct, tok = [], first
-    for _ in range(10):
+    for _ in range(19):
         tok = model.forward_tokens([tok], c2)["argmax"]
         direct.append(tok)
     assert list(graph) == direct
