@@ -445,8 +445,8 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: every box in this pool has one, and batch-1 decode of a "
-              "0.5B model is not sharded (see DESIGN.md for how it would be). Run with --gpus 1.",
+        print("bench.py measures one GPU: batch-1 decode of a 0.5B model runs on a single GPU and "
+              "is not sharded across several. Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
