@@ -110,9 +110,12 @@ int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_
               float* d_y, int32_t seq);
 /* The batched-prefill contraction on the matrix cores (no counterpart kernel in the reference,
  * whose prefill is batchedMatvec, kernels.js:232-290, selected by model.js:297-306):
- * y [M, rows] = x [M, cols] . W^T (+ bias) for int8 / int4 weights, as bf16 MFMA over the exact
- * weight codes and an exact three-term bf16 split of x (products exact, f32 accumulation,
- * scales factored out). cols must be a multiple of 32. x, y f32 [M, cols] / [M, rows]. */
+ * y [M, rows] = x [M, cols] . W^T (+ bias) for int8 / int4 weights, as int8 MFMA
+ * (v_mfma_i32_16x16x64_i8) of the exact weight codes against each activation row written as a
+ * 24-bit fixed-point integer in three int8 digit planes: every product and sum is exact in
+ * int32, and the digits and scales are recombined in f64 once per output (int8) or per group
+ * (int4), ~4e-7 relative to the f64 sum. cols must be a multiple of 32. x, y f32 [M, cols] /
+ * [M, rows]. */
 int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
                       float* d_y, int32_t M);
 /* The isolated-matvec form: f16 activation x [cols], f32 y [rows]. */
@@ -236,9 +239,12 @@ typedef struct qh_cache qh_cache;
 int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out);
 
 /* Arithmetic of the model's forward/decode kernels.
- *   QH_NUMERICS_FAST (default): split-K online-softmax attention in f32 (one pass over the f16
- *     cache, slots merged in the o-projection's staging); matvecs as in EXACT. Logits agree
- *     with the CPU path (src/cpu/model.js:55-166) to f32 rounding (~1e-6 relative).
+ *   QH_NUMERICS_FAST (default): the arithmetic of the reference's WebGPU kernels -- matvecs
+ *     summed in f32 (the quantization scale factored out of each 16-byte chunk), rmsnorm and
+ *     swiglu in f32, split-K online-softmax attention in f32 (one pass over the f16 cache,
+ *     slots merged in the o-projection's staging). Each launch agrees with the CPU path's
+ *     arithmetic to ~1e-6 relative; logits of a whole forward within the reference's 1e-4
+ *     (an f16 cache entry that rounds the other way moves later layers slightly).
  *   QH_NUMERICS_EXACT: every kernel evaluates the CPU path's arithmetic in its order (f64
  *     accumulation stored to f32, attention by the global max with a sequential f32 PV sum),
  *     so logits and the f16 cache are the oracle's bit for bit up to f64 ordering noise.
@@ -253,9 +259,11 @@ int qh_model_set_numerics(qh_model* m, int32_t numerics);
  *     tile (batchedMatvec); every output is summed as the decode step sums it, so a prefill and
  *     the same positions decoded one by one give the same bits (README.md:256-272).
  *   QH_MATMUL_MATVEC: one decode step per position (the reference's 'matvec').
- *   QH_MATMUL_MFMA: all positions per layer, int8/int4 weights contracted on bf16 MFMA
- *     (qh_matmul_prefill; f16 weights use the batched tiles); within a stated tolerance of the
- *     others, as the reference's 'tiled' was (web/scaling.html:122-127).
+ *   QH_MATMUL_MFMA: all positions per layer, int8/int4 weights contracted on int8 MFMA
+ *     (qh_matmul_prefill's digit planes; f16 weights use the batched tiles) and the prompt's
+ *     attention on f16 MFMA (qh_attention_mfma); not bitwise equal to the others, within the
+ *     reference's 1e-4 of them, as its 'tiled' path was (web/scaling.html:122-127). The
+ *     reference's matmul option 'tiled' selects this mode in the bindings.
  * May be changed between forward() calls. */
 enum { QH_MATMUL_BATCHED = 0, QH_MATMUL_MATVEC = 1, QH_MATMUL_MFMA = 2 };
 int qh_model_set_matmul(qh_model* m, int32_t matmul);
@@ -309,6 +317,11 @@ int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int3
 /* Enqueue the graph replays without waiting (for timing); qh_decode_collect waits and copies. */
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps);
 int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens);
+/* Captures and uploads the cache's decode graphs (one step, and a run of 8 steps) now instead
+ * of at the first decode that needs them, so a timed decode replays graphs that are already
+ * resident. Optional: qh_decode_launch captures whatever is missing. No counterpart in the
+ * reference, which records every step anew (src/gpu/model.js:261). */
+int qh_decode_prepare(qh_model* m, qh_cache* c);
 /* use_graph = 0: later decodes on this cache enqueue every kernel of a step directly instead
  * of replaying the captured graph (same kernels, same tokens), for tools that cannot follow
  * graph launches. No counterpart in the reference, which re-encodes every step
@@ -340,6 +353,30 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
  * web/decode-profile.html:239-283). It overwrites the position's decode scratch (and, for the
  * residual roles, the hidden row): rewind or re-prefill before decoding on. */
 int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, float* us_per_launch);
+
+/* Kernel-level parity access to one decode step (the reference's per-kernel harness,
+ * web/kernels.html:56-134, checks each WGSL kernel against the CPU on the same inputs; these
+ * entry points give the decode step's fused launches the same treatment). No counterpart in
+ * the reference's GpuModel.
+ *
+ * The decode vectors of a cache: QH_VEC_X the residual row [hidden], QH_VEC_Q the rotated
+ * queries [hidden], QH_VEC_H the swiglu output [intermediate], QH_VEC_LOGITS [vocab]; and,
+ * read-only, QH_VEC_KEY / QH_VEC_VALUE: layer `layer`'s cache row at the current position
+ * (cache length) as f32 [kv_heads * head_dim], kv head major. */
+enum { QH_VEC_X = 0, QH_VEC_Q = 1, QH_VEC_H = 2, QH_VEC_LOGITS = 3, QH_VEC_KEY = 4, QH_VEC_VALUE = 5 };
+/* Writes h_in (if not NULL) into the vector, then reads it into h_out (if not NULL). Waits. */
+int qh_cache_vector(qh_cache* c, int32_t which, int32_t layer, const float* h_in, float* h_out);
+/* Runs the one launch of `role` that a decode step makes for `layer`, at position = the cache
+ * length (which does not advance), and waits:
+ *   QH_ROLE_QKV        x -> rmsnorm -> q|k|v + bias -> rope -> q, and the f16 K/V row at the position
+ *   QH_ROLE_ATTENTION  q and the cache rows 0..position -> attention (FAST: the slot partials)
+ *   QH_ROLE_OPROJ      (FAST: merge of the slot partials) -> o-projection -> x += it
+ *   QH_ROLE_GATEUP     x -> rmsnorm -> gate|up -> swiglu -> h
+ *   QH_ROLE_DOWN       h -> down projection -> x += it
+ *   QH_ROLE_HEAD       x -> final rmsnorm -> lm_head -> logits, and the argmax into *h_token
+ *                      (the pick then overwrites x with that token's embedding; `layer` ignored)
+ * h_token may be NULL (and is set to -1 for the other roles). */
+int qh_decode_role(qh_model* m, qh_cache* c, int32_t role, int32_t layer, int32_t* h_token);
 
 #ifdef __cplusplus
 }

@@ -837,6 +837,40 @@ int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t se
 
 constexpr int kGraphRun = 8;  // decode steps per replayed run graph
 
+// Captures the cache's decode graphs that are not captured yet: one carried step, and
+// (`run`) kGraphRun carried steps back to back. Each is uploaded to the device once, so
+// its first replay costs what every later one does.
+static int capture_graphs(qh_model* m, qh_cache* c, bool run) {
+  hipStream_t s = m->ctx->stream;
+  auto capture = [&](int n, hipGraph_t* graph, hipGraphExec_t* exec) -> int {
+    QH_HIP(hipStreamSynchronize(s));
+    QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < n && e == hipSuccess; i++) e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
+    hipGraph_t g = nullptr;
+    hipError_t e2 = hipStreamEndCapture(s, &g);
+    QH_HIP(e);
+    QH_HIP(e2);
+    *graph = g;
+    QH_HIP(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
+    QH_HIP(hipGraphUpload(*exec, s));
+    QH_HIP(hipStreamSynchronize(s));
+    return QH_OK;
+  };
+  int rc = QH_OK;
+  if (!c->exec && (rc = capture(1, &c->graph, &c->exec))) return rc;
+  if (run && !c->exec_run && (rc = capture(kGraphRun, &c->graph_run, &c->exec_run))) return rc;
+  return QH_OK;
+}
+
+int qh_decode_prepare(qh_model* m, qh_cache* c) {
+  QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode_prepare needs a model and its cache");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_HIP(hipSetDevice(m->ctx->device));
+  if (!c->use_graph) return QH_OK;
+  return capture_graphs(m, c, true);
+}
+
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps) {
   QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode needs a model and its cache");
   QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
@@ -849,22 +883,7 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   hipStream_t s = m->ctx->stream;
   // Carried steps are identical launches (position and tokens live on the device), so a
   // graph of kGraphRun of them replays runs of steps with one launch each.
-  auto capture = [&](int n, hipGraph_t* graph, hipGraphExec_t* exec) -> int {
-    QH_HIP(hipStreamSynchronize(s));
-    QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
-    hipError_t e = hipSuccess;
-    for (int i = 0; i < n && e == hipSuccess; i++) e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
-    hipGraph_t g = nullptr;
-    hipError_t e2 = hipStreamEndCapture(s, &g);
-    QH_HIP(e);
-    QH_HIP(e2);
-    *graph = g;
-    QH_HIP(hipGraphInstantiate(exec, g, nullptr, nullptr, 0));
-    return QH_OK;
-  };
-  if (c->use_graph && !c->exec && (rc = capture(1, &c->graph, &c->exec))) return rc;
-  if (c->use_graph && steps >= kGraphRun && !c->exec_run && (rc = capture(kGraphRun, &c->graph_run, &c->exec_run)))
-    return rc;
+  if (c->use_graph && (rc = capture_graphs(m, c, steps >= kGraphRun))) return rc;
   c->h_pinned[3] = first_token;
   QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s));
   if ((rc = set_state(c, c->length, c->length + 1))) return rc;
@@ -941,6 +960,75 @@ int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, 
   if (e1) hipEventDestroy(e1);
   QH_HIP(err);
   *us_per_launch = ms * 1e3f / reps;
+  return QH_OK;
+}
+
+int qh_decode_role(qh_model* m, qh_cache* c, int32_t role, int32_t layer, int32_t* h_token) {
+  QH_CHECK(m && c && c->m == m, QH_ERR_INVALID, "decode_role needs a model and its cache");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(role >= QH_ROLE_QKV && role <= QH_ROLE_HEAD, QH_ERR_INVALID, "role %d has no single decode launch", role);
+  QH_CHECK(role == QH_ROLE_HEAD || (layer >= 0 && layer < m->dev.layers), QH_ERR_RANGE, "layer %d out of range",
+           layer);
+  QH_CHECK(c->length < c->dev.capacity, QH_ERR_RANGE, "the cache is full");
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  const int pos = c->length;
+  int rc = set_state(c, pos, pos + 1);
+  if (rc) return rc;
+  if (role == QH_ROLE_HEAD) {
+    // The head and the pick, as a step ends; the pick's gather of the next row is undone by
+    // the caller rewriting x before the next role.
+    QH_HIP(qh::enqueue_head(s, m->dev, c->dev));
+    QH_HIP(hipMemcpyAsync(c->h_pinned + 2, c->dev.pred + pos, 4, hipMemcpyDeviceToHost, s));
+  } else {
+    QH_HIP(qh::enqueue_role(s, m->dev, c->dev, role, layer));
+  }
+  QH_HIP(hipStreamSynchronize(s));
+  if (h_token) *h_token = role == QH_ROLE_HEAD ? c->h_pinned[2] : -1;
+  return QH_OK;
+}
+
+int qh_cache_vector(qh_cache* c, int32_t which, int32_t layer, const float* h_in, float* h_out) {
+  QH_CHECK(c, QH_ERR_INVALID, "cache_vector needs a cache");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight");
+  const qh::ModelDev& md = c->m->dev;
+  const qh::CacheDev& d = c->dev;
+  hipStream_t s = c->m->ctx->stream;
+  QH_HIP(hipSetDevice(c->m->ctx->device));
+  if (which == QH_VEC_KEY || which == QH_VEC_VALUE) {
+    QH_CHECK(!h_in, QH_ERR_INVALID, "the cache rows are read-only here");
+    QH_CHECK(layer >= 0 && layer < md.layers, QH_ERR_RANGE, "layer %d out of range", layer);
+    QH_CHECK(c->length < d.capacity, QH_ERR_RANGE, "the cache is full");
+    if (!h_out) return QH_OK;
+    const int pos = c->length, hd = md.head_dim;
+    const uint16_t* base = d.kv + (size_t)layer * d.layer_elems;
+    std::vector<uint16_t> row((size_t)md.kv_heads * hd);
+    for (int h = 0; h < md.kv_heads; h++) {
+      if (which == QH_VEC_KEY) {
+        QH_HIP(hipMemcpyAsync(row.data() + (size_t)h * hd, base + ((size_t)h * d.capacity + pos) * hd, hd * 2,
+                              hipMemcpyDeviceToHost, s));
+      } else {
+        // One value per dimension row of the dimension-major cache.
+        QH_HIP(hipMemcpy2DAsync(row.data() + (size_t)h * hd, 2, base + d.key_elems + (size_t)h * hd * d.vstride + pos,
+                                (size_t)d.vstride * 2, 2, hd, hipMemcpyDeviceToHost, s));
+      }
+    }
+    QH_HIP(hipStreamSynchronize(s));
+    for (size_t i = 0; i < row.size(); i++) h_out[i] = f16_to_f32(row[i]);
+    return QH_OK;
+  }
+  float* dev = nullptr;
+  size_t n = 0;
+  switch (which) {
+    case QH_VEC_X: dev = d.x, n = md.hidden; break;
+    case QH_VEC_Q: dev = d.q, n = md.hidden; break;
+    case QH_VEC_H: dev = d.h, n = md.intermediate; break;
+    case QH_VEC_LOGITS: dev = d.logits, n = md.vocab; break;
+    default: return fail(QH_ERR_INVALID, "unknown decode vector %d", which);
+  }
+  if (h_in) QH_HIP(hipMemcpyAsync(dev, h_in, n * 4, hipMemcpyHostToDevice, s));
+  if (h_out) QH_HIP(hipMemcpyAsync(h_out, dev, n * 4, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
   return QH_OK;
 }
 

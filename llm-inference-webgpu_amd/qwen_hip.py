@@ -31,6 +31,8 @@ MATMUL = {"batched": 0, "matvec": 1, "mfma": 2}
 FORMAT_OF = {"f32": FMT_F32, "f16": FMT_F16, "int8": FMT_INT8, "int4": FMT_INT4, "bf16": FMT_BF16}
 # Kernel roles of a decode step, in QH_ROLE_* order.
 ROLES = ("embed", "qkv", "attention", "oproj", "gateup", "down", "head")
+# Decode-state vectors of a cache, in QH_VEC_* order.
+VECTORS = ("x", "q", "h", "logits", "key", "value")
 
 
 class QwenHipError(RuntimeError):
@@ -234,6 +236,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_decode_collect": [vp, vp, i32, vp], "qh_decode_use_graph": [vp, i32],
         "qh_decode_profile": [vp, vp, i32, i32, vp, vp, vp],
         "qh_decode_kernel_time": [vp, vp, i32, i32, vp],
+        "qh_decode_prepare": [vp, vp], "qh_decode_role": [vp, vp, i32, i32, vp],
+        "qh_cache_vector": [vp, i32, i32, vp, vp],
     }
     for name, args in sigs.items():
         f = getattr(lib, name)
@@ -581,6 +585,20 @@ class GpuKVCache:
         c = self.model.config
         return c.layers * self.capacity * c.kv_dim * 2 * 2
 
+    def vector(self, which: str, value=None, layer: int = 0) -> np.ndarray:
+        """One decode-state vector of the cache ("x", "q", "h", "logits"; or, read-only, the
+        "key" / "value" row of `layer` at the current position): writes `value` first when
+        given, then returns the vector's contents."""
+        c = self.model.config
+        n = {"x": c.hidden, "q": c.hidden, "h": c.intermediate, "logits": c.vocab,
+             "key": c.kv_dim, "value": c.kv_dim}[which]
+        src = None if value is None else np.ascontiguousarray(value, np.float32)
+        if src is not None and src.size != n:
+            raise ValueError(f"{which} has {n} values, got {src.size}")
+        out = np.empty(n, np.float32)
+        _check(self.model.lib.qh_cache_vector(self.handle, VECTORS.index(which), layer, _ptr(src), _ptr(out)))
+        return out
+
     def present(self, layer: int):
         """{key, value} as [kvHeads, length, headDim] f32 (src/cpu/cache.js:97-115)."""
         c, n = self.model.config, self.length
@@ -803,6 +821,17 @@ class GpuModel:
         _check(self.lib.qh_decode_profile(self.handle, cache.handle, first_token, steps, _ptr(out),
                                           _ptr(ms), _ptr(n)))
         return out, {r: (float(ms[i]), int(n[i])) for i, r in enumerate(ROLES)}
+
+    def decode_prepare(self, cache: GpuKVCache) -> None:
+        """Capture and upload the cache's decode graphs now (before a timed decode)."""
+        _check(self.lib.qh_decode_prepare(self.handle, cache.handle))
+
+    def decode_role(self, cache: GpuKVCache, role: str, layer: int = 0):
+        """Run one decode launch of `role` for `layer` at the cache's position (which does not
+        advance); for "head", returns the argmax token."""
+        tok = ctypes.c_int32(-1)
+        _check(self.lib.qh_decode_role(self.handle, cache.handle, ROLES.index(role), layer, ctypes.byref(tok)))
+        return tok.value if role == "head" else None
 
     def kernel_time(self, cache: GpuKVCache, role: str, reps: int = 240) -> float:
         """Microseconds per back-to-back launch of one decode role's kernel (see the C ABI)."""

@@ -248,11 +248,34 @@ void or_rmsnorm(const float* x, const float* weight, double eps, int n, float* o
   for (int i = 0; i < n; i++) out[i] = (float)((double)x[i] * scale * (double)weight[i]);
 }
 
-/* ops.js:33-41: the sum starts from the bias and runs in column order in f64. */
+/* ops.js:33-41: the sum starts from the bias and runs in column order in f64. Four rows are
+ * summed side by side (each still in its own column order, so every output is the same), which
+ * keeps four independent add chains in flight instead of one. */
 void or_matvec(const float* W, const float* x, int rows, int cols, const float* bias,
                float* out) {
+  const int quads = rows / 4;
 #pragma omp parallel for schedule(static) if ((size_t)rows * cols > (1u << 18))
-  for (int r = 0; r < rows; r++) {
+  for (int g = 0; g < quads; g++) {
+    const int r = 4 * g;
+    const float* w0 = W + (size_t)r * cols;
+    const float* w1 = w0 + cols;
+    const float* w2 = w1 + cols;
+    const float* w3 = w2 + cols;
+    double a0 = bias ? (double)bias[r] : 0, a1 = bias ? (double)bias[r + 1] : 0;
+    double a2 = bias ? (double)bias[r + 2] : 0, a3 = bias ? (double)bias[r + 3] : 0;
+    for (int c = 0; c < cols; c++) {
+      const double xc = (double)x[c];
+      a0 += (double)w0[c] * xc;
+      a1 += (double)w1[c] * xc;
+      a2 += (double)w2[c] * xc;
+      a3 += (double)w3[c] * xc;
+    }
+    out[r] = (float)a0;
+    out[r + 1] = (float)a1;
+    out[r + 2] = (float)a2;
+    out[r + 3] = (float)a3;
+  }
+  for (int r = 4 * quads; r < rows; r++) {
     const float* row = W + (size_t)r * cols;
     double acc = bias ? (double)bias[r] : 0;
     for (int c = 0; c < cols; c++) acc += (double)row[c] * (double)x[c];
@@ -350,10 +373,13 @@ void or_grouped_attention(const float* q, const float* keys, const float* values
 #pragma omp parallel if ((size_t)num_heads * seq * total * head_dim > (1u << 20))
   {
     float* sc = (float*)malloc(sizeof(float) * (size_t)(total > 0 ? total : 1));
+    /* (head, query) pairs write disjoint outputs, each in its own sequential order. */
 #pragma omp for schedule(dynamic)
-    for (int h = 0; h < num_heads; h++) {
+    for (int ht = 0; ht < num_heads * seq; ht++) {
+      const int h = ht / seq;
       const int kv_base = (h / group) * head_dim;
-      for (int t = 0; t < seq; t++) {
+      {
+        const int t = ht % seq;
         const int q_base = t * q_dim + h * head_dim;
         const int up_to = past + t;
         for (int s = 0; s <= up_to; s++) {
@@ -381,8 +407,12 @@ void or_grouped_attention(const float* q, const float* keys, const float* values
 
 struct or_cache {
   int layers, kv_dim, kv_heads, head_dim, capacity, length;
+  int pinned;  /* positions below this keep their contents when a forward pass writes them */
   float** keys;
   float** values;
+  /* While pinned: what a forward pass computed for the pinned rows, unrounded f32. */
+  float** shadow_keys;
+  float** shadow_values;
 };
 
 /* cache.js:20-31: [capacity, kvDim] f32 per layer for keys and for values. */
@@ -405,14 +435,46 @@ or_cache* or_cache_new(const or_config* cfg, int capacity) {
 
 void or_cache_free(or_cache* c) {
   if (!c) return;
-  for (int l = 0; l < c->layers; l++) { free(c->keys[l]); free(c->values[l]); }
+  for (int l = 0; l < c->layers; l++) {
+    free(c->keys[l]);
+    free(c->values[l]);
+    if (c->shadow_keys) free(c->shadow_keys[l]);
+    if (c->shadow_values) free(c->shadow_values[l]);
+  }
   free(c->keys);
   free(c->values);
+  free(c->shadow_keys);
+  free(c->shadow_values);
   free(c);
 }
 
 int or_cache_length(const or_cache* c) { return c->length; }
 void or_cache_set_length(or_cache* c, int length) { c->length = length; }
+void or_cache_pin(or_cache* c, int positions) {
+  c->pinned = positions < 0 ? 0 : positions > c->capacity ? c->capacity : positions;
+  if (c->pinned && !c->shadow_keys) {
+    c->shadow_keys = (float**)calloc((size_t)c->layers, sizeof(float*));
+    c->shadow_values = (float**)calloc((size_t)c->layers, sizeof(float*));
+    for (int l = 0; l < c->layers; l++) {
+      c->shadow_keys[l] = (float*)calloc((size_t)c->capacity * c->kv_dim, sizeof(float));
+      c->shadow_values[l] = (float*)calloc((size_t)c->capacity * c->kv_dim, sizeof(float));
+    }
+  }
+}
+
+/* The shadow rows 0..n-1 of a layer in the present layout [kv_heads, n, head_dim]. */
+int or_cache_shadow(const or_cache* c, int layer, int n, float* key, float* value) {
+  if (!c->shadow_keys || layer < 0 || layer >= c->layers || n < 0 || n > c->pinned) return -3;
+  for (int h = 0; h < c->kv_heads; h++) {
+    for (int t = 0; t < n; t++) {
+      const size_t from = (size_t)t * c->kv_dim + (size_t)h * c->head_dim;
+      const size_t to = ((size_t)h * n + t) * c->head_dim;
+      memcpy(key + to, c->shadow_keys[layer] + from, sizeof(float) * (size_t)c->head_dim);
+      memcpy(value + to, c->shadow_values[layer] + from, sizeof(float) * (size_t)c->head_dim);
+    }
+  }
+  return 0;
+}
 
 /* cache.js:97-115: stored [position, kvHead*headDim], published [kvHead, position, headDim]. */
 void or_cache_present(const or_cache* c, int layer, float* key, float* value) {
@@ -427,22 +489,36 @@ void or_cache_present(const or_cache* c, int layer, float* key, float* value) {
   }
 }
 
-/* cache.js:66-71 (writeAt), with the optional same-f16 rounding. */
-static void cache_write(or_cache* c, int layer, int at, const float* k, const float* v, int count,
-                        int kv_f16) {
+/* cache.js:66-71 (writeAt), with the optional same-f16 rounding. Rows below `floor` are left
+ * as they are. */
+static void cache_write_from(or_cache* c, int layer, int at, const float* k, const float* v, int count,
+                             int kv_f16, int floor) {
+  const size_t first = at < floor ? (size_t)(floor - at) * c->kv_dim : 0;
   const size_t n = (size_t)count * c->kv_dim;
   float* kd = c->keys[layer] + (size_t)at * c->kv_dim;
   float* vd = c->values[layer] + (size_t)at * c->kv_dim;
-  for (size_t i = 0; i < n; i++) {
+  for (size_t i = first; i < n; i++) {
     kd[i] = kv_f16 ? or_f16_to_f32(or_f32_to_f16(k[i])) : k[i];
     vd[i] = kv_f16 ? or_f16_to_f32(or_f32_to_f16(v[i])) : v[i];
   }
 }
 
+/* A forward pass's append: pinned rows keep the contents loaded into them, and what the pass
+ * computed for them goes to the shadow rows unrounded. */
+static void cache_write(or_cache* c, int layer, int at, const float* k, const float* v, int count,
+                        int kv_f16) {
+  for (int t = at; t < at + count && t < c->pinned; t++) {
+    const size_t o = (size_t)t * c->kv_dim, i = (size_t)(t - at) * c->kv_dim;
+    memcpy(c->shadow_keys[layer] + o, k + i, sizeof(float) * (size_t)c->kv_dim);
+    memcpy(c->shadow_values[layer] + o, v + i, sizeof(float) * (size_t)c->kv_dim);
+  }
+  cache_write_from(c, layer, at, k, v, count, kv_f16, c->pinned);
+}
+
 int or_cache_write(or_cache* c, int layer, int at, const float* k, const float* v, int count,
                    int kv_f16) {
   if (layer < 0 || layer >= c->layers || at < 0 || count < 0 || at + count > c->capacity) return -3;
-  cache_write(c, layer, at, k, v, count, kv_f16);
+  cache_write_from(c, layer, at, k, v, count, kv_f16, 0);
   return 0;
 }
 
@@ -470,57 +546,74 @@ int or_forward_hidden(const or_model* m, or_cache* cache, const float* hidden, i
 
   float* x = (float*)malloc(sizeof(float) * (size_t)seq * d);
   memcpy(x, hidden, sizeof(float) * (size_t)seq * d);
-  float* normed = (float*)malloc(sizeof(float) * d);
   float* q = (float*)malloc(sizeof(float) * (size_t)seq * d);
   float* k = (float*)malloc(sizeof(float) * (size_t)seq * kv_dim);
   float* v = (float*)malloc(sizeof(float) * (size_t)seq * kv_dim);
   float* attn = (float*)malloc(sizeof(float) * (size_t)seq * d);
   float* scores = (float*)malloc(sizeof(float) * (size_t)total);
-  float* gate = (float*)malloc(sizeof(float) * ffn);
-  float* up = (float*)malloc(sizeof(float) * ffn);
-  float* projected = (float*)malloc(sizeof(float) * d);
   double* inv = (double*)malloc(sizeof(double) * (size_t)(hd / 2));
   or_rope_freqs(hd, cfg->rope_theta, inv);
+  /* Positions are independent within each of the three per-position loops below, and every
+   * output keeps its own summation order, so running positions on several threads (several
+   * positions) or a matvec's rows on several threads (one position) gives the same bits. */
+  const int by_position = seq >= 4;
 
   for (int layer = 0; layer < cfg->layers; layer++) {
     const or_layer* w = &m->layers[layer];
-    for (int t = 0; t < seq; t++) {          /* model.js:96-114 */
-      or_rmsnorm(x + (size_t)t * d, w->input_norm, cfg->eps, d, normed);
-      or_matvec(w->wq, normed, d, d, w->bq, q + (size_t)t * d);
-      or_matvec(w->wk, normed, kv_dim, d, w->bk, k + (size_t)t * kv_dim);
-      or_matvec(w->wv, normed, kv_dim, d, w->bv, v + (size_t)t * kv_dim);
-      const int position = past + t;
-      for (int h = 0; h < cfg->heads; h++) or_rope_inplace(q, t * d + h * hd, hd, position, inv);
-      for (int h = 0; h < cfg->kv_heads; h++) or_rope_inplace(k, t * kv_dim + h * hd, hd, position, inv);
+#pragma omp parallel if (by_position)
+    {
+      float* normed = (float*)malloc(sizeof(float) * d);
+#pragma omp for schedule(dynamic)
+      for (int t = 0; t < seq; t++) {          /* model.js:96-114 */
+        or_rmsnorm(x + (size_t)t * d, w->input_norm, cfg->eps, d, normed);
+        or_matvec(w->wq, normed, d, d, w->bq, q + (size_t)t * d);
+        or_matvec(w->wk, normed, kv_dim, d, w->bk, k + (size_t)t * kv_dim);
+        or_matvec(w->wv, normed, kv_dim, d, w->bv, v + (size_t)t * kv_dim);
+        const int position = past + t;
+        for (int h = 0; h < cfg->heads; h++) or_rope_inplace(q, t * d + h * hd, hd, position, inv);
+        for (int h = 0; h < cfg->kv_heads; h++) or_rope_inplace(k, t * kv_dim + h * hd, hd, position, inv);
+      }
+      free(normed);
     }
     cache_write(cache, layer, past, k, v, seq, m->kv_f16);   /* model.js:116 */
     or_grouped_attention(q, cache->keys[layer], cache->values[layer], attn, scores, seq, past,
                          cfg->heads, cfg->kv_heads, hd);      /* model.js:121-123 */
-    for (int t = 0; t < seq; t++) {          /* model.js:125-128 */
-      or_matvec(w->wo, attn + (size_t)t * d, d, d, NULL, projected);
-      float* row = x + (size_t)t * d;
-      for (int i = 0; i < d; i++) row[i] = (float)((double)row[i] + (double)projected[i]);
-    }
-    for (int t = 0; t < seq; t++) {          /* model.js:131-140 */
-      float* row = x + (size_t)t * d;
-      or_rmsnorm(row, w->post_norm, cfg->eps, d, normed);
-      or_matvec(w->w_gate, normed, ffn, d, NULL, gate);
-      or_matvec(w->w_up, normed, ffn, d, NULL, up);
-      or_swiglu(gate, up, ffn);
-      or_matvec(w->w_down, gate, d, ffn, NULL, projected);
-      for (int i = 0; i < d; i++) row[i] = (float)((double)row[i] + (double)projected[i]);
+#pragma omp parallel if (by_position)
+    {
+      float* normed = (float*)malloc(sizeof(float) * d);
+      float* projected = (float*)malloc(sizeof(float) * d);
+      float* gate = (float*)malloc(sizeof(float) * ffn);
+      float* up = (float*)malloc(sizeof(float) * ffn);
+#pragma omp for schedule(dynamic)
+      for (int t = 0; t < seq; t++) {          /* model.js:125-128 */
+        or_matvec(w->wo, attn + (size_t)t * d, d, d, NULL, projected);
+        float* row = x + (size_t)t * d;
+        for (int i = 0; i < d; i++) row[i] = (float)((double)row[i] + (double)projected[i]);
+      }
+#pragma omp for schedule(dynamic)
+      for (int t = 0; t < seq; t++) {          /* model.js:131-140 */
+        float* row = x + (size_t)t * d;
+        or_rmsnorm(row, w->post_norm, cfg->eps, d, normed);
+        or_matvec(w->w_gate, normed, ffn, d, NULL, gate);
+        or_matvec(w->w_up, normed, ffn, d, NULL, up);
+        or_swiglu(gate, up, ffn);
+        or_matvec(w->w_down, gate, d, ffn, NULL, projected);
+        for (int i = 0; i < d; i++) row[i] = (float)((double)row[i] + (double)projected[i]);
+      }
+      free(normed); free(projected); free(gate); free(up);
     }
   }
   cache->length += seq;                        /* model.js:146 */
 
   if (logits) {                                /* model.js:151-157, 218-228 */
+    float* normed = (float*)malloc(sizeof(float) * d);
     or_rmsnorm(x + (size_t)(seq - 1) * d, m->final_norm, cfg->eps, d, normed);
     if (m->lm_head_f32) or_matvec(m->lm_head_f32, normed, cfg->vocab, d, NULL, logits);
     else or_matvec_bf16(m->embed_bf16, normed, cfg->vocab, d, logits);
+    free(normed);
   }
 
-  free(x); free(normed); free(q); free(k); free(v); free(attn); free(scores);
-  free(gate); free(up); free(projected); free(inv);
+  free(x); free(q); free(k); free(v); free(attn); free(scores); free(inv);
   return 0;
 }
 

@@ -101,6 +101,17 @@ int or_cache_write(or_cache* c, int layer, int at, const float* k, const float* 
                    int kv_f16);
 /* [kv_heads, length, head_dim] per layer (cache.js:97-115). */
 void or_cache_present(const or_cache* c, int layer, float* key, float* value);
+/* Positions below `positions` keep what or_cache_write put there when a forward pass appends
+ * over them: the pass computes its own keys and values for those positions but attends to the
+ * loaded ones. With a device's f16 cache loaded this way, the CPU path and the device read the
+ * same K/V at every position, so their difference is each position's own arithmetic, not a
+ * cache entry that rounded to the neighbouring f16 value on one side (the same-input
+ * comparison of web/kernels.html:51-54, applied to a whole forward pass). 0 (the default)
+ * is the reference's cache. No counterpart in src/cpu/cache.js. */
+void or_cache_pin(or_cache* c, int positions);
+/* What forward passes computed for pinned rows 0..n-1 of `layer` (unrounded f32, in the present
+ * layout [kv_heads, n, head_dim]); -3 when nothing is pinned or n exceeds the pinned rows. */
+int or_cache_shadow(const or_cache* c, int layer, int n, float* key, float* value);
 
 /*
  * ReferenceModel.forward (model.js:55-166) over `seq` token ids continuing from `cache`.

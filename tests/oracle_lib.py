@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         "or_cache_set_length": ([vp, i32], None),
         "or_cache_present": ([vp, i32, vp, vp], None),
         "or_cache_write": ([vp, i32, i32, vp, vp, i32, i32], i32),
+        "or_cache_pin": ([vp, i32], None),
+        "or_cache_shadow": ([vp, i32, i32, vp, vp], i32),
         "or_forward": ([vp, vp, vp, i32, vp], i32),
         "or_forward_hidden": ([vp, vp, vp, i32, vp], i32),
         "or_argmax": ([vp, i32], ctypes.c_int32),
@@ -356,6 +358,35 @@ class OracleCache:
         rc = lib().or_cache_write(self.h, layer, at, P(c32(k)), P(c32(v)), count, 1 if kv_f16 else 0)
         if rc:
             raise ValueError("cache write outside the capacity")
+
+    def pin(self, positions):
+        """Positions below `positions` keep their loaded contents when a forward appends over
+        them (or_cache_pin): the same-input comparison of web/kernels.html:51-54."""
+        lib().or_cache_pin(self.h, positions)
+
+    def shadow(self, layer, n):
+        """{key, value} [kv_heads, n, head_dim]: what forward passes computed (unrounded f32)
+        for pinned rows 0..n-1 of `layer`."""
+        c = self.model.cfg
+        k = np.empty((c.kv_heads, n, c.head_dim), np.float32)
+        v = np.empty_like(k)
+        if lib().or_cache_shadow(self.h, layer, n, P(k), P(v)):
+            raise ValueError("no shadow rows: pin the cache and run a forward over them first")
+        return {"key": k, "value": v}
+
+    def load_device(self, device_cache, positions, pin=False):
+        """Copy the first `positions` K/V rows of every layer from a device cache (its f16
+        values, widened exactly) into this cache, and set the length to `positions`; with
+        `pin`, a later forward over those positions attends to these rows, not its own."""
+        c = self.model.cfg
+        for L in range(c.layers):
+            p = device_cache.present(L)
+            k = np.ascontiguousarray(p["key"][:, :positions].transpose(1, 0, 2).reshape(positions, -1))
+            v = np.ascontiguousarray(p["value"][:, :positions].transpose(1, 0, 2).reshape(positions, -1))
+            self.write(L, 0, k, v, positions)
+        self.length = positions
+        if pin:
+            self.pin(positions)
 
     def present(self, layer):
         c = self.model.cfg

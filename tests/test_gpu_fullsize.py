@@ -1,0 +1,295 @@
+"""The benchmark configurations at their stated sizes against the CPU oracle, and the decode
+step's own launches one by one.
+
+Tolerances are the reference's (test/model.test.js:39-40, web/kernels.html:134): logits 1e-4
+relative (max-abs over max |ref|), per-layer 5e-4, a kernel against the CPU on the same inputs
+1e-5, greedy tokens exact. Two comparisons are made where an f16 cache is involved:
+  - independent: the oracle runs the whole prompt itself with its own f16 cache;
+  - same-f16 (web/kernels.html:51-54): the oracle attends to the device's own f16 K/V rows
+    (OracleCache.load_device with pin), so a cache entry that rounded to the neighbouring f16
+    value on one side cannot move the comparison; what remains is each position's arithmetic.
+"""
+import time
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_REL = 1e-4      # test/model.test.js:40
+LAYER_REL = 5e-4      # test/model.test.js:39
+KERNEL_REL = 1e-5     # web/kernels.html:134
+
+
+def rel_err(got, ref):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / np.max(np.abs(ref)))
+
+
+def cosine(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def say(msg):
+    print(f"[{time.strftime('%H:%M:%S')}] {msg}", flush=True)
+
+
+def top2_margin(logits):
+    top = np.partition(np.asarray(logits, np.float64), -2)[-2:]
+    return float(top[1] - top[0])
+
+
+@pytest.fixture(scope="module")
+def full_ckpt(hip):
+    return hip.synthesize_checkpoint(hip.QWEN25_05B, seed=1)
+
+
+def per_layer_present(cfg, gpu_cache, oracle_cache, upto):
+    """Per layer: max-abs relative and cosine of the device's f16 K/V against the oracle's."""
+    rows = []
+    for L in range(cfg.layers):
+        g, o = gpu_cache.present(L), oracle_cache.present(L)
+        for kind in ("key", "value"):
+            a, b = g[kind][:, :upto], o[kind][:, :upto]
+            rows.append((L, kind, rel_err(a, b), cosine(a, b)))
+    return rows
+
+
+def same_f16_layers(cfg, gpu_cache, pinned_cache, upto, label):
+    """The device's stored f16 K/V of every layer against what the same-f16 oracle computed for
+    the same rows, unrounded (OracleCache.shadow): each entry within half an f16 unit of the CPU's
+    value plus the kernel tolerance of the layer's largest, so the per-layer max-abs relative is
+    within the reference's 5e-4. Returns the worst per-layer relative and cosine."""
+    worst, min_cos = 0.0, 1.0
+    for L in range(cfg.layers):
+        g, o = gpu_cache.present(L), pinned_cache.shadow(L, upto)
+        for kind in ("key", "value"):
+            a, b = g[kind][:, :upto].astype(np.float64), o[kind].astype(np.float64)
+            half = 0.5 * np.spacing(np.abs(b).astype(np.float16)).astype(np.float64)
+            excess = np.abs(a - b) - half - KERNEL_REL * np.max(np.abs(b))
+            assert np.all(excess <= 0), (label, L, kind, float(np.max(excess)))
+            worst, min_cos = max(worst, rel_err(a, b)), min(min_cos, cosine(a, b))
+    say(f"{label}: device f16 K/V vs the CPU's unrounded values (same-f16 run): per-layer max-abs rel "
+        f"{worst:.2e}, min cosine {min_cos:.9f}")
+    assert worst <= LAYER_REL
+    return worst, min_cos
+
+
+# ------------------------------------------------------------------------------- config 4
+
+@pytest.mark.timeout(600)
+def test_config4_1024_prompt_and_256_graph_replayed_greedy_tokens(ctx, hip, full_ckpt):
+    """BASELINE config 4 as the bench runs it: int4-g128 layers, int8 head, f16 cache, a seeded
+    1024-token prompt prefilled (8-position batched tiles), then 256 greedy tokens by hipGraph
+    replay (runs of 8 steps per graph launch). Checks:
+      - prompt logits vs the oracle's own 1024-token prefill within 1e-4, same argmax; per-layer
+        present K/V max-abs and cosine reported;
+      - the prompt against the same-f16 oracle: logits within 1e-4, and every layer's stored
+        f16 K/V within half an f16 unit of the CPU's value (per-layer max-abs within 5e-4);
+      - every one of the 256 tokens against the oracle continuing from the device's cache,
+        teacher-forced (each step is fed the device's previous token, so one flip would not
+        hide the rest), with the top-2 logit margin of every step reported
+        (src/cpu/model.js:174-187, test/model.test.js:138-152)."""
+    cfg = hip.QWEN25_05B
+    P, STEPS = 1024, 256
+    say("config4: loading the int4 model")
+    model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int4", 128, "int8", maxPositions=P + STEPS + 8)
+    prompt = hip.synth_tokens(1, "config4.prompt", cfg.vocab, P)      # the bench's prompt
+    cache = model.newCache(P + STEPS + 1)
+    out = model.forward_tokens(prompt, cache)
+    model.decode_prepare(cache)
+    tokens = model.decode(cache, out["argmax"], STEPS)
+    say(f"config4: device prefill + {STEPS} decode steps done, first token {out['argmax']}")
+
+    oracle = O.OracleModel(cfg, full_ckpt, scheme="int4", group=128, lm_head="int8", kv_f16=True)
+    ocache = oracle.new_cache(P + 1)
+    t0 = time.perf_counter()
+    ologits = oracle.forward(prompt, ocache)
+    err = rel_err(out["logits"], ologits)
+    say(f"config4: oracle prefill of {P} in {time.perf_counter() - t0:.1f}s; prompt logits rel {err:.2e}, "
+        f"cosine {cosine(out['logits'], ologits):.9f}, argmax {out['argmax']} vs {O.argmax(ologits)}")
+    layers = per_layer_present(cfg, cache, ocache, P)
+    worst = max(r[2] for r in layers)
+    for L, kind, e, c in layers:
+        if L in (0, 11, 23):
+            say(f"config4: layer {L} {kind}: max-abs rel {e:.2e}, cosine {c:.9f}")
+    say(f"config4: per-layer present worst max-abs rel {worst:.2e}, min cosine {min(r[3] for r in layers):.9f}")
+    assert err <= LOGIT_REL
+    assert out["argmax"] == O.argmax(ologits)
+    assert min(r[3] for r in layers) >= 0.99999
+    del ocache
+
+    # The whole prompt against the same-f16 oracle (attending to the device's 1024 rows).
+    scache = oracle.new_cache(P + STEPS + 1)
+    scache.load_device(cache, P, pin=True)
+    scache.length = 0
+    slogits = oracle.forward(prompt, scache)
+    serr = rel_err(out["logits"], slogits)
+    say(f"config4: prompt logits vs the same-f16 oracle: rel {serr:.2e}")
+    assert serr <= LOGIT_REL
+    same_f16_layers(cfg, cache, scache, P, "config4")
+
+    # 256 teacher-forced steps continuing from the device's cache (the pinned prompt rows).
+    fed = [out["argmax"]] + list(tokens[:-1])
+    t0 = time.perf_counter()
+    margins, mismatches = [], []
+    for i in range(STEPS):
+        logits = oracle.forward([fed[i]], scache)
+        want = O.argmax(logits)
+        margins.append(top2_margin(logits))
+        if want != tokens[i]:
+            mismatches.append((i, int(tokens[i]), want, margins[-1]))
+        if i % 64 == 63:
+            say(f"config4: {i + 1}/{STEPS} teacher-forced steps, {len(mismatches)} mismatches")
+    m = np.array(margins)
+    say(f"config4: {STEPS - len(mismatches)}/{STEPS} greedy tokens equal in "
+        f"{time.perf_counter() - t0:.1f}s; top-2 margin min {m.min():.3e} (step {int(m.argmin())}), "
+        f"median {np.median(m):.3e}; margins < 1e-3: {int(np.sum(m < 1e-3))}")
+    print("config4 top-2 margins per step:", " ".join(f"{v:.2e}" for v in m), flush=True)
+    assert not mismatches, mismatches
+    cache.destroy()
+    model.destroy()
+
+
+# ------------------------------------------------------------------------------- config 5
+
+@pytest.mark.timeout(600)
+def test_config5_512_prefill_batched_and_mfma_match_oracle(ctx, hip, full_ckpt):
+    """a seeded 512-token prompt, int8 layers and head, f16 cache, through
+    the 8-position batched tiles and through the MFMA contraction + flash attention.
+      - batched: logits within 1e-4 of the oracle's own prefill (bitwise equal to one decode
+        step per position, tested elsewhere);
+      - MFMA: within 1e-4 of the same-f16 oracle (the oracle attending to the MFMA run's own
+        cache rows), same argmax; its distance from the independent oracle is reported, and
+        the same-f16 comparison of the batched path is given beside it;
+      - both: every layer's stored f16 K/V within half an f16 unit of the CPU's value."""
+    cfg = hip.QWEN25_05B
+    P = 512
+    model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int8", 128, "int8", maxPositions=P + 8)
+    prompt = hip.synth_tokens(1, "config5.prompt", cfg.vocab, P)     # the bench's prompt
+    runs = {}
+    for mode in ("batched", "mfma"):
+        model.set_matmul(mode)
+        c = model.newCache(P)
+        runs[mode] = (model.forward_tokens(prompt, c), c)
+    oracle = O.OracleModel(cfg, full_ckpt, scheme="int8", lm_head="int8", kv_f16=True)
+    t0 = time.perf_counter()
+    ologits = oracle.forward(prompt, oracle.new_cache(P))
+    say(f"config5: oracle prefill of {P} in {time.perf_counter() - t0:.1f}s")
+    res = {}
+    for mode, (r, c) in runs.items():
+        same = oracle.new_cache(P)
+        same.load_device(c, P, pin=True)
+        same.length = 0
+        slogits = oracle.forward(prompt, same)
+        res[mode] = (rel_err(r["logits"], ologits), rel_err(r["logits"], slogits))
+        say(f"config5 {mode}: logits rel {res[mode][0]:.2e} vs the oracle, {res[mode][1]:.2e} vs the same-f16 "
+            f"oracle; argmax {r['argmax']} vs {O.argmax(ologits)}")
+        assert r["argmax"] == O.argmax(ologits)
+        assert res[mode][1] <= LOGIT_REL
+        same_f16_layers(cfg, c, same, P, f"config5 {mode}")
+    assert res["batched"][0] <= LOGIT_REL
+    for _, c in runs.values():
+        c.destroy()
+    model.destroy()
+
+
+# ------------------------------------------------------------------- decode launches one by one
+
+@pytest.mark.parametrize("numerics", ["fast", "exact"])
+def test_decode_launches_match_oracle_at_full_shape(ctx, hip, full_ckpt, numerics):
+    """Each fused launch of the decode step (the kernels the headline runs) at the full
+    Qwen2.5-0.5B shape, int4-g128 layers and int8 head, context 1024, against the CPU path's
+    arithmetic on the same inputs (the per-kernel harness of web/kernels.html:56-134), within
+    1e-5 relative:
+      qkv        rmsnorm + q|k|v + bias + rope -> q; the f16 K/V row within half an f16 unit
+                 of the CPU's f32 value (+1e-5 of the largest)
+      attention + o-projection   split-K slots (FAST) merged in the o-projection's staging
+      gate/up    rmsnorm + gate|up + swiglu
+      down       down projection + residual
+      head       final rmsnorm + lm_head + argmax (the pick)."""
+    cfg = hip.QWEN25_05B
+    d, kv, ffn = cfg.hidden, cfg.kv_dim, cfg.intermediate
+    P = 1024
+    model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int4", 128, "int8", maxPositions=P + 8,
+                                         numerics=numerics)
+    cache = model.newCache(P + 4)
+    model.forward_tokens(hip.synth_tokens(3, "roles.prompt", cfg.vocab, P), cache)
+    inv = O.rope_freqs(64, cfg.rope_theta)
+    rng = np.random.default_rng(7)
+
+    def deq4(name):
+        w = O.bf16_to_f32(full_ckpt[name])
+        return O.round_trip(w, "int4", 128)
+
+    def f32(name):
+        return O.bf16_to_f32(full_ckpt[name])
+
+    worst = {}
+
+    def check(role, got, want, tol=KERNEL_REL):
+        e = rel_err(got, want)
+        worst[role] = max(worst.get(role, 0.0), e)
+        assert e <= tol, (role, e)
+
+    for L in (0, 11, 23):
+        p = f"model.layers.{L}."
+        x0 = (rng.standard_normal(d) * 0.7).astype(np.float32)
+        # qkv
+        cache.vector("x", x0)
+        model.decode_role(cache, "qkv", L)
+        q_g, k_g, v_g = cache.vector("q"), cache.vector("key", layer=L), cache.vector("value", layer=L)
+        xn = O.rmsnorm(x0, f32(p + "input_layernorm.weight"), cfg.eps)
+        q_o = O.matvec(deq4(p + "self_attn.q_proj.weight"), xn, d, d, f32(p + "self_attn.q_proj.bias"))
+        k_o = O.matvec(deq4(p + "self_attn.k_proj.weight"), xn, kv, d, f32(p + "self_attn.k_proj.bias"))
+        v_o = O.matvec(deq4(p + "self_attn.v_proj.weight"), xn, kv, d, f32(p + "self_attn.v_proj.bias"))
+        for h in range(cfg.heads):
+            O.rope_inplace(q_o, h * 64, 64, P, inv)
+        for h in range(cfg.kv_heads):
+            O.rope_inplace(k_o, h * 64, 64, P, inv)
+        check("qkv", q_g, q_o)
+        for g, o in ((k_g, k_o), (v_g, v_o)):
+            half_ulp = 0.5 * np.spacing(np.abs(o).astype(np.float16)).astype(np.float64)
+            assert np.all(np.abs(g.astype(np.float64) - o) <= half_ulp + KERNEL_REL * np.max(np.abs(o))), L
+        # attention + o-projection over positions 0..P (the row just written included)
+        cache.vector("x", np.zeros(d, np.float32))
+        model.decode_role(cache, "attention", L)
+        model.decode_role(cache, "oproj", L)
+        x_g = cache.vector("x")
+        pres = cache.present(L)
+        keys = np.concatenate([pres["key"].transpose(1, 0, 2).reshape(P, kv), k_g[None]], 0)
+        vals = np.concatenate([pres["value"].transpose(1, 0, 2).reshape(P, kv), v_g[None]], 0)
+        att = O.grouped_attention(q_g, keys, vals, 1, P, cfg.heads, cfg.kv_heads, 64)
+        proj = O.matvec(deq4(p + "self_attn.o_proj.weight"), att, d, d)
+        check("attention+oproj", x_g, proj)
+        # gate/up + swiglu
+        cache.vector("x", x0)
+        model.decode_role(cache, "gateup", L)
+        h_g = cache.vector("h")
+        xn = O.rmsnorm(x0, f32(p + "post_attention_layernorm.weight"), cfg.eps)
+        gate = O.matvec(deq4(p + "mlp.gate_proj.weight"), xn, ffn, d)
+        up = O.matvec(deq4(p + "mlp.up_proj.weight"), xn, ffn, d)
+        check("gateup", h_g, O.swiglu(gate, up))
+        # down + residual (onto x = x0)
+        cache.vector("x", x0)
+        model.decode_role(cache, "down", L)
+        x_g = cache.vector("x")
+        down = O.matvec(deq4(p + "mlp.down_proj.weight"), h_g, d, ffn)
+        want = (x0.astype(np.float64) + down.astype(np.float64)).astype(np.float32)
+        check("down", x_g - x0, want - x0)
+    # output head + argmax
+    x0 = (rng.standard_normal(d) * 0.7).astype(np.float32)
+    cache.vector("x", x0)
+    tok = model.decode_role(cache, "head")
+    logits_g = cache.vector("logits")
+    xn = O.rmsnorm(x0, f32("model.norm.weight"), cfg.eps)
+    lm = O.round_trip(O.bf16_to_f32(full_ckpt["model.embed_tokens.weight"]), "int8")
+    logits_o = O.matvec(lm, xn, cfg.vocab, d)
+    check("head", logits_g, logits_o)
+    assert tok == O.argmax(logits_g) == O.argmax(logits_o)
+    say(f"decode launches ({numerics}) worst rel vs the CPU: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
+    cache.destroy()
+    model.destroy()

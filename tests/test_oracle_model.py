@@ -212,3 +212,66 @@ def test_forward_matches_float64_rederivation(model):
     rel = np.max(np.abs(logits - ref)) / np.max(np.abs(ref))
     assert rel < 2e-6, rel
     assert O.argmax(logits) == int(np.argmax(ref))
+
+
+# ------------------------------------------------- same-input comparison (pinned rows)
+
+class _DeviceLike:
+    """A cache-shaped source of rows for OracleCache.load_device (present() per layer)."""
+
+    def __init__(self, presents):
+        self.presents = presents
+
+    def present(self, layer):
+        return self.presents[layer]
+
+
+def test_pinned_rows_with_the_oracles_own_values_reproduce_its_forward_bitwise():
+    """Pinning a cache loaded with exactly the rows the forward would write changes nothing:
+    same logits bit for bit. The shadow rows are the unrounded values: their f16 rounding is the
+    f16-cache run's present at every layer, and at layer 0 (whose input does not depend on the
+    cache) they equal an f32-cache run's present."""
+    cfg = tiny_cfg()
+    ck = tiny_ckpt(cfg, seed=5)
+    ids = np.arange(1, 20, dtype=np.int32) * 7 % cfg.vocab
+    m16 = O.OracleModel(cfg, ck, kv_f16=True)
+    m32 = O.OracleModel(cfg, ck, kv_f16=False)
+    c16 = m16.new_cache(32)
+    want = m16.forward(ids, c16)
+    c32 = m32.new_cache(32)
+    m32.forward(ids, c32)
+    pinned = m16.new_cache(32)
+    pinned.load_device(_DeviceLike([c16.present(L) for L in range(cfg.layers)]), ids.size, pin=True)
+    pinned.length = 0
+    got = m16.forward(ids, pinned)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    for L in range(cfg.layers):
+        sh, p32, p16 = pinned.shadow(L, ids.size), c32.present(L), c16.present(L)
+        for kind in ("key", "value"):
+            if L == 0:
+                np.testing.assert_array_equal(sh[kind].view(np.uint32), p32[kind].view(np.uint32))
+            np.testing.assert_array_equal(O.through_f16(sh[kind]).view(np.uint32), p16[kind].view(np.uint32))
+            assert not np.array_equal(sh[kind], p16[kind])     # unrounded, not the stored f16
+
+
+def test_pinned_rows_are_attended_to_and_kept():
+    """A forward over pinned positions attends to the loaded rows (a perturbed row changes the
+    logits) and leaves them in place; unpinned positions are written as usual."""
+    cfg = tiny_cfg()
+    ck = tiny_ckpt(cfg, seed=6)
+    ids = np.arange(3, 15, dtype=np.int32) * 5 % cfg.vocab
+    m = O.OracleModel(cfg, ck, kv_f16=True)
+    c = m.new_cache(16)
+    base = m.forward(ids, c)
+    presents = [c.present(L) for L in range(cfg.layers)]
+    presents[0]["value"][:, 2] += 0.25            # position 2 of layer 0, every kv head
+    pinned = m.new_cache(16)
+    pinned.load_device(_DeviceLike(presents), 6, pin=True)   # rows 0..5 pinned
+    pinned.length = 0
+    got = m.forward(ids, pinned)
+    assert not np.array_equal(got, base)
+    np.testing.assert_array_equal(pinned.present(0)["value"][:, :6], presents[0]["value"][:, :6])
+    # rows past the pin are the pass's own: layer 0's keys there do not depend on any cache row
+    np.testing.assert_array_equal(pinned.present(0)["key"][:, 6:], c.present(0)["key"][:, 6:])
+    with pytest.raises(ValueError):
+        m.new_cache(4).shadow(0, 1)       # nothing pinned
