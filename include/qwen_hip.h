@@ -118,6 +118,16 @@ int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_
  * [M, rows]. */
 int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
                       float* d_y, int32_t M);
+/* qh_matmul_prefill without any allocation: no counterpart in the reference; for callers that
+ * cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses
+ * that forbid it). The same kernels and results, bit for bit, with the digit planes, row factors
+ * and split partials in a 24 MiB array the library holds on each device from qh_open until the
+ * process ends, instead of a temporary allocation per call. Shapes whose scratch exceeds it are
+ * QH_ERR_RANGE (every M <= 512 with cols <= 8192 fits). Every call on one device shares that
+ * array: calls that overlap on one GPU (another stream, another context) race; calls in order on
+ * one stream do not. */
+int qh_matmul_prefill_noalloc(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+                              float* d_y, int32_t M);
 /* The isolated-matvec form: f16 activation x [cols], f32 y [rows]. */
 int qh_matvec_xh(qh_ctx* ctx, const qh_weight* w, const uint16_t* d_x, float* d_y);
 /* A list of `count` same-shape matrices in one launch: weight i starts at

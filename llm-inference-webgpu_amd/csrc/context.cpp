@@ -6,9 +6,48 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "qh_internal.h"
+
+namespace {
+
+// Scratch of qh_matmul_prefill_noalloc, the entry point that allocates nothing: one array on
+// every device the library runs on, held until the process ends. The row kernel writes the
+// activation digit planes and row factors into it and the contraction its split partials; each
+// launch writes before it reads, so nothing in it has to start at zero. 24 MiB covers the digit
+// planes of 512 rows of up to 8192 columns (12 MiB) plus the split partials, which stay within
+// one 64 x 128 f32 tile per CU (256 x 32 KiB = 8 MiB) whatever the shape.
+constexpr size_t kNoAllocScratchBytes = size_t(24) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// The array's device address per device. On the host, `scratch` only names the symbol; kernels
+// and copies get the address hipGetSymbolAddress returns with that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices] = {};
+hipError_t g_noalloc_err[kMaxDevices] = {};
+
+// With `device` current: the address of its copy of `scratch` (resolved once per device), or
+// nullptr and the lookup's error.
+void* noalloc_scratch(int device, hipError_t* err) {
+  if (device < 0 || device >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (!g_noalloc_ptr[device] && g_noalloc_err[device] == hipSuccess) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && ptr) g_noalloc_ptr[device] = ptr;
+    else g_noalloc_err[device] = e != hipSuccess ? e : hipErrorInvalidSymbol;
+  }
+  *err = g_noalloc_err[device];
+  return g_noalloc_ptr[device];
+}
+
+}  // namespace
 
 namespace qh {
 
@@ -119,6 +158,9 @@ int qh_open(int device, qh_ctx** out) {
     delete c;
     return fail(QH_ERR_NOMEM, "context scratch allocation failed");
   }
+  // The no-allocation entry point's scratch, resolved once per device at set-up; a failed
+  // lookup is reported by that entry point, not here.
+  c->noalloc_scratch = noalloc_scratch(device, &c->noalloc_err);
   *out = c;
   return QH_OK;
 }
@@ -264,27 +306,60 @@ int qh_matvec(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_
   return QH_OK;
 }
 
-int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
-                      float* d_y, int32_t M) {
+}  // extern "C"
+
+// The argument checks both forms of the MFMA prefill share.
+static int check_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_y, int32_t M,
+                                qh::DMat* m) {
   QH_CHECK(ctx, QH_ERR_INVALID, "context is NULL");
-  qh::DMat m;
-  int rc = qh::make_dmat(w, &m);
+  int rc = qh::make_dmat(w, m);
   if (rc) return rc;
-  QH_CHECK(m.format == QH_FMT_INT8 || m.format == QH_FMT_INT4, QH_ERR_INVALID,
-           "the MFMA prefill takes int8 or int4 weights (format %d given)", m.format);
-  QH_CHECK(m.cols % 32 == 0, QH_ERR_INVALID, "cols %d must be a multiple of 32", m.cols);
-  QH_CHECK(qh::matmul_prefill_supported(m), QH_ERR_INVALID,
-           "the MFMA prefill takes int8, or int4 in groups of a multiple of 64 columns, and at most "
-           "131072 columns (group %d, cols %d)", w->group, m.cols);
+  QH_CHECK(m->format == QH_FMT_INT8 || m->format == QH_FMT_INT4, QH_ERR_INVALID,
+           "the MFMA prefill takes int8 or int4 weights (format %d given)", m->format);
+  QH_CHECK(m->cols % 32 == 0, QH_ERR_INVALID, "cols %d must be a multiple of 32", m->cols);
+  QH_CHECK(qh::matmul_prefill_supported(*m), QH_ERR_INVALID,
+           "the MFMA prefill takes int8, or int4 in groups of a multiple of 64 columns (group %d, cols %d)",
+           w->group, m->cols);
+  QH_CHECK(m->cols <= 8192, QH_ERR_INVALID, "the MFMA prefill stages rows of at most 8192 columns (cols %d)",
+           m->cols);
   QH_CHECK(d_x && d_y, QH_ERR_INVALID, "matmul needs x and y");
   QH_CHECK(((uintptr_t)d_x & 15) == 0, QH_ERR_INVALID, "x must be 16-byte aligned");
   QH_CHECK(M >= 1, QH_ERR_INVALID, "M %d must be at least 1", M);
+  return QH_OK;
+}
+
+extern "C" {
+
+int qh_matmul_prefill(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+                      float* d_y, int32_t M) {
+  qh::DMat m;
+  int rc = check_matmul_prefill(ctx, w, d_x, d_y, M, &m);
+  if (rc) return rc;
   void* tmp = nullptr;
   const size_t scratch = qh::matmul_prefill_scratch_bytes(m, M);
   QH_HIP(hipMallocAsync(&tmp, scratch, ctx->stream));
   hipError_t e = qh::launch_matmul_prefill(ctx->stream, m, d_x, d_bias, d_y, M, tmp, scratch);
   QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
+  return QH_OK;
+}
+
+int qh_matmul_prefill_noalloc(qh_ctx* ctx, const qh_weight* w, const float* d_x, const float* d_bias,
+                              float* d_y, int32_t M) {
+  qh::DMat m;
+  int rc = check_matmul_prefill(ctx, w, d_x, d_y, M, &m);
+  if (rc) return rc;
+  // The digit planes alone grow with M: past the scratch they reject a large M before the
+  // partials' per-M scan below runs.
+  QH_CHECK(qh::digits_bytes(M, m.cols) <= kNoAllocScratchBytes &&
+               qh::matmul_prefill_scratch_bytes(m, M) <= kNoAllocScratchBytes,
+           QH_ERR_RANGE,
+           "the no-allocation MFMA prefill has %zu bytes of scratch; M %d x cols %d needs more "
+           "(every M <= 512 with cols <= 8192 fits)",
+           kNoAllocScratchBytes, M, m.cols);
+  QH_CHECK(ctx->noalloc_scratch, QH_ERR_DEVICE, "the no-allocation scratch of device %d is unavailable: %s",
+           ctx->device, hipGetErrorString(ctx->noalloc_err));
+  QH_HIP(qh::launch_matmul_prefill(ctx->stream, m, d_x, d_bias, d_y, M, ctx->noalloc_scratch, kNoAllocScratchBytes));
   return QH_OK;
 }
 

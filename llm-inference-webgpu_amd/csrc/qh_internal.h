@@ -70,6 +70,9 @@ struct qh_ctx {
   size_t scratch_bytes = 0;
   static constexpr size_t kScratchCounterBytes = 16384;
   int32_t* h_pinned = nullptr;  // 4-byte pinned readback slots
+  // This device's copy of the no-allocation entry point's static scratch (or nullptr, and why).
+  void* noalloc_scratch = nullptr;
+  hipError_t noalloc_err = hipSuccess;
 };
 
 struct qh_event {

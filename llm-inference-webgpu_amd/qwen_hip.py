@@ -215,7 +215,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_attention_splitk": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_attention_mfma": [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, i32],
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
-        "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32],
+        "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32], "qh_matmul_prefill_noalloc": [vp, vp, vp, vp, vp, i32],
         "qh_attention_splitk_list": [vp, vp, vp, vp, sz, sz, i32, i32, vp, i32, i32, i32, i32],
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
@@ -515,6 +515,11 @@ class GpuContext:
         """y [M, rows] = x [M, cols] . W^T (+ bias) on the int8 matrix cores (int8 / int4 weights)."""
         _check(self.lib.qh_matmul_prefill(self.handle, ctypes.byref(w), x.ptr,
                                           bias.ptr if bias else None, y.ptr, M))
+
+    def matmul_prefill_noalloc(self, w: Weight, x: DeviceBuffer, bias, y: DeviceBuffer, M: int) -> None:
+        """matmul_prefill with its scratch in the library's per-device static array (no allocation)."""
+        _check(self.lib.qh_matmul_prefill_noalloc(self.handle, ctypes.byref(w), x.ptr,
+                                                  bias.ptr if bias else None, y.ptr, M))
 
     def matvec_xh_list(self, w: Weight, count: int, data_stride: int, scale_stride: int,
                        x: DeviceBuffer, x_stride: int, y: DeviceBuffer) -> None:
