@@ -303,6 +303,9 @@ int qh_model_finalize(qh_model* m);
 int qh_model_free(qh_model* m);
 /* Device bytes held by the model's weights. */
 int qh_model_bytes(qh_model* m, size_t* bytes);
+/* The dimensions the model was created with (for bindings that size their outputs from the
+ * model itself; the reference's GpuModel keeps its `config`, src/gpu/model.js:88). */
+int qh_model_config(qh_model* m, qh_config* out);
 
 int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out);  /* model.js:209 */
 int qh_cache_free(qh_cache* c);

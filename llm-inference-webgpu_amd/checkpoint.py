@@ -1,144 +1,174 @@
-"""Safetensors checkpoints for the load path (src/core/safetensors.js:1-160).
+"""Safetensors checkpoints for the load path.
 
-The container: a little-endian u64 header length, a JSON header mapping tensor names
-to {dtype, shape, data_offsets}, then the tensor bytes back to back. ``Safetensors.open``
-validates the header against the file the way the reference does (safetensors.js:56-125)
-and maps the data section read-only, so a tensor's bytes are handed to the device
-loader (qh_model_load_tensor) straight from the page cache: nothing is widened or copied
-on the host, and at most one tensor's pages are touched at a time.
+The container, as the safetensors format defines it: an unsigned 64-bit little-endian
+byte count N, N bytes of UTF-8 JSON, then one byte buffer. The JSON object maps each
+tensor name to ``{"dtype": <element type>, "shape": [dims], "data_offsets": [start,
+stop]}`` with the offsets counted from the start of the buffer; an optional
+``"__metadata__"`` entry maps strings to strings.
+
+``Safetensors.open`` checks the whole header against the file before anything is read
+and reports every defect it finds in one error (a checkpoint with a bad record usually
+has more than one). The buffer is then memory-mapped read-only, so a tensor's bytes go
+to the device loader (qh_model_load_tensor) straight from the page cache, one tensor at
+a time. The reader's methods carry the names of the reference's reader that callers use
+(names / has / info / read_raw, src/core/safetensors.js); the checks and messages are
+this module's own.
 """
 from __future__ import annotations
 
 import json
 import os
+from dataclasses import dataclass
 
 import numpy as np
 
-# Bytes per element of every dtype safetensors defines (safetensors.js:15-21).
-DTYPE_SIZE = {
+# Bytes per element of each element type of the format.
+ELEMENT_BYTES = {
     "BOOL": 1, "U8": 1, "I8": 1, "F8_E4M3": 1, "F8_E5M2": 1,
     "I16": 2, "U16": 2, "F16": 2, "BF16": 2,
     "I32": 4, "U32": 4, "F32": 4,
     "I64": 8, "U64": 8, "F64": 8,
 }
-# The element views the loader hands on: bf16 and f16 as their bits.
-VIEW = {"BF16": np.uint16, "F16": np.uint16, "F32": np.float32}
+# How the loader hands on the element types it reads: 16-bit floats as their bits.
+LOADER_VIEWS = {"BF16": np.uint16, "F16": np.uint16, "F32": np.float32}
+# Headers beyond this are refused outright (the format's own readers cap them too).
+HEADER_LIMIT = 100 << 20
 
 
 class SafetensorsError(ValueError):
     pass
 
 
+@dataclass(frozen=True)
 class TensorInfo:
-    __slots__ = ("name", "dtype", "shape", "begin", "end")
-
-    def __init__(self, name, dtype, shape, begin, end):
-        self.name, self.dtype, self.shape, self.begin, self.end = name, dtype, tuple(shape), begin, end
+    name: str
+    dtype: str
+    shape: tuple
+    begin: int   # offset of the first byte within the buffer
+    end: int     # one past the last byte
 
     @property
     def numel(self) -> int:
-        n = 1
-        for d in self.shape:
-            n *= d
-        return n
+        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
 
     @property
     def byte_length(self) -> int:
         return self.end - self.begin
 
 
-def _int(v) -> bool:
-    return isinstance(v, int) and not isinstance(v, bool)
+def _is_count(v) -> bool:
+    """A non-negative integer (JSON booleans are not counts)."""
+    return isinstance(v, int) and not isinstance(v, bool) and v >= 0
+
+
+def _record_defects(name, record, buffer_bytes):
+    """(TensorInfo or None, [defects]) for one header record."""
+    if not isinstance(record, dict):
+        return None, [f"'{name}': the record is a JSON {type(record).__name__}, not an object"]
+    defects = []
+    dtype, shape, span = record.get("dtype"), record.get("shape"), record.get("data_offsets")
+    if dtype not in ELEMENT_BYTES:
+        defects.append(f"'{name}': {dtype!r} is not a safetensors element type")
+    if not (isinstance(shape, list) and all(_is_count(d) for d in shape)):
+        defects.append(f"'{name}': dimensions {shape!r} are not a list of non-negative integers")
+    if not (isinstance(span, list) and len(span) == 2 and all(_is_count(v) for v in span) and span[0] <= span[1]):
+        defects.append(f"'{name}': data_offsets {span!r} is not [start, stop] with 0 <= start <= stop")
+    if defects:
+        return None, defects
+    info = TensorInfo(name, dtype, tuple(shape), span[0], span[1])
+    if info.end > buffer_bytes:
+        return None, [f"'{name}': bytes [{info.begin}, {info.end}) extend past the {buffer_bytes}-byte buffer"]
+    need = info.numel * ELEMENT_BYTES[dtype]
+    if info.byte_length != need:
+        return None, [f"'{name}': {info.numel} x {dtype} is {need} bytes, the record spans {info.byte_length}"]
+    return info, []
 
 
 class Safetensors:
-    """Safetensors.open / names / has / info / readRaw (safetensors.js:36-160)."""
+    """A checked, memory-mapped safetensors file."""
 
-    def __init__(self, path, tensors, data_start, metadata, file_size):
+    def __init__(self, path, records, buffer_start, metadata, file_bytes):
         self.path, self.metadata = path, metadata
-        self._tensors, self._data_start, self._file_size = tensors, data_start, file_size
+        self._records, self._buffer_start, self._file_bytes = records, buffer_start, file_bytes
         self._map = None
 
     @staticmethod
     def open(path: str) -> "Safetensors":
-        size = os.path.getsize(path)
-        if size < 8:
-            raise SafetensorsError(f"not a safetensors file: {size} bytes")
+        file_bytes = os.path.getsize(path)
+        where = os.path.basename(path)
+        if file_bytes < 8:
+            raise SafetensorsError(f"{where}: {file_bytes} bytes is too short for a safetensors length prefix")
         with open(path, "rb") as f:
-            header_len = int.from_bytes(f.read(8), "little")
-            if header_len <= 0 or header_len > 2 ** 53 - 1 or 8 + header_len > size:
-                raise SafetensorsError(f"header length {header_len} does not fit in a {size}-byte file")
-            raw = f.read(header_len)
+            n = int.from_bytes(f.read(8), "little")
+            if n == 0 or n > min(file_bytes - 8, HEADER_LIMIT):
+                raise SafetensorsError(f"{where}: the length prefix declares a {n}-byte header, but "
+                                       f"{file_bytes - 8} bytes follow it (and headers are limited to "
+                                       f"{HEADER_LIMIT} bytes)")
+            text = f.read(n)
         try:
-            header = json.loads(raw.decode("utf-8"))
+            header = json.loads(text.decode("utf-8"))
         except (UnicodeDecodeError, ValueError) as e:
-            raise SafetensorsError(f"header is not valid UTF-8 JSON: {e}") from e
+            raise SafetensorsError(f"{where}: the header is not UTF-8 JSON ({e})") from e
         if not isinstance(header, dict):
-            raise SafetensorsError("header must be a JSON object")
+            raise SafetensorsError(f"{where}: the header is a JSON {type(header).__name__}, "
+                                   "not an object of tensor records")
+        buffer_start = 8 + n
+        buffer_bytes = file_bytes - buffer_start
+        defects = []
         metadata = header.pop("__metadata__", None)
-        data_start = 8 + header_len
-        data_size = size - data_start
-        tensors = {}
-        for name, entry in header.items():
-            entry = entry if isinstance(entry, dict) else {}
-            dtype, shape, offsets = entry.get("dtype"), entry.get("shape"), entry.get("data_offsets")
-            if dtype not in DTYPE_SIZE:
-                raise SafetensorsError(f"{name}: unknown dtype {json.dumps(dtype)}")
-            if not isinstance(shape, list) or not all(_int(d) and d >= 0 for d in shape):
-                raise SafetensorsError(f"{name}: shape must be an array of non-negative integers")
-            if not isinstance(offsets, list) or len(offsets) != 2:
-                raise SafetensorsError(f"{name}: data_offsets must be a pair")
-            begin, end = offsets
-            if not (_int(begin) and _int(end)) or begin < 0 or end < begin:
-                raise SafetensorsError(f"{name}: bad data_offsets [{begin}, {end}]")
-            if end > data_size:
-                raise SafetensorsError(f"{name}: ends at {end} but the data section is only {data_size} bytes")
-            info = TensorInfo(name, dtype, shape, begin, end)
-            if end - begin != info.numel * DTYPE_SIZE[dtype]:
-                raise SafetensorsError(f"{name}: shape {list(shape)} of {dtype} needs "
-                                       f"{info.numel * DTYPE_SIZE[dtype]} bytes but the header reserves "
-                                       f"{end - begin}")
-            tensors[name] = info
-        ranges = sorted(tensors.values(), key=lambda t: t.begin)
-        for a, b in zip(ranges, ranges[1:]):
+        if metadata is not None and not (isinstance(metadata, dict)
+                                         and all(isinstance(v, str) for v in metadata.values())):
+            defects.append("__metadata__ is not an object of strings")
+        records = {}
+        for name, record in header.items():
+            info, found = _record_defects(name, record, buffer_bytes)
+            defects += found
+            if info is not None:
+                records[name] = info
+        # Two records must never claim the same byte.
+        by_start = sorted((r for r in records.values() if r.byte_length), key=lambda r: (r.begin, r.end))
+        for a, b in zip(by_start, by_start[1:]):
             if b.begin < a.end:
-                raise SafetensorsError(f"{b.name} overlaps {a.name}")
-        return Safetensors(path, tensors, data_start, metadata, size)
+                defects.append(f"'{b.name}' [{b.begin}, {b.end}) overlaps '{a.name}' [{a.begin}, {a.end})")
+        if defects:
+            raise SafetensorsError(f"{where}: {len(defects)} defect{'s' if len(defects) > 1 else ''} in the "
+                                   "header: " + "; ".join(defects))
+        return Safetensors(path, records, buffer_start, metadata, file_bytes)
 
     def __len__(self) -> int:
-        return len(self._tensors)
+        return len(self._records)
 
     def names(self) -> list:
-        return list(self._tensors)
+        return list(self._records)
 
     def has(self, name: str) -> bool:
-        return name in self._tensors
+        return name in self._records
 
     def info(self, name: str) -> TensorInfo:
-        t = self._tensors.get(name)
-        if t is None:
-            raise SafetensorsError(f"no tensor named {json.dumps(name)}")
-        return t
+        try:
+            return self._records[name]
+        except KeyError:
+            raise SafetensorsError(f"{os.path.basename(self.path)} holds no tensor {name!r}") from None
 
     def read_raw(self, name: str) -> np.ndarray:
-        """The tensor's bytes exactly as stored (a read-only view of the file mapping)."""
+        """The tensor's bytes as stored: a read-only view of the file mapping."""
         t = self.info(name)
         if t.byte_length == 0:
             return np.zeros(0, np.uint8)
         if self._map is None:
-            self._map = np.memmap(self.path, np.uint8, "r", offset=self._data_start,
-                                  shape=(self._file_size - self._data_start,))
+            self._map = np.memmap(self.path, np.uint8, "r", offset=self._buffer_start,
+                                  shape=(self._file_bytes - self._buffer_start,))
         return self._map[t.begin:t.end]
 
     def array(self, name: str) -> np.ndarray:
-        """The tensor as its element view, shaped: BF16 and F16 as uint16 bits, F32 as float32."""
+        """The tensor in the loader's view, shaped: BF16 and F16 as uint16 bits, F32 as float32."""
         t = self.info(name)
-        view = VIEW.get(t.dtype)
+        view = LOADER_VIEWS.get(t.dtype)
         if view is None:
-            raise SafetensorsError(f"{name}: dtype {t.dtype} is not a weight format the loader reads")
+            raise SafetensorsError(f"{name}: the loader reads BF16, F16 and F32 tensors, not {t.dtype}")
         raw = self.read_raw(name)
         if raw.ctypes.data % np.dtype(view).itemsize:
-            raw = raw.copy()   # a misaligned tensor (the format does not promise alignment)
+            raw = raw.copy()   # the format does not promise aligned tensors
         return raw.view(view).reshape(t.shape)
 
     def close(self) -> None:
@@ -146,17 +176,15 @@ class Safetensors:
 
 
 def write(path: str, tensors: dict, metadata: dict | None = None) -> None:
-    """Write {name: (dtype, array)} as a safetensors file: the header padded with spaces to a
-    multiple of 8 bytes, tensors back to back in the given order. (For tests and tools that
-    make checkpoints; the reference only reads them.)"""
-    header, offset = {}, 0
-    blobs = []
+    """Write {name: (dtype, array)} as a safetensors file, tensors back to back in the given
+    order and the header padded with spaces to a multiple of 8 bytes (for tests and tools that
+    make checkpoints)."""
+    header, blobs, offset = {}, [], 0
     for name, (dtype, a) in tensors.items():
         a = np.ascontiguousarray(a)
-        n = a.nbytes
-        header[name] = {"dtype": dtype, "shape": list(a.shape), "data_offsets": [offset, offset + n]}
+        header[name] = {"dtype": dtype, "shape": list(a.shape), "data_offsets": [offset, offset + a.nbytes]}
         blobs.append(a)
-        offset += n
+        offset += a.nbytes
     if metadata is not None:
         header["__metadata__"] = metadata
     text = json.dumps(header).encode()

@@ -543,6 +543,12 @@ int qh_model_bytes(qh_model* m, size_t* bytes) {
   return QH_OK;
 }
 
+int qh_model_config(qh_model* m, qh_config* out) {
+  QH_CHECK(m && out, QH_ERR_INVALID, "model_config needs a model and an output");
+  *out = m->cfg;
+  return QH_OK;
+}
+
 int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   QH_CHECK(m && out, QH_ERR_INVALID, "cache_create needs a model and an output");
   *out = nullptr;

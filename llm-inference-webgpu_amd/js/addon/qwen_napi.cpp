@@ -78,34 +78,53 @@ bool to_str(napi_env env, napi_value v, std::string* out) {
   return true;
 }
 
-// The bytes of a typed array (null / undefined give nullptr).
-bool to_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+const char* type_name(napi_typedarray_type t) {
+  switch (t) {
+    case napi_int8_array: return "Int8Array";
+    case napi_uint8_array: return "Uint8Array";
+    case napi_uint16_array: return "Uint16Array";
+    case napi_int32_array: return "Int32Array";
+    case napi_float32_array: return "Float32Array";
+    default: return "a typed array";
+  }
+}
+
+// A typed array of exactly the element type `want` holding at least `need` elements; with
+// `optional`, null / undefined give nullptr. Anything else throws (TypeError for the wrong
+// kind of value, RangeError for too few elements), so no C entry point reads past a caller's
+// array.
+bool to_array(napi_env env, napi_value v, napi_typedarray_type want, const char* what, size_t need, bool optional,
+              void** data) {
   napi_valuetype t;
   napi_typeof(env, v, &t);
-  if (t == napi_null || t == napi_undefined) {
+  if (optional && (t == napi_null || t == napi_undefined)) {
     *data = nullptr;
-    if (bytes) *bytes = 0;
     return true;
   }
   bool is_ta = false;
   napi_is_typedarray(env, v, &is_ta);
-  if (!is_ta) {
-    napi_throw_type_error(env, nullptr, "expected a typed array");
-    return false;
-  }
-  napi_typedarray_type type;
+  napi_typedarray_type type = napi_int8_array;
   size_t length = 0, offset = 0;
   napi_value ab;
-  napi_get_typedarray_info(env, v, &type, &length, data, &ab, &offset);
-  size_t el = 1;
-  switch (type) {
-    case napi_int16_array: case napi_uint16_array: el = 2; break;
-    case napi_int32_array: case napi_uint32_array: case napi_float32_array: el = 4; break;
-    case napi_float64_array: el = 8; break;
-    default: el = 1;
+  if (is_ta) napi_get_typedarray_info(env, v, &type, &length, data, &ab, &offset);
+  if (!is_ta || type != want) {
+    const std::string msg = std::string(what) + " must be a " + type_name(want);
+    napi_throw_type_error(env, nullptr, msg.c_str());
+    return false;
   }
-  if (bytes) *bytes = length * el;
+  if (length < need) {
+    const std::string msg = std::string(what) + " holds " + std::to_string(length) + " values where " +
+                            std::to_string(need) + " are needed";
+    napi_throw_range_error(env, nullptr, msg.c_str());
+    return false;
+  }
   return true;
+}
+
+bool positive(napi_env env, int32_t rows, int32_t cols) {
+  if (rows >= 1 && cols >= 1) return true;
+  napi_throw_range_error(env, nullptr, "rows and cols must be positive");
+  return false;
 }
 
 template <typename T>
@@ -199,8 +218,9 @@ napi_value QuantizeInt8(napi_env env, napi_callback_info info) {  // (Float32Arr
   Args a;
   void* w;
   int32_t rows, cols;
-  if (!get_args(env, info, a, 3) || !to_bytes(env, a.v[0], &w, nullptr) || !to_i32(env, a.v[1], &rows) ||
-      !to_i32(env, a.v[2], &cols))
+  if (!get_args(env, info, a, 3) || !to_i32(env, a.v[1], &rows) || !to_i32(env, a.v[2], &cols) ||
+      !positive(env, rows, cols) ||
+      !to_array(env, a.v[0], napi_float32_array, "weights", (size_t)rows * cols, false, &w))
     return nullptr;
   void *q, *s;
   napi_value tq = typed(env, napi_int8_array, (size_t)rows * cols, 1, &q);
@@ -218,8 +238,9 @@ napi_value QuantizeInt4(napi_env env, napi_callback_info info) {  // (Float32Arr
   Args a;
   void* w;
   int32_t rows, cols, group;
-  if (!get_args(env, info, a, 4) || !to_bytes(env, a.v[0], &w, nullptr) || !to_i32(env, a.v[1], &rows) ||
-      !to_i32(env, a.v[2], &cols) || !to_i32(env, a.v[3], &group))
+  if (!get_args(env, info, a, 4) || !to_i32(env, a.v[1], &rows) || !to_i32(env, a.v[2], &cols) ||
+      !to_i32(env, a.v[3], &group) || !positive(env, rows, cols) ||
+      !to_array(env, a.v[0], napi_float32_array, "weights", (size_t)rows * cols, false, &w))
     return nullptr;
   if (group < 2 || cols % group) return fail(env, qh_quantize_int4(nullptr, rows, cols, group, nullptr, nullptr, nullptr));
   const size_t ng = (size_t)rows * (cols / group);
@@ -285,9 +306,38 @@ napi_value ModelSetTensor(napi_env env, napi_callback_info info) {
   void *data, *scales, *zeros;
   if (!get_args(env, info, a, 9) || !to_handle(env, a.v[0], &m) || !to_str(env, a.v[1], &name) ||
       !to_i32(env, a.v[2], &fmt) || !to_i32(env, a.v[3], &rows) || !to_i32(env, a.v[4], &cols) ||
-      !to_i32(env, a.v[5], &group) || !to_bytes(env, a.v[6], &data, nullptr) ||
-      !to_bytes(env, a.v[7], &scales, nullptr) || !to_bytes(env, a.v[8], &zeros, nullptr))
+      !to_i32(env, a.v[5], &group) || !positive(env, rows, cols))
     return nullptr;
+  // The arrays each format stores (qh_model_set_tensor): codes or values, then scales and
+  // zero points. An int4 group that does not divide the row is the C call's error to report.
+  const size_t n = (size_t)rows * cols;
+  const bool grouped = fmt == QH_FMT_INT4 && group > 0 && cols % group == 0;
+  const size_t groups = grouped ? (size_t)rows * (cols / group) : 0;
+  bool ok = true;
+  switch (fmt) {
+    case QH_FMT_F32:
+      ok = to_array(env, a.v[6], napi_float32_array, "data", n, false, &data);
+      scales = zeros = nullptr;
+      break;
+    case QH_FMT_F16:
+    case QH_FMT_BF16:
+      ok = to_array(env, a.v[6], napi_uint16_array, "data", n, false, &data);
+      scales = zeros = nullptr;
+      break;
+    case QH_FMT_INT8:
+      ok = to_array(env, a.v[6], napi_int8_array, "codes", n, false, &data) &&
+           to_array(env, a.v[7], napi_float32_array, "scales", (size_t)rows, false, &scales);
+      zeros = nullptr;
+      break;
+    case QH_FMT_INT4:
+      ok = to_array(env, a.v[6], napi_uint8_array, "codes", (n + 1) / 2, false, &data) &&
+           to_array(env, a.v[7], napi_float32_array, "scales", groups, false, &scales) &&
+           to_array(env, a.v[8], napi_float32_array, "zeros", groups, false, &zeros);
+      break;
+    default:
+      data = scales = zeros = nullptr;  // an unknown format: the C call reports it
+  }
+  if (!ok) return nullptr;
   QH_CALL(qh_model_set_tensor(m, name.c_str(), fmt, rows, cols, group, data, static_cast<const float*>(scales),
                               static_cast<const float*>(zeros)));
   return nullptr;
@@ -301,16 +351,14 @@ napi_value ModelLoadTensor(napi_env env, napi_callback_info info) {
   std::string name;
   int32_t src_fmt, rows, cols, fmt, group;
   void* data;
-  size_t bytes = 0;
   if (!get_args(env, info, a, 8) || !to_handle(env, a.v[0], &m) || !to_str(env, a.v[1], &name) ||
       !to_i32(env, a.v[2], &src_fmt) || !to_i32(env, a.v[3], &rows) || !to_i32(env, a.v[4], &cols) ||
-      !to_bytes(env, a.v[5], &data, &bytes) || !to_i32(env, a.v[6], &fmt) || !to_i32(env, a.v[7], &group))
+      !to_i32(env, a.v[6], &fmt) || !to_i32(env, a.v[7], &group) || !positive(env, rows, cols))
     return nullptr;
-  const size_t width = src_fmt == QH_FMT_BF16 ? 2 : 4;
-  if (rows < 1 || cols < 1 || bytes < (size_t)rows * cols * width) {
-    napi_throw_range_error(env, nullptr, "the data array is smaller than rows * cols values");
-    return nullptr;
-  }
+  // bf16 checkpoints arrive as their bits, f32 ones as values
+  const napi_typedarray_type want = src_fmt == QH_FMT_BF16 || src_fmt == QH_FMT_F16 ? napi_uint16_array
+                                                                                   : napi_float32_array;
+  if (!to_array(env, a.v[5], want, "data", (size_t)rows * cols, false, &data)) return nullptr;
   QH_CALL(qh_model_load_tensor(m, name.c_str(), src_fmt, rows, cols, data, fmt, group));
   return nullptr;
 }
@@ -365,27 +413,38 @@ napi_value CacheLength(napi_env env, napi_callback_info info) {  // (cache[, new
   return num(env, len);
 }
 
-// (model, cache, Int32Array ids | Float32Array hidden, seq, wantLogits, vocab) -> {logits, argmax}
+// (model, cache, Int32Array ids | Float32Array hidden [seq * hidden], seq, wantLogits) ->
+// {logits, argmax}; the logits array has the model's vocabulary size.
 napi_value Forward(napi_env env, napi_callback_info info) {
   Args a;
   qh_model* m;
   qh_cache* c;
   void* in;
-  int32_t seq, vocab;
+  int32_t seq;
   bool want = true;
-  if (!get_args(env, info, a, 6) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c) ||
-      !to_bytes(env, a.v[2], &in, nullptr) || !to_i32(env, a.v[3], &seq))
+  if (!get_args(env, info, a, 5) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c) ||
+      !to_i32(env, a.v[3], &seq))
     return nullptr;
   napi_get_value_bool(env, a.v[4], &want);
-  if (!to_i32(env, a.v[5], &vocab)) return nullptr;
-  napi_typedarray_type type;
-  size_t len, off;
-  void* d;
-  napi_value ab;
-  napi_get_typedarray_info(env, a.v[2], &type, &len, &d, &ab, &off);
+  qh_config cfg{};
+  QH_CALL(qh_model_config(m, &cfg));
+  bool is_ta = false;
+  napi_typedarray_type type = napi_float32_array;
+  napi_is_typedarray(env, a.v[2], &is_ta);
+  if (is_ta) {
+    size_t len, off;
+    napi_value ab;
+    napi_get_typedarray_info(env, a.v[2], &type, &len, &in, &ab, &off);
+  }
+  const size_t rows = seq > 0 ? (size_t)seq : 0;
+  if (type == napi_int32_array) {
+    if (!to_array(env, a.v[2], napi_int32_array, "token ids", rows, false, &in)) return nullptr;
+  } else if (!to_array(env, a.v[2], napi_float32_array, "hidden", rows * cfg.hidden, false, &in)) {
+    return nullptr;
+  }
   void* lp = nullptr;
   napi_value logits = nullptr;
-  if (want) logits = typed(env, napi_float32_array, (size_t)vocab, 4, &lp);
+  if (want) logits = typed(env, napi_float32_array, (size_t)cfg.vocab, 4, &lp);
   int32_t am = -1;
   if (type == napi_int32_array) {
     QH_CALL(qh_forward_tokens(m, c, static_cast<const int32_t*>(in), seq, static_cast<float*>(lp),
@@ -415,6 +474,31 @@ napi_value Decode(napi_env env, napi_callback_info info) {  // (model, cache, fi
   return out;
 }
 
+// (model, cache, layer) -> {key, value}: layer `layer`'s cache rows 0 .. length-1 as f32
+// [kv_heads, length, head_dim] (qh_cache_present).
+napi_value CachePresent(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  qh_cache* c;
+  int32_t layer, len = 0;
+  if (!get_args(env, info, a, 3) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c) ||
+      !to_i32(env, a.v[2], &layer))
+    return nullptr;
+  qh_config cfg{};
+  QH_CALL(qh_model_config(m, &cfg));
+  QH_CALL(qh_cache_length(c, &len));
+  const size_t n = (size_t)cfg.kv_heads * len * cfg.head_dim;
+  void *k, *v;
+  napi_value tk = typed(env, napi_float32_array, n, 4, &k);
+  napi_value tv = typed(env, napi_float32_array, n, 4, &v);
+  QH_CALL(qh_cache_present(c, layer, static_cast<float*>(k), static_cast<float*>(v)));
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "key", tk);
+  napi_set_named_property(env, o, "value", tv);
+  return o;
+}
+
 napi_value AbiVersion(napi_env env, napi_callback_info) { return num(env, qh_abi_version()); }
 
 }  // namespace
@@ -432,6 +516,7 @@ static napi_value Init(napi_env env, napi_value exports) {
              {"modelFinalize", ModelFinalize},
              {"modelFree", ModelFree},     {"cacheCreate", CacheCreate},
              {"cacheFree", CacheFree},     {"cacheLength", CacheLength},
+             {"cachePresent", CachePresent},
              {"forward", Forward},         {"decode", Decode}};
   for (const auto& f : fns) {
     napi_value v;

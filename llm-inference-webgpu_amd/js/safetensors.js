@@ -1,125 +1,200 @@
 'use strict';
-// Checkpoint files for the loader, for Node 12 (CommonJS, synchronous reads): a safetensors
-// reader with the validation of the reference's Safetensors.open (src/core/safetensors.js:56-125)
-// and the config checks of src/core/config.js:16-153. Tensors are read one at a time, as the
-// reference's loader reads them, and handed on as stored (bf16 bits, f16 bits or f32).
+// Safetensors checkpoints for the Node driver (Node 12: CommonJS, synchronous file reads).
+//
+// The container, as the safetensors format defines it: an unsigned 64-bit little-endian
+// byte count N, N bytes of UTF-8 JSON, then one byte buffer. The JSON object maps each
+// tensor name to {dtype, shape, data_offsets: [start, stop]} with the offsets counted from
+// the start of the buffer, and may carry "__metadata__" (an object of strings).
+//
+// Safetensors.open checks the whole header before anything is read and reports every
+// defect it finds in one error. The reader offers the methods the reference's callers use
+// (names / has / info / readRaw / readRawRange / readF32, src/core/safetensors.js); they
+// return their results directly, which `await` accepts as it accepts the reference's
+// promises. The checks and messages are this file's own.
 
 const fs = require('fs');
 const util = require('util');
 
-// Bytes per element of every dtype safetensors defines (safetensors.js:15-21).
-const DTYPE_SIZE = {
+// Bytes per element of each element type of the format.
+const ELEMENT_BYTES = {
   BOOL: 1, U8: 1, I8: 1, F8_E4M3: 1, F8_E5M2: 1,
   I16: 2, U16: 2, F16: 2, BF16: 2,
   I32: 4, U32: 4, F32: 4,
   I64: 8, U64: 8, F64: 8,
 };
+const HEADER_LIMIT = 100 * 1024 * 1024;  // headers beyond this are refused outright
 
-function isInt(v) { return Number.isSafeInteger(v); }
+function isCount(v) { return typeof v === 'number' && Number.isSafeInteger(v) && v >= 0; }
+function typeName(v) { return v === null ? 'null' : Array.isArray(v) ? 'array' : typeof v; }
+
+// {info, defects} for one header record; info is null when the record is unusable.
+function checkRecord(name, rec, bufferBytes) {
+  if (rec === null || typeof rec !== 'object' || Array.isArray(rec)) {
+    return { info: null, defects: ["'" + name + "': the record is a JSON " + typeName(rec) + ', not an object'] };
+  }
+  const defects = [];
+  const dtype = rec.dtype, shape = rec.shape, span = rec.data_offsets;
+  if (!Object.prototype.hasOwnProperty.call(ELEMENT_BYTES, dtype)) {
+    defects.push("'" + name + "': " + JSON.stringify(dtype) + ' is not a safetensors element type');
+  }
+  if (!Array.isArray(shape) || !shape.every(isCount)) {
+    defects.push("'" + name + "': dimensions " + JSON.stringify(shape) + ' are not a list of non-negative integers');
+  }
+  if (!Array.isArray(span) || span.length !== 2 || !span.every(isCount) || span[0] > span[1]) {
+    defects.push("'" + name + "': data_offsets " + JSON.stringify(span) + ' is not [start, stop] with 0 <= start <= stop');
+  }
+  if (defects.length) return { info: null, defects: defects };
+  const numel = shape.reduce(function (a, b) { return a * b; }, 1);
+  const info = { name: name, dtype: dtype, shape: shape.slice(), begin: span[0], end: span[1], numel: numel,
+                 byteLength: span[1] - span[0] };
+  if (info.end > bufferBytes) {
+    return { info: null, defects: ["'" + name + "': bytes [" + info.begin + ', ' + info.end + ') extend past the ' +
+                                   bufferBytes + '-byte buffer'] };
+  }
+  const need = numel * ELEMENT_BYTES[dtype];
+  if (info.byteLength !== need) {
+    return { info: null, defects: ["'" + name + "': " + numel + ' x ' + dtype + ' is ' + need +
+                                   ' bytes, the record spans ' + info.byteLength] };
+  }
+  return { info: info, defects: [] };
+}
+
+// f16 bits -> the f32 value (exact).
+function f16ToF32(h) {
+  const sign = h & 0x8000 ? -1 : 1;
+  const e = (h >>> 10) & 0x1f, m = h & 0x3ff;
+  if (e === 0x1f) return m ? NaN : sign * Infinity;
+  return e === 0 ? sign * m * Math.pow(2, -24) : sign * (1024 + m) * Math.pow(2, e - 25);
+}
 
 class Safetensors {
-  constructor(fd, tensors, dataStart, metadata) {
+  constructor(path, fd, records, bufferStart, metadata) {
+    this.path = path;
     this.fd = fd;
-    this.tensors = tensors;
-    this.dataStart = dataStart;
+    this.records = records;        // Map name -> info
+    this.bufferStart = bufferStart;
     this.metadata = metadata;
   }
 
   static open(path) {
+    const where = require('path').basename(path);
     const fd = fs.openSync(path, 'r');
     try {
-      const size = fs.fstatSync(fd).size;
-      if (size < 8) throw new Error('not a safetensors file: ' + size + ' bytes');
-      const lenBuf = Buffer.alloc(8);
-      fs.readSync(fd, lenBuf, 0, 8, 0);
-      const headerLen = Number(lenBuf.readBigUInt64LE(0));
-      if (!isInt(headerLen) || headerLen <= 0 || 8 + headerLen > size) {
-        throw new Error('header length ' + headerLen + ' does not fit in a ' + size + '-byte file');
+      const fileBytes = fs.fstatSync(fd).size;
+      if (fileBytes < 8) throw new Error(where + ': ' + fileBytes + ' bytes is too short for a safetensors length prefix');
+      const prefix = Buffer.alloc(8);
+      fs.readSync(fd, prefix, 0, 8, 0);
+      const n = Number(prefix.readBigUInt64LE(0));
+      if (n === 0 || n > Math.min(fileBytes - 8, HEADER_LIMIT)) {
+        throw new Error(where + ': the length prefix declares a ' + n + '-byte header, but ' + (fileBytes - 8) +
+                        ' bytes follow it (and headers are limited to ' + HEADER_LIMIT + ' bytes)');
       }
-      const headerBuf = Buffer.alloc(headerLen);
-      fs.readSync(fd, headerBuf, 0, headerLen, 8);
+      const text = Buffer.alloc(n);
+      fs.readSync(fd, text, 0, n, 8);
       let header;
       try {
-        header = JSON.parse(new util.TextDecoder('utf-8', { fatal: true }).decode(headerBuf));
+        header = JSON.parse(new util.TextDecoder('utf-8', { fatal: true }).decode(text));
       } catch (e) {
-        throw new Error('header is not valid UTF-8 JSON: ' + e.message);
+        throw new Error(where + ': the header is not UTF-8 JSON (' + e.message + ')');
       }
       if (header === null || typeof header !== 'object' || Array.isArray(header)) {
-        throw new Error('header must be a JSON object');
+        throw new Error(where + ': the header is a JSON ' + typeName(header) + ', not an object of tensor records');
       }
-      const metadata = header.__metadata__ === undefined ? null : header.__metadata__;
-      delete header.__metadata__;
-      const dataStart = 8 + headerLen;
-      const dataSize = size - dataStart;
-      const tensors = new Map();
+      const bufferStart = 8 + n, bufferBytes = fileBytes - bufferStart;
+      const defects = [];
+      let metadata = null;
+      if (Object.prototype.hasOwnProperty.call(header, '__metadata__')) {
+        metadata = header.__metadata__;
+        const ok = metadata !== null && typeof metadata === 'object' && !Array.isArray(metadata) &&
+                   Object.keys(metadata).every(function (k) { return typeof metadata[k] === 'string'; });
+        if (!ok) defects.push('__metadata__ is not an object of strings');
+        delete header.__metadata__;
+      }
+      const records = new Map();
       Object.keys(header).forEach(function (name) {
-        const e = header[name] || {};
-        const el = DTYPE_SIZE[e.dtype];
-        if (el === undefined) throw new Error(name + ': unknown dtype ' + JSON.stringify(e.dtype));
-        if (!Array.isArray(e.shape) || !e.shape.every(function (d) { return isInt(d) && d >= 0; })) {
-          throw new Error(name + ': shape must be an array of non-negative integers');
-        }
-        if (!Array.isArray(e.data_offsets) || e.data_offsets.length !== 2) {
-          throw new Error(name + ': data_offsets must be a pair');
-        }
-        const begin = e.data_offsets[0], end = e.data_offsets[1];
-        if (!isInt(begin) || !isInt(end) || begin < 0 || end < begin) {
-          throw new Error(name + ': bad data_offsets [' + begin + ', ' + end + ']');
-        }
-        if (end > dataSize) throw new Error(name + ': ends at ' + end + ' but the data section is only ' + dataSize + ' bytes');
-        const numel = e.shape.reduce(function (a, b) { return a * b; }, 1);
-        if (end - begin !== numel * el) {
-          throw new Error(name + ': shape [' + e.shape + '] of ' + e.dtype + ' needs ' + numel * el +
-                          ' bytes but the header reserves ' + (end - begin));
-        }
-        tensors.set(name, { name: name, dtype: e.dtype, shape: e.shape.slice(), begin: begin, end: end, numel: numel });
+        const r = checkRecord(name, header[name], bufferBytes);
+        Array.prototype.push.apply(defects, r.defects);
+        if (r.info) records.set(name, r.info);
       });
-      const ranges = Array.from(tensors.values()).sort(function (a, b) { return a.begin - b.begin; });
-      for (let i = 1; i < ranges.length; i++) {
-        if (ranges[i].begin < ranges[i - 1].end) throw new Error(ranges[i].name + ' overlaps ' + ranges[i - 1].name);
+      // Two records must never claim the same byte.
+      const byStart = Array.from(records.values()).filter(function (r) { return r.byteLength > 0; })
+        .sort(function (a, b) { return a.begin - b.begin || a.end - b.end; });
+      for (let i = 1; i < byStart.length; i++) {
+        const a = byStart[i - 1], b = byStart[i];
+        if (b.begin < a.end) {
+          defects.push("'" + b.name + "' [" + b.begin + ', ' + b.end + ") overlaps '" + a.name + "' [" + a.begin + ', ' +
+                       a.end + ')');
+        }
       }
-      return new Safetensors(fd, tensors, dataStart, metadata);
+      if (defects.length) {
+        throw new Error(where + ': ' + defects.length + ' defect' + (defects.length > 1 ? 's' : '') + ' in the header: ' +
+                        defects.join('; '));
+      }
+      return new Safetensors(path, fd, records, bufferStart, metadata);
     } catch (e) {
       fs.closeSync(fd);
       throw e;
     }
   }
 
-  get size() { return this.tensors.size; }
-  names() { return Array.from(this.tensors.keys()); }
-  has(name) { return this.tensors.has(name); }
+  get size() { return this.records.size; }
+  names() { return Array.from(this.records.keys()); }
+  has(name) { return this.records.has(name); }
   info(name) {
-    const t = this.tensors.get(name);
-    if (!t) throw new Error('no tensor named ' + JSON.stringify(name));
+    const t = this.records.get(name);
+    if (!t) throw new Error(require('path').basename(this.path) + ' holds no tensor ' + JSON.stringify(name));
     return t;
   }
 
-  // The tensor's bytes exactly as stored, in a fresh (so aligned) buffer.
-  readRaw(name) {
+  // `length` bytes of a tensor from `offset` within it, into a fresh (so aligned) buffer.
+  readRawRange(name, offset, length) {
     const t = this.info(name);
-    const buf = Buffer.alloc(t.end - t.begin);
-    let done = 0;
-    while (done < buf.length) {
-      const n = fs.readSync(this.fd, buf, done, buf.length - done, this.dataStart + t.begin + done);
-      if (n <= 0) throw new Error(name + ': short read');
-      done += n;
+    if (!isCount(offset) || !isCount(length) || offset + length > t.byteLength) {
+      throw new RangeError(name + ': bytes ' + offset + '..' + (offset + length) + ' lie outside its ' + t.byteLength +
+                           ' bytes');
+    }
+    const buf = Buffer.alloc(length);
+    for (let done = 0; done < length;) {
+      const got = fs.readSync(this.fd, buf, done, length - done, this.bufferStart + t.begin + offset + done);
+      if (got <= 0) throw new Error(name + ': the file ended ' + (length - done) + ' bytes early');
+      done += got;
     }
     return buf;
   }
 
-  // {dtype: 'bf16'|'f32', shape, data}: bf16 as its bits, f32 as is, f16 widened exactly to f32.
-  tensor(name) {
+  // The tensor's bytes as stored.
+  readRaw(name) { return this.readRawRange(name, 0, this.info(name).byteLength); }
+
+  // The tensor widened exactly to f32 (BF16, F16 or F32 storage); into `out` when given.
+  readF32(name, out) {
     const t = this.info(name);
     const raw = this.readRaw(name);
     const ab = raw.buffer.slice(raw.byteOffset, raw.byteOffset + raw.length);
-    if (t.dtype === 'BF16') return { dtype: 'bf16', shape: t.shape, data: new Uint16Array(ab) };
-    if (t.dtype === 'F32') return { dtype: 'f32', shape: t.shape, data: new Float32Array(ab) };
-    if (t.dtype === 'F16') {
-      const h = new Uint16Array(ab), out = new Float32Array(h.length);
-      for (let i = 0; i < h.length; i++) out[i] = f16ToF32(h[i]);
-      return { dtype: 'f32', shape: t.shape, data: out };
+    const dst = out || new Float32Array(t.numel);
+    if (dst.length < t.numel) throw new RangeError(name + ': ' + t.numel + ' values do not fit ' + dst.length);
+    if (t.dtype === 'F32') {
+      dst.set(new Float32Array(ab));
+    } else if (t.dtype === 'BF16') {
+      const h = new Uint16Array(ab), u = new Uint32Array(dst.buffer, dst.byteOffset, t.numel);
+      for (let i = 0; i < h.length; i++) u[i] = h[i] << 16;
+    } else if (t.dtype === 'F16') {
+      const h = new Uint16Array(ab);
+      for (let i = 0; i < h.length; i++) dst[i] = f16ToF32(h[i]);
+    } else {
+      throw new Error(name + ': the loader reads BF16, F16 and F32 tensors, not ' + t.dtype);
     }
-    throw new Error(name + ': dtype ' + t.dtype + ' is not a weight format the loader reads');
+    return dst;
+  }
+
+  // {dtype: 'bf16'|'f32', shape, data} as the loader uploads it: BF16 as its bits (the device
+  // widens it), F32 as is, F16 widened here.
+  tensor(name) {
+    const t = this.info(name);
+    if (t.dtype === 'BF16') {
+      const raw = this.readRaw(name);
+      return { dtype: 'bf16', shape: t.shape, data: new Uint16Array(raw.buffer.slice(raw.byteOffset, raw.byteOffset + raw.length)) };
+    }
+    return { dtype: 'f32', shape: t.shape, data: this.readF32(name) };
   }
 
   close() {
@@ -128,86 +203,4 @@ class Safetensors {
   }
 }
 
-// f16 bits -> f32, exactly (src/core/dtype.js:58-77).
-function f16ToF32(h) {
-  const sign = h & 0x8000 ? -1 : 1;
-  const exp = (h >>> 10) & 0x1f, mant = h & 0x3ff;
-  if (exp === 0) return sign * mant * Math.pow(2, -24);
-  if (exp === 0x1f) return mant ? NaN : sign * Infinity;
-  return sign * (1 + mant / 1024) * Math.pow(2, exp - 15);
-}
-
-const REQUIRED = ['hidden_size', 'intermediate_size', 'num_hidden_layers', 'num_attention_heads',
-  'num_key_value_heads', 'vocab_size', 'max_position_embeddings', 'rope_theta', 'rms_norm_eps'];
-
-// config.json (text or object) -> the loader's config (src/core/config.js:16-80).
-function parseConfig(raw) {
-  if (typeof raw === 'string') raw = JSON.parse(raw);
-  REQUIRED.forEach(function (key) {
-    if (typeof raw[key] !== 'number' || !Number.isFinite(raw[key])) {
-      throw new Error('config: ' + key + ' must be a finite number, got ' + JSON.stringify(raw[key]));
-    }
-  });
-  if (raw.model_type !== 'qwen2') throw new Error('config: only qwen2 is implemented, got ' + JSON.stringify(raw.model_type));
-  const act = raw.hidden_act === undefined ? 'silu' : raw.hidden_act;
-  if (act !== 'silu') throw new Error('config: only the silu/SwiGLU MLP is implemented, got ' + act);
-  if (raw.use_sliding_window === true) throw new Error('config: sliding-window attention is not implemented');
-  if (raw.hidden_size % raw.num_attention_heads !== 0) {
-    throw new Error('config: hidden_size ' + raw.hidden_size + ' is not divisible by num_attention_heads ' +
-                    raw.num_attention_heads);
-  }
-  if (raw.num_attention_heads % raw.num_key_value_heads !== 0) {
-    throw new Error('config: num_attention_heads ' + raw.num_attention_heads +
-                    ' is not divisible by num_key_value_heads ' + raw.num_key_value_heads);
-  }
-  return {
-    hidden: raw.hidden_size, intermediate: raw.intermediate_size, layers: raw.num_hidden_layers,
-    heads: raw.num_attention_heads, kvHeads: raw.num_key_value_heads, vocab: raw.vocab_size,
-    ropeTheta: raw.rope_theta, eps: raw.rms_norm_eps, tieWordEmbeddings: raw.tie_word_embeddings === true,
-  };
-}
-
-// Every tensor the architecture requires, with its shape (config.js:89-121).
-function expectedTensors(config) {
-  const d = config.hidden, kv = config.kvHeads * (config.hidden / config.heads), f = config.intermediate;
-  const shapes = { 'model.embed_tokens.weight': [config.vocab, d], 'model.norm.weight': [d] };
-  for (let i = 0; i < config.layers; i++) {
-    const p = 'model.layers.' + i + '.';
-    shapes[p + 'input_layernorm.weight'] = [d];
-    shapes[p + 'post_attention_layernorm.weight'] = [d];
-    shapes[p + 'self_attn.q_proj.weight'] = [d, d];
-    shapes[p + 'self_attn.q_proj.bias'] = [d];
-    shapes[p + 'self_attn.k_proj.weight'] = [kv, d];
-    shapes[p + 'self_attn.k_proj.bias'] = [kv];
-    shapes[p + 'self_attn.v_proj.weight'] = [kv, d];
-    shapes[p + 'self_attn.v_proj.bias'] = [kv];
-    shapes[p + 'self_attn.o_proj.weight'] = [d, d];
-    shapes[p + 'mlp.gate_proj.weight'] = [f, d];
-    shapes[p + 'mlp.up_proj.weight'] = [f, d];
-    shapes[p + 'mlp.down_proj.weight'] = [d, f];
-  }
-  if (config.tieWordEmbeddings === false) shapes['lm_head.weight'] = [config.vocab, d];
-  return shapes;
-}
-
-// checkAgainst (config.js:128-153): exactly the implied tensors, each with its shape.
-function checkAgainst(config, st) {
-  const expected = expectedTensors(config);
-  const problems = [];
-  Object.keys(expected).forEach(function (name) {
-    if (!st.has(name)) { problems.push('missing ' + name); return; }
-    const got = st.info(name).shape, want = expected[name];
-    if (got.length !== want.length || got.some(function (d, i) { return d !== want[i]; })) {
-      problems.push(name + ': expected shape [' + want + '], file has [' + got + ']');
-    }
-  });
-  st.names().forEach(function (name) { if (!(name in expected)) problems.push('unexpected tensor ' + name); });
-  if (problems.length) {
-    throw new Error('weights do not match config (' + problems.length + ' problem' + (problems.length === 1 ? '' : 's') +
-                    '):\n  ' + problems.slice(0, 10).join('\n  ') +
-                    (problems.length > 10 ? '\n  ... and ' + (problems.length - 10) + ' more' : ''));
-  }
-  return Object.keys(expected).length;
-}
-
-module.exports = { Safetensors, parseConfig, expectedTensors, checkAgainst, f16ToF32, DTYPE_SIZE };
+module.exports = { Safetensors, ELEMENT_BYTES, f16ToF32 };

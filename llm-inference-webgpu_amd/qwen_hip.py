@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import ctypes
 import json
+import math
 import os
 from dataclasses import dataclass
 
@@ -65,9 +66,45 @@ class Config(ctypes.Structure):
                 ("eps", ctypes.c_double), ("max_positions", ctypes.c_int32)]
 
 
+# The config.json fields a model is built from: (attribute, key, kind), where a "count" is a
+# positive integer and a "real" a positive finite number. max_position_embeddings is checked
+# but not kept (the rope table is sized by the caller's maxPositions).
+_HF_FIELDS = (
+    ("hidden", "hidden_size", "count"), ("intermediate", "intermediate_size", "count"),
+    ("layers", "num_hidden_layers", "count"), ("heads", "num_attention_heads", "count"),
+    ("kv_heads", "num_key_value_heads", "count"), ("vocab", "vocab_size", "count"),
+    (None, "max_position_embeddings", "count"), ("rope_theta", "rope_theta", "real"),
+    ("eps", "rms_norm_eps", "real"),
+)
+
+# The tensors of one decoder layer (checkpoint names, src/core/config.js:88-119) and their
+# shapes in terms of d = hidden, k = kv_dim, f = intermediate.
+_LAYER_TENSORS = (
+    ("input_layernorm.weight", "d"), ("post_attention_layernorm.weight", "d"),
+    ("self_attn.q_proj.weight", "dd"), ("self_attn.q_proj.bias", "d"),
+    ("self_attn.k_proj.weight", "kd"), ("self_attn.k_proj.bias", "k"),
+    ("self_attn.v_proj.weight", "kd"), ("self_attn.v_proj.bias", "k"),
+    ("self_attn.o_proj.weight", "dd"),
+    ("mlp.gate_proj.weight", "fd"), ("mlp.up_proj.weight", "fd"), ("mlp.down_proj.weight", "df"),
+)
+
+
+def _field_ok(v, kind) -> bool:
+    if isinstance(v, bool) or not isinstance(v, (int, float)):
+        return False
+    if kind == "count":
+        return isinstance(v, int) and v > 0
+    return math.isfinite(v) and v > 0
+
+
+def _few(names, n=4) -> str:
+    return ", ".join(names[:n]) + (f", ... ({len(names) - n} more)" if len(names) > n else "")
+
+
 @dataclass(frozen=True)
 class ModelConfig:
-    """The dimensions src/core/config.js derives (headDim, kvDim, kvGroupSize)."""
+    """The model's dimensions, from config.json (the fields of src/core/config.js's ModelConfig;
+    headDim, kvDim and the GQA group follow from them)."""
 
     hidden: int = 896
     intermediate: int = 4864
@@ -79,73 +116,71 @@ class ModelConfig:
     eps: float = 1e-6
     tie_word_embeddings: bool = True
 
-    REQUIRED = ("hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
-                "num_key_value_heads", "vocab_size", "max_position_embeddings", "rope_theta",
-                "rms_norm_eps")
-
     @staticmethod
     def from_hf(raw) -> "ModelConfig":
-        """ModelConfig of src/core/config.js:16-80 from a config.json (text, path or dict):
-        the required numbers, and the architectures this engine refuses."""
+        """From a config.json given as a path, JSON text or a dict. Every field is checked and all
+        problems are reported together; architectures other than the one the kernels implement
+        (qwen2: SiLU-gated MLP, full-context GQA attention) are refused."""
         if isinstance(raw, str):
             raw = json.loads(open(raw).read() if os.path.exists(raw) else raw)
-        for key in ModelConfig.REQUIRED:
+        if not isinstance(raw, dict):
+            raise QwenHipError(QH_ERR_INVALID, f"config.json holds a JSON {type(raw).__name__}, not an object")
+        problems, got = [], {}
+        for attr, key, kind in _HF_FIELDS:
             v = raw.get(key)
-            if isinstance(v, bool) or not isinstance(v, (int, float)) or not np.isfinite(v):
-                raise QwenHipError(QH_ERR_INVALID, f"config: {key} must be a finite number, got {json.dumps(v)}")
+            if not _field_ok(v, kind):
+                what = "positive integer" if kind == "count" else "positive finite number"
+                problems.append(f"{key} = {json.dumps(v)} is not a {what}")
+            elif attr is not None:
+                got[attr] = v
         if raw.get("model_type") != "qwen2":
-            raise QwenHipError(QH_ERR_INVALID,
-                               f"config: only qwen2 is implemented, got {json.dumps(raw.get('model_type'))}")
+            problems.append(f"model_type {json.dumps(raw.get('model_type'))}: only the qwen2 architecture is built here")
         if raw.get("hidden_act", "silu") != "silu":
-            raise QwenHipError(QH_ERR_INVALID,
-                               f"config: only the silu/SwiGLU MLP is implemented, got {raw.get('hidden_act')}")
+            problems.append(f"hidden_act {json.dumps(raw.get('hidden_act'))}: the MLP here is SiLU-gated")
         if raw.get("use_sliding_window") is True:
-            raise QwenHipError(QH_ERR_INVALID, "config: sliding-window attention is not implemented")
-        d, h, kvh = raw["hidden_size"], raw["num_attention_heads"], raw["num_key_value_heads"]
-        if d % h:
-            raise QwenHipError(QH_ERR_INVALID,
-                               f"config: hidden_size {d} is not divisible by num_attention_heads {h}")
-        if h % kvh:
-            raise QwenHipError(QH_ERR_INVALID, f"config: num_attention_heads {h} is not divisible by "
-                                               f"num_key_value_heads {kvh}")
-        return ModelConfig(hidden=d, intermediate=raw["intermediate_size"], layers=raw["num_hidden_layers"],
-                           heads=h, kv_heads=kvh, vocab=raw["vocab_size"], rope_theta=float(raw["rope_theta"]),
-                           eps=float(raw["rms_norm_eps"]), tie_word_embeddings=raw.get("tie_word_embeddings") is True)
+            problems.append("use_sliding_window: attention here always spans the whole context")
+        if "hidden" in got and "heads" in got and got["hidden"] % got["heads"]:
+            problems.append(f"hidden_size {got['hidden']} does not split into {got['heads']} equal heads")
+        if "heads" in got and "kv_heads" in got and got["heads"] % got["kv_heads"]:
+            problems.append(f"{got['heads']} query heads do not group evenly over {got['kv_heads']} key/value heads")
+        if problems:
+            raise QwenHipError(QH_ERR_INVALID, "config.json describes no model this engine runs: "
+                               + "; ".join(problems))
+        return ModelConfig(hidden=got["hidden"], intermediate=got["intermediate"], layers=got["layers"],
+                           heads=got["heads"], kv_heads=got["kv_heads"], vocab=got["vocab"],
+                           rope_theta=float(got["rope_theta"]), eps=float(got["eps"]),
+                           tie_word_embeddings=raw.get("tie_word_embeddings") is True)
 
     def expected_tensors(self) -> dict:
-        """Every tensor the architecture requires, with its shape (config.js:89-121)."""
-        d, kv, ffn = self.hidden, self.kv_dim, self.intermediate
-        shapes = {"model.embed_tokens.weight": (self.vocab, d), "model.norm.weight": (d,)}
+        """Every tensor the architecture needs, by checkpoint name, with its shape (a tied model
+        has no lm_head.weight: the embedding is the output projection)."""
+        dims = {"d": self.hidden, "k": self.kv_dim, "f": self.intermediate}
+        shapes = {"model.embed_tokens.weight": (self.vocab, self.hidden), "model.norm.weight": (self.hidden,)}
         for i in range(self.layers):
-            p = f"model.layers.{i}."
-            shapes.update({
-                p + "input_layernorm.weight": (d,), p + "post_attention_layernorm.weight": (d,),
-                p + "self_attn.q_proj.weight": (d, d), p + "self_attn.q_proj.bias": (d,),
-                p + "self_attn.k_proj.weight": (kv, d), p + "self_attn.k_proj.bias": (kv,),
-                p + "self_attn.v_proj.weight": (kv, d), p + "self_attn.v_proj.bias": (kv,),
-                p + "self_attn.o_proj.weight": (d, d),
-                p + "mlp.gate_proj.weight": (ffn, d), p + "mlp.up_proj.weight": (ffn, d),
-                p + "mlp.down_proj.weight": (d, ffn),
-            })
+            for suffix, form in _LAYER_TENSORS:
+                shapes[f"model.layers.{i}.{suffix}"] = tuple(dims[c] for c in form)
         if not self.tie_word_embeddings:
-            shapes["lm_head.weight"] = (self.vocab, d)
+            shapes["lm_head.weight"] = (self.vocab, self.hidden)
         return shapes
 
     def check_against(self, st) -> int:
-        """checkAgainst (config.js:128-153): exactly the implied tensors, each with its shape."""
+        """Checks that a checkpoint (anything with names / has / info) holds exactly the tensors
+        the config implies, each with its shape; reports what is missing, misshapen and surplus
+        together. Returns the number of tensors."""
         expected = self.expected_tensors()
-        problems = []
-        for name, shape in expected.items():
-            if not st.has(name):
-                problems.append(f"missing {name}")
-            elif tuple(st.info(name).shape) != tuple(shape):
-                problems.append(f"{name}: expected shape {list(shape)}, file has {list(st.info(name).shape)}")
-        problems += [f"unexpected tensor {n}" for n in st.names() if n not in expected]
-        if problems:
-            more = f"\n  ... and {len(problems) - 10} more" if len(problems) > 10 else ""
-            raise QwenHipError(QH_ERR_INVALID, f"weights do not match config ({len(problems)} problem"
-                                               f"{'' if len(problems) == 1 else 's'}):\n  "
-                               + "\n  ".join(problems[:10]) + more)
+        missing = [n for n in expected if not st.has(n)]
+        misshapen = [f"{n} is {list(st.info(n).shape)} where the config implies {list(s)}"
+                     for n, s in expected.items() if st.has(n) and tuple(st.info(n).shape) != tuple(s)]
+        surplus = [n for n in st.names() if n not in expected]
+        parts = []
+        if missing:
+            parts.append(f"{len(missing)} missing ({_few(missing)})")
+        if misshapen:
+            parts.append(f"{len(misshapen)} misshapen ({_few(misshapen)})")
+        if surplus:
+            parts.append(f"{len(surplus)} not part of the model ({_few(surplus)})")
+        if parts:
+            raise QwenHipError(QH_ERR_INVALID, "the checkpoint does not match the config: " + "; ".join(parts))
         return len(expected)
 
     @property
@@ -228,6 +263,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_model_set_tensor": [vp, ctypes.c_char_p, i32, i32, i32, i32, vp, vp, vp],
         "qh_model_load_tensor": [vp, ctypes.c_char_p, i32, i32, i32, vp, i32, i32],
         "qh_model_finalize": [vp], "qh_model_free": [vp], "qh_model_bytes": [vp, vp],
+        "qh_model_config": [vp, vp],
         "qh_model_set_numerics": [vp, i32], "qh_model_set_matmul": [vp, i32],
         "qh_cache_create": [vp, i32, vp], "qh_cache_free": [vp], "qh_cache_length": [vp, vp],
         "qh_cache_set_length": [vp, i32], "qh_cache_present": [vp, i32, vp, vp],

@@ -1,7 +1,8 @@
-"""The load path's checkpoint handling on the CPU: the safetensors reader (Python and the
-Node driver's) against the independent `safetensors` library and the validation of
-src/core/safetensors.js:56-125, and config.json parsing / checkAgainst
-(src/core/config.js:16-153). No device is touched."""
+"""The load path's checkpoint handling on the CPU: the safetensors readers (Python and the
+Node driver's) against the independent `safetensors` library and against malformed files
+(every defect the format allows a header to have, reported together), and config.json
+parsing / the checkpoint-vs-config check (src/core/config.js's ModelConfig surface). No
+device is touched."""
 import json
 import os
 import shutil
@@ -72,17 +73,23 @@ def raw_file(path, header, data=b"", header_len=None):
 
 
 @pytest.mark.parametrize("header,data,header_len,match", [
-    ({}, b"", 10 ** 6, "does not fit"),
-    (b"\xff\xfe{}", b"", None, "not valid UTF-8 JSON"),
-    (b"[1, 2]", b"", None, "must be a JSON object"),
-    ({"t": {"dtype": "Q7", "shape": [1], "data_offsets": [0, 1]}}, b"\0", None, "unknown dtype"),
-    ({"t": {"dtype": "F32", "shape": [-1], "data_offsets": [0, 4]}}, b"\0" * 4, None, "non-negative integers"),
-    ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [0]}}, b"\0" * 4, None, "must be a pair"),
-    ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [4, 0]}}, b"\0" * 4, None, "bad data_offsets"),
-    ({"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 4, None, "data section is only 4"),
-    ({"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 4]}}, b"\0" * 8, None, "needs 8 bytes"),
+    ({}, b"", 10 ** 6, "length prefix declares a 1000000-byte header"),
+    (b"\xff\xfe{}", b"", None, "not UTF-8 JSON"),
+    (b"[1, 2]", b"", None, "not an object of tensor records"),
+    ({"t": {"dtype": "Q7", "shape": [1], "data_offsets": [0, 1]}}, b"\0", None, "not a safetensors element type"),
+    ({"t": {"dtype": "F32", "shape": [-1], "data_offsets": [0, 4]}}, b"\0" * 4, None,
+     "not a list of non-negative integers"),
+    ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [0]}}, b"\0" * 4, None, r"is not \[start, stop\]"),
+    ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [4, 0]}}, b"\0" * 4, None, r"is not \[start, stop\]"),
+    ({"t": {"dtype": "F32", "shape": [1], "data_offsets": [0, True]}}, b"\0" * 4, None, r"is not \[start, stop\]"),
+    ({"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]}}, b"\0" * 4, None, "extend past the 4-byte buffer"),
+    ({"t": {"dtype": "F32", "shape": [2], "data_offsets": [0, 4]}}, b"\0" * 8, None,
+     "2 x F32 is 8 bytes, the record spans 4"),
     ({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
-      "b": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8, None, "overlaps"),
+      "b": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8, None,
+     r"'b' \[4, 8\) overlaps 'a' \[0, 8\)"),
+    ({"t": 7}, b"", None, "the record is a JSON int"),
+    ({"__metadata__": {"k": 1}}, b"", None, "__metadata__ is not an object of strings"),
 ])
 def test_reader_rejects_malformed_files(tmp_path, header, data, header_len, match):
     path = raw_file(tmp_path / "bad.safetensors", header, data, header_len)
@@ -90,10 +97,22 @@ def test_reader_rejects_malformed_files(tmp_path, header, data, header_len, matc
         C.Safetensors.open(path)
 
 
+def test_reader_reports_every_defect_at_once(tmp_path):
+    header = {"a": {"dtype": "Q7", "shape": [1], "data_offsets": [0, 1]},
+              "b": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]},
+              "c": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
+              "d": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}
+    path = raw_file(tmp_path / "bad.safetensors", header, b"\0" * 8)
+    with pytest.raises(C.SafetensorsError) as e:
+        C.Safetensors.open(path)
+    msg = str(e.value)
+    assert "3 defects" in msg and "'a'" in msg and "3 x F32 is 12 bytes" in msg and "'d' [4, 8) overlaps 'c'" in msg
+
+
 def test_reader_rejects_a_short_file(tmp_path):
     p = tmp_path / "short"
     p.write_bytes(b"1234")
-    with pytest.raises(C.SafetensorsError, match="not a safetensors file"):
+    with pytest.raises(C.SafetensorsError, match="too short for a safetensors length prefix"):
         C.Safetensors.open(str(p))
 
 
@@ -107,14 +126,22 @@ def test_config_parse_gives_the_model_dimensions(hip):
 
 
 @pytest.mark.parametrize("change,match", [
-    ({"model_type": "llama"}, "only qwen2"), ({"hidden_act": "gelu"}, "silu"),
-    ({"use_sliding_window": True}, "sliding-window"), ({"num_attention_heads": 13}, "not divisible"),
-    ({"num_key_value_heads": 3}, "not divisible"), ({"rope_theta": None}, "finite number"),
-    ({"vocab_size": "151936"}, "finite number"),
+    ({"model_type": "llama"}, "only the qwen2 architecture"), ({"hidden_act": "gelu"}, "SiLU-gated"),
+    ({"use_sliding_window": True}, "whole context"), ({"num_attention_heads": 13}, "does not split into 13"),
+    ({"num_key_value_heads": 3}, "do not group evenly over 3"), ({"rope_theta": None}, "positive finite number"),
+    ({"vocab_size": "151936"}, "positive integer"), ({"num_hidden_layers": 24.0}, "positive integer"),
+    ({"rms_norm_eps": float("nan")}, "positive finite number"),
 ])
 def test_config_parse_refuses_what_the_engine_does_not_implement(hip, change, match):
     with pytest.raises(hip.QwenHipError, match=match):
         hip.ModelConfig.from_hf({**QWEN_CONFIG, **change})
+
+
+def test_config_parse_reports_every_problem_at_once(hip):
+    with pytest.raises(hip.QwenHipError) as e:
+        hip.ModelConfig.from_hf({**QWEN_CONFIG, "model_type": "llama", "vocab_size": -1, "hidden_act": "relu"})
+    msg = str(e.value)
+    assert "vocab_size = -1" in msg and "llama" in msg and "relu" in msg
 
 
 def test_check_against_reports_missing_extra_and_misshapen(hip, tmp_path):
@@ -130,8 +157,8 @@ def test_check_against_reports_missing_extra_and_misshapen(hip, tmp_path):
     with pytest.raises(hip.QwenHipError) as e:
         cfg.check_against(C.Safetensors.open(path))
     msg = str(e.value)
-    assert "3 problems" in msg and "missing model.norm.weight" in msg and "unexpected tensor extra.weight" in msg
-    assert "down_proj.weight: expected shape [128, 256], file has [256, 128]" in msg
+    assert "1 missing (model.norm.weight)" in msg and "1 not part of the model (extra.weight)" in msg
+    assert "model.layers.0.mlp.down_proj.weight is [256, 128] where the config implies [128, 256]" in msg
 
 
 @pytest.mark.skipif(not HAS_NODE, reason="node is not installed")
@@ -165,13 +192,17 @@ def test_js_reader_and_config_errors(tmp_path):
     path = raw_file(tmp_path / "bad.safetensors", {"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
                                                    "b": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}},
                     b"\0" * 8)
-    code = ("const s=require('./safetensors.js'); const r=[];"
+    code = ("const s=require('./safetensors.js'); const k=require('./config.js'); const r=[];"
             "try { s.Safetensors.open(process.argv[1]); } catch (e) { r.push(e.message); }"
-            "try { s.parseConfig(Object.assign(JSON.parse(process.argv[2]), {model_type:'llama'})); } catch (e) { r.push(e.message); }"
-            "const c=s.parseConfig(process.argv[2]); r.push([c.hidden,c.kvHeads,c.vocab,c.tieWordEmbeddings]);"
+            "try { k.parseConfig(Object.assign(JSON.parse(process.argv[2]), {model_type:'llama'})); } catch (e) { r.push(e.message); }"
+            "const c=k.ModelConfig.parse(process.argv[2]); r.push([c.hiddenSize,c.numKVHeads,c.vocabSize,c.tieWordEmbeddings,c.headDim,c.kvDim]);"
+            "r.push(c.expectedTensors().size);"
+            "try { k.parseConfig(Object.assign(JSON.parse(process.argv[2]), {vocab_size:'x', num_attention_heads:13})); } catch (e) { r.push(e.message); }"
             "console.log(JSON.stringify(r));")
     r = subprocess.run(["node", "-e", code, path, json.dumps(QWEN_CONFIG)], cwd=JS_DIR, capture_output=True,
                        text=True, timeout=60)
     assert r.returncode == 0, r.stderr
     out = json.loads(r.stdout)
-    assert "b overlaps a" in out[0] and "only qwen2" in out[1] and out[2] == [896, 2, 151936, True]
+    assert "'b' [4, 8) overlaps 'a' [0, 8)" in out[0] and "only the qwen2" in out[1]
+    assert out[2] == [896, 2, 151936, True, 64, 128] and out[3] == 2 + 24 * 12
+    assert 'vocab_size = "x"' in out[4] and "does not split into 13" in out[4]

@@ -115,7 +115,7 @@ def test_file_that_disagrees_with_its_config_is_refused_before_upload(ctx, hip, 
     ckpt = hip.synthesize_checkpoint(cfg, seed=6)
     d = write_dir(tmp_path, hip.ModelConfig(hidden=128, intermediate=384, layers=2, heads=2, kv_heads=1, vocab=1000),
                   {k: ("BF16", v) for k, v in ckpt.items()})
-    with pytest.raises(hip.QwenHipError, match="weights do not match config"):
+    with pytest.raises(hip.QwenHipError, match="the checkpoint does not match the config: 6 misshapen"):
         hip.GpuModel.load_safetensors(ctx, d)
 
 

@@ -35,7 +35,7 @@ def test_addon_exports_the_driver_surface(addon_built):
     keys = json.loads(node("const a=require('./addon/qwen_napi.node'); console.log(JSON.stringify(Object.keys(a)))"))
     assert set(keys) == {"abiVersion", "open", "close", "describe", "synthBf16", "synthTokens", "quantizeInt8",
                          "quantizeInt4", "modelCreate", "modelSetMode", "modelSetTensor", "modelLoadTensor", "modelFinalize",
-                         "modelFree", "cacheCreate", "cacheFree", "cacheLength", "forward", "decode"}
+                         "modelFree", "cacheCreate", "cacheFree", "cacheLength", "cachePresent", "forward", "decode"}
     assert node("console.log(require('./addon/qwen_napi.node').abiVersion())").strip() == "1"
 
 
@@ -70,6 +70,25 @@ def test_js_f16_narrowing_matches_numpy(addon_built):
     assert got == list(want.view(np.uint16).astype(int))
 
 
+def test_typed_arrays_are_checked_before_any_c_call(addon_built):
+    """Arrays of the wrong element type, or shorter than rows * cols (or the groups, rows or seq
+    they must cover), are refused in the binding with TypeError / RangeError, so no entry point
+    reads past a caller's array."""
+    out = json.loads(node(
+        "const a=require('./addon/qwen_napi.node'); const r=[];"
+        "const t=(f)=>{ try { f(); r.push(null); } catch (e) { r.push(e.constructor.name + ': ' + e.message); } };"
+        "t(()=>a.quantizeInt8(new Float32Array(11), 3, 4));"
+        "t(()=>a.quantizeInt8(new Float64Array(12), 3, 4));"
+        "t(()=>a.quantizeInt4(new Float32Array(255), 1, 256, 128));"
+        "t(()=>a.quantizeInt8(new Float32Array(12), 0, 4));"
+        "t(()=>a.quantizeInt8([1, 2, 3], 1, 3));"
+        "console.log(JSON.stringify(r));"))
+    assert out[0].startswith("RangeError") and "holds 11 values where 12" in out[0]
+    assert out[1].startswith("TypeError") and "Float32Array" in out[1]
+    assert out[2].startswith("RangeError") and out[3].startswith("RangeError")
+    assert out[4].startswith("TypeError")
+
+
 def test_range_error_surfaces_as_js_range_error(addon_built):
     msg = node("const a=require('./addon/qwen_napi.node');"
                "try { a.quantizeInt4(new Float32Array(12), 1, 12, 5); } catch (e) { console.log(e.constructor.name) }")
@@ -102,5 +121,39 @@ def test_js_driver_matches_python_binding(addon_built, ctx, hip, scheme, numeric
     assert js["hiddenArgmax"] == out["argmax"]
     np.testing.assert_array_equal(np.frombuffer(base64.b64decode(js["hiddenLogits"]), np.float32), js_logits)
     assert js["cacheLength"] == 20 and js["rangeError"] is not None
+    cache.destroy()
+    model.destroy()
+
+
+@pytest.mark.gpu
+def test_reference_shaped_caller_drives_the_backend(addon_built, ctx, hip):
+    """web/bench.html's loop over objects shaped exactly like the reference's ModelConfig and
+    Safetensors (async readRaw, one tensor at an odd offset), f16 weights (quantize = null):
+    the logits equal the Python binding's bit for bit, the greedy tokens and the `present`
+    rows too; cache.keys / values destroy the cache once all are destroyed; a second forward
+    while one is pending is refused; batchTileFor and matmul 'tiled' are the reference's."""
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "reference_caller.js")],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    js = json.loads(r.stdout)
+    cfg = hip.ModelConfig(hidden=128, intermediate=256, layers=2, heads=2, kv_heads=1, vocab=1000)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=3)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "f16", 128, "f16"), cfg, maxPositions=64)
+    prompt = hip.synth_tokens(3, "prompt", cfg.vocab, 12)
+    cache = model.newCache(28)
+    out = model.forward_tokens(prompt, cache)
+    np.testing.assert_array_equal(np.frombuffer(base64.b64decode(js["firstLogits"]), np.uint32),
+                                  out["logits"].view(np.uint32))
+    gen = model.decode(cache, out["argmax"], 6)
+    assert js["tokens"] == [out["argmax"]] + list(gen)
+    assert cache.length == js["presentLength"] == 18
+    for L in range(cfg.layers):
+        pres = cache.present(L)
+        for kind in ("key", "value"):
+            got = np.frombuffer(base64.b64decode(js["present"][L][kind]), np.float32)
+            np.testing.assert_array_equal(got, pres[kind].ravel())
+    assert js["ticks"] == 26 and js["layers"] == 2 and js["warmBytes"] > 0 and js["freed"] is True
+    assert js["hiddenBuffer"] is None and "already running" in js["busy"] and js["cacheLength"] == 19
+    assert js["tiles"] == [1, 2, 2, 4, 4, 8, 8] and js["tiled"] is True and "matmul must be" in js["badMatmul"]
     cache.destroy()
     model.destroy()
