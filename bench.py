@@ -14,6 +14,12 @@ Also reported on the same JSON line:
                  bytes per launch over its average in-situ launch time, vs 8 TB/s
   per_kernel_us  in-situ microseconds per token by kernel role (events around
                  every launch, the reference's decode-profile split)
+  decode_bounds  what bounds the step on this device: the pure streaming-read ceiling, and
+                 the cost of a graph-replayed launch that reads its predecessor's output (as
+                 every decode launch does) times the step's launches
+  decode_kernels_cold  the step's own launches (int4 qkv / o / gate-up / down, int8 head,
+                 split-K attention) each over copies of its operands past 512 MiB, GB/s and
+                 the fraction of 8 TB/s and of the read ceiling
   matvec_isolated  BASELINE config 2: int8 matvec with an f16 activation at the
                  five layer shapes, one list-driven launch over >= 512 MiB of
                  distinct matrices (larger than the 256 MB last-level cache)
@@ -89,18 +95,24 @@ def measured_traffic(role, context):
 
 
 def isolated_matvec(ctx, shapes, reps=5):
-    """Config 2: int8 weights, x ~ N(0,1) f16, rotation of distinct matrices >= 512 MiB."""
+    """Config 2: weights W ~ N(0, 0.02) quantized per row to int8 by the reference quantizer's
+    rule (the device quantizer, qh_quantize), x ~ N(0,1) f16, one list-driven launch over
+    >= 512 MiB of distinct matrices (copies of the quantized matrix at distinct addresses)."""
     out = {}
     rng = np.random.default_rng(2)
     for name, rows, cols in shapes:
         per = rows * cols + 4 * rows                   # codes + scales stored
         count = int(np.ceil((512 << 20) / per))
         algo = rows * cols + 4 * rows + 2 * cols + 4 * rows   # + x read + y written
-        q = rng.integers(-127, 128, size=(count, rows, cols), dtype=np.int8)
-        s = (rng.random((count, rows), dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+        w = ctx.upload((rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02)))
+        dq, ds = ctx.empty(count * rows * cols, np.int8), ctx.empty(count * rows * 4)
+        ctx.quantize(w, H.FMT_F32, rows, cols, H.FMT_INT8, data=dq, scales=ds)
+        w.free()
+        for z in range(1, count):
+            ctx.copy(dq, 0, dq, z * rows * cols, rows * cols)
+            ctx.copy(ds, 0, ds, z * rows * 4, rows * 4)
         x = rng.standard_normal(cols).astype(np.float16).view(np.uint16)
-        dq, ds, dx, dy = ctx.upload(q), ctx.upload(s), ctx.upload(x), ctx.empty(count * rows * 4)
-        del q
+        dx, dy = ctx.upload(x), ctx.empty(count * rows * 4)
         W = ctx.weight(H.FMT_INT8, rows, cols, dq, ds)
         ctx.matvec_xh_list(W, count, rows * cols, rows, dx, 0, dy)   # warm
         e0, e1 = ctx.event(), ctx.event()
@@ -117,6 +129,48 @@ def isolated_matvec(ctx, shapes, reps=5):
         log(f"isolated int8 matvec {name} {rows}x{cols} x{count}: {gbs:.0f} GB/s")
         for b in (dq, ds, dx, dy):
             b.free()
+    return out
+
+
+def decode_bounds(ctx, launches_per_step):
+    """What bounds the batch-1 decode step on this device: the pure streaming-read ceiling
+    (1 GiB), and the cost of a graph-replayed launch of 224 blocks that does nothing, reads
+    nothing it depends on, or reads the vector the previous launch wrote (as each decode launch
+    reads its predecessor's output) -- times the step's launches, the step's latency floor."""
+    ceiling = ctx.read_ceiling(1 << 30, 10)
+    empty = ctx.launch_floor(0)
+    static = ctx.launch_floor(2)
+    dependent = ctx.launch_floor(1)
+    out = {"read_ceiling_GBps": round(ceiling, 1), "read_ceiling_frac": round(ceiling / PEAK_HBM_GBS, 4),
+           "launch_us": {"empty": round(empty, 3), "no_dependency": round(static, 3),
+                         "reads_previous_output": round(dependent, 3)},
+           "step_launches": launches_per_step,
+           "step_floor_us": round(launches_per_step * dependent, 1)}
+    log(f"bounds: read ceiling {ceiling:.0f} GB/s; launch {empty:.2f} us empty, {dependent:.2f} us dependent; "
+        f"step floor {out['step_floor_us']} us over {launches_per_step} launches")
+    return out
+
+
+def cold_decode_kernels(model, cache, cfg, ctx_len, ceiling, reps=5):
+    """The decode step's own launches timed cold: one launch over copies of the role's operands
+    exceeding 512 MiB (qh_decode_kernel_time_cold). Bytes per copy are what streams from HBM:
+    the weights with their scales and zero points (int4-g128 layers, int8 head), or for the
+    attention the f16 K and V chunks of 64 positions its slots read at position ctx_len."""
+    d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
+    int4 = lambda r, c: r * c // 2 + r * (c // 128) * 8
+    per_copy = {"qkv": int4(d + 2 * kv, d), "oproj": int4(d, d), "gateup": int4(2 * ffn, d),
+                "down": int4(d, ffn), "head": V * d + 4 * V,
+                "attention": ((ctx_len + 1 + 63) // 64) * 64 * kv * 2 * 2}
+    out = {}
+    cache.length = ctx_len
+    for role in ("qkv", "attention", "oproj", "gateup", "down", "head"):
+        us, copies = model.kernel_time_cold(cache, role, 512 << 20, reps)
+        nbytes = copies * per_copy[role]
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[role] = {"copies": copies, "bytes_per_launch": nbytes, "us_per_launch": round(us, 2),
+                     "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "frac_of_read_ceiling": round(gbs / ceiling, 4)}
+        log(f"cold {role}: {copies} copies, {us:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
     return out
 
 
@@ -597,6 +651,11 @@ def main():
                 "us_per_launch": round(kernel_us, 3)}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
+    # What bounds the step, and the step's own launches timed cold (at the position the in-situ
+    # timing used, past the timed tokens, so the cache rows the CPU check reads stay as decoded).
+    bounds = decode_bounds(ctx, sum(v["launches_per_token"] for v in per_kernel.values()))
+    cold = cold_decode_kernels(model, cache, cfg, args.context + psteps, bounds["read_ceiling_GBps"])
+
     iso = attn = prefill = loader = None
     if args.isolated == "all":
         d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
@@ -638,6 +697,8 @@ def main():
         "greedy_match": greedy,
         "greedy_match_cpu_sample": match,
         "greedy_match_cpu_c_sample": match_c,
+        "decode_bounds": bounds,
+        "decode_kernels_cold": cold,
         "matvec_isolated": iso,
         "attention_decode": attn,
         "prefill_512": prefill,

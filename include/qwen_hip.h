@@ -366,6 +366,23 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
  * web/decode-profile.html:239-283). It overwrites the position's decode scratch (and, for the
  * residual roles, the hidden row): rewind or re-prefill before decoding on. */
 int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, float* us_per_launch);
+/* The same launch of `role` (QH_ROLE_QKV .. QH_ROLE_HEAD) timed cold: one launch reads
+ * *copies copies of its operands (layer 0's matrix, the output head, or -- QH_ROLE_ATTENTION,
+ * fast numerics -- layer 0's f16 cache) that together exceed min_bytes, so with min_bytes past
+ * the 256 MB last-level cache every launch streams from HBM (the cold side of
+ * web/decode-profile.html:239-283; BASELINE config 2 rotates >= 512 MiB the same way). The
+ * copies are allocated, filled and freed by the call; *us_per_launch covers all copies. */
+int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
+                               float* us_per_launch, int32_t* copies);
+/* What bounds a batch-1 launch, measured on this device (no counterpart in the reference, which
+ * measures the same bounds in web/decode-profile.html:288-327): `launches` launches of `blocks`
+ * 256-thread blocks captured as one graph and replayed -- kind 0 does nothing; kind 1 reads the
+ * 896-float vector the previous launch wrote (as every decode launch reads its predecessor's
+ * output) and writes 4 floats per block; kind 2 is kind 1 reading nothing -- giving microseconds
+ * per launch. */
+int qh_probe_launch_floor(qh_ctx* ctx, int32_t kind, int32_t blocks, int32_t launches, float* us_per_launch);
+/* The pure-read ceiling: a streaming read of `bytes` (allocated and freed here), GB/s. */
+int qh_read_ceiling(qh_ctx* ctx, size_t bytes, int32_t reps, float* gbps);
 
 /* Kernel-level parity access to one decode step (the reference's per-kernel harness,
  * web/kernels.html:56-134, checks each WGSL kernel against the CPU on the same inputs; these

@@ -558,3 +558,42 @@ int qh_argmax(qh_ctx* ctx, const float* d_v, int32_t n, int32_t* h_index) {
 }
 
 }  // extern "C"
+
+extern "C" {
+
+int qh_probe_launch_floor(qh_ctx* ctx, int32_t kind, int32_t blocks, int32_t launches, float* us_per_launch) {
+  QH_CHECK(ctx && us_per_launch, QH_ERR_INVALID, "probe_launch_floor needs a context and an output");
+  QH_CHECK(kind >= 0 && kind <= 2 && blocks >= 1 && blocks <= 65536 && launches >= 1 && launches <= 4096,
+           QH_ERR_INVALID, "probe kind 0..2, blocks 1..65536 and launches 1..4096");
+  QH_HIP(hipSetDevice(ctx->device));
+  float* buf = nullptr;
+  QH_HIP(hipMalloc((void**)&buf, 2 * 4096 * sizeof(float)));
+  hipError_t e = hipMemsetAsync(buf, 0, 2 * 4096 * sizeof(float), ctx->stream);
+  if (e == hipSuccess) e = qh::probe_launch_floor(ctx->stream, kind, blocks, launches, buf, us_per_launch);
+  hipStreamSynchronize(ctx->stream);
+  hipFree(buf);
+  QH_HIP(e);
+  return QH_OK;
+}
+
+int qh_read_ceiling(qh_ctx* ctx, size_t bytes, int32_t reps, float* gbps) {
+  QH_CHECK(ctx && gbps, QH_ERR_INVALID, "read_ceiling needs a context and an output");
+  QH_CHECK(bytes >= ((size_t)1 << 20) && bytes <= ((size_t)64 << 30) && bytes % 64 == 0 && reps >= 1,
+           QH_ERR_INVALID, "read_ceiling reads 1 MiB .. 64 GiB (a multiple of 64 bytes), reps >= 1");
+  QH_HIP(hipSetDevice(ctx->device));
+  void* p = nullptr;
+  uint32_t* sink = nullptr;
+  QH_HIP(hipMalloc(&p, bytes));
+  hipError_t e = hipMalloc((void**)&sink, 4096 * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemsetAsync(p, 0x5a, bytes, ctx->stream);
+  float ms = 0.f;
+  if (e == hipSuccess) e = qh::read_ceiling(ctx->stream, p, bytes, reps, sink, &ms);
+  hipStreamSynchronize(ctx->stream);
+  hipFree(p);
+  if (sink) hipFree(sink);
+  QH_HIP(e);
+  *gbps = (float)(bytes / (ms * 1e-3) / 1e9);
+  return QH_OK;
+}
+
+}  // extern "C"

@@ -55,6 +55,12 @@ struct FusedArgs {
   ArgPair* partials;     // [blocks]: each block's best (value, index)
   int f32;              // fast numerics: the f32 matvec core
   // PRO_COMBINE: `in` holds the attention slot partials of the current position
+  // A list of list_count copies of the weights, one per blockIdx.y (the launch timed over a
+  // working set past the last-level cache): copy z reads w.data + z * list_w bytes and its
+  // scales / zero points + z * list_s floats, and writes out + z * list_out floats (and its
+  // argmax partials + z * list_part). 0: the one matrix of the decode step.
+  int list_count;
+  size_t list_w, list_s, list_out, list_part;
 };
 
 // Rows of work item `it`. QKV: a rope pair (j, j+32) of a q or k head, or two
@@ -209,6 +215,14 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   __shared__ float wl[PRO == PRO_COMBINE ? kBlock : 1];
   using Acc = typename std::conditional<F32, float, double>::type;
   using T = Teams<TL>;
+  if (blockIdx.y) {  // a copy of a weight list (block-uniform; never in the decode step)
+    const size_t z = blockIdx.y;
+    a.w.data += z * a.list_w;
+    if (a.w.scales) a.w.scales += z * a.list_s;
+    if (a.w.zeros) a.w.zeros += z * a.list_s;
+    a.out += z * a.list_out;
+    if (a.partials) a.partials += z * a.list_part;
+  }
   const int lane = T::lane();
   const int stride = gridDim.x * T::kTeams;
   int it = blockIdx.x * T::kTeams + T::team();
@@ -372,10 +386,11 @@ static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks)
   const int blocks = fused_blocks(items, T::kTeams, max_blocks);
   const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
                          : (size_t)a.w.cols * sizeof(double);
+  const dim3 grid(blocks, a.list_count > 1 ? a.list_count : 1);
   if ((size_t)blocks * T::kTeams >= (size_t)items) {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false, F32>), dim3(blocks), dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false, F32>), grid, dim3(kBlock), lds, s, a);
   } else {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true, F32>), dim3(blocks), dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true, F32>), grid, dim3(kBlock), lds, s, a);
   }
   return hipGetLastError();
 }
@@ -436,14 +451,30 @@ hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c) {
   return hipGetLastError();
 }
 
-// The launch of `role` (QKV, ATTENTION, OPROJ, GATEUP or DOWN) for layer L.
-static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role) {
+// Sets a launch up for a weight list (RoleList), else leaves it as the decode step's.
+static void apply_list(FusedArgs& f, const RoleList* list) {
+  if (!list) return;
+  f.w = list->w;
+  f.list_count = list->count;
+  f.list_w = list->w_stride;
+  f.list_s = list->s_stride;
+  f.list_out = list->out_stride;
+  f.list_part = list->part_stride;
+  f.out = list->out;
+  if (list->partials) f.partials = static_cast<ArgPair*>(list->partials);
+}
+
+// The launch of `role` (QKV, ATTENTION, OPROJ, GATEUP or DOWN) for layer L; with `list`, the
+// same launch over a list of copies of its weights (matrix roles only).
+static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role,
+                             const RoleList* list = nullptr) {
   const int kv_dim = m.kv_heads * m.head_dim;
   const LayerDev& l = m.layers_host[L];
   uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
   uint16_t* vt = kc + c.key_elems;
   FusedArgs f{};
   f.f32 = m.numerics == QH_NUMERICS_FAST;
+  if (list && role == QH_ROLE_ATTENTION) return hipErrorInvalidValue;
   switch (role) {
     case QH_ROLE_QKV:
       f.eps = m.eps;
@@ -461,6 +492,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.kv_heads = m.kv_heads;
       f.state = c.state;
       f.capacity = c.capacity;
+      apply_list(f, list);
       return fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2);
     case QH_ROLE_ATTENTION:
       if (m.numerics == QH_NUMERICS_FAST) {
@@ -506,9 +538,11 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         f.in = c.part;
         f.heads = m.heads;
         f.state = c.state;
+        apply_list(f, list);
         return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows);
       }
       f.in = c.attn;
+      apply_list(f, list);
       return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
     case QH_ROLE_GATEUP:
       f.eps = m.eps;
@@ -516,11 +550,13 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.in = c.x;
       f.gain = l.post_norm;
       f.out = c.h;
+      apply_list(f, list);
       return fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2);
     case QH_ROLE_DOWN:
       f.w = l.down;
       f.in = c.h;
       f.out = c.x;
+      apply_list(f, list);
       return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows);
     default:
       return hipErrorInvalidValue;
@@ -528,7 +564,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
 }
 
 // The output head's matvec alone (final rmsnorm, lm_head, logits, block argmax partials).
-static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c) {
+static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c, const RoleList* list = nullptr) {
   FusedArgs f{};
   f.f32 = m.numerics == QH_NUMERICS_FAST;
   f.eps = m.eps;
@@ -537,7 +573,33 @@ static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& 
   f.gain = m.final_norm;
   f.out = c.logits;
   f.partials = static_cast<ArgPair*>(c.lm_partials);
+  apply_list(f, list);
   return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, kLmMaxBlocks);
+}
+
+hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list) {
+  if (role == QH_ROLE_HEAD) return head_matvec(s, m, c, &list);
+  return layer_role(s, m, c, 0, role, &list);
+}
+
+hipError_t enqueue_attention_list(hipStream_t s, const ModelDev& m, const CacheDev& c, const uint16_t* kv,
+                                  int count, size_t copy_elems, float* part) {
+  if (m.numerics != QH_NUMERICS_FAST) return hipErrorInvalidValue;
+  SlotArgs a{};
+  a.q = c.q;
+  a.kc = kv;
+  a.vt = kv + c.key_elems;
+  a.d_pos = c.state;
+  a.part = part;
+  a.capacity = c.capacity;
+  a.vstride = c.vstride;
+  a.heads = m.heads;
+  a.kv_heads = m.kv_heads;
+  a.max_slots = kDecodeSlots;
+  a.list_k = copy_elems;
+  a.list_v = copy_elems;
+  a.list_part = (size_t)m.heads * kDecodeSlots * kPartStride;
+  return launch_attn_slots<kDecodeSlots>(s, a, 1, count);
 }
 
 hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer) {

@@ -19,6 +19,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <functional>
 #include <vector>
 
 #include "model_dev.h"
@@ -966,6 +967,110 @@ int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, 
   if (e1) hipEventDestroy(e1);
   QH_HIP(err);
   *us_per_launch = ms * 1e3f / reps;
+  return QH_OK;
+}
+
+// One decode launch of `role` over copies of its operands that together exceed `min_bytes`
+// (larger than the last-level cache, so every launch streams from HBM): copies of layer 0's
+// matrix for the layer roles, of the output head for QH_ROLE_HEAD, of layer 0's cache for
+// QH_ROLE_ATTENTION. The copies and their outputs are allocated here and freed before return.
+int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
+                               float* us_per_launch, int32_t* copies) {
+  QH_CHECK(m && c && c->m == m && us_per_launch && copies, QH_ERR_INVALID,
+           "kernel_time_cold needs a model, its cache and outputs");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(role >= QH_ROLE_QKV && role <= QH_ROLE_HEAD, QH_ERR_INVALID, "role %d has no single decode kernel", role);
+  QH_CHECK(role != QH_ROLE_ATTENTION || m->dev.numerics == QH_NUMERICS_FAST, QH_ERR_INVALID,
+           "the attention list form is the fast-numerics split-K launch");
+  QH_CHECK(reps >= 1 && min_bytes >= 1 && min_bytes <= ((size_t)64 << 30), QH_ERR_INVALID,
+           "reps must be >= 1 and min_bytes in [1, 64 GiB]");
+  QH_CHECK(c->length < c->dev.capacity, QH_ERR_RANGE, "the cache is full");
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  int rc = set_state(c, c->length, c->length + 1);
+  if (rc) return rc;
+  const qh::ModelDev& md = m->dev;
+  const qh::CacheDev& cd = c->dev;
+  std::vector<void*> held;
+  auto grab = [&](size_t bytes, void** p) -> hipError_t {
+    hipError_t e = hipMalloc(p, bytes);
+    if (e == hipSuccess) held.push_back(*p);
+    return e;
+  };
+  auto round256 = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  hipError_t err = hipSuccess;
+  int count = 1;
+  std::function<hipError_t()> launch;
+  qh::RoleList list{};
+  if (role == QH_ROLE_ATTENTION) {
+    const size_t elems = cd.layer_elems, stride = round256(elems * 2) / 2;
+    count = (int)std::max<size_t>(1, (min_bytes + elems * 2 - 1) / (elems * 2));
+    uint16_t* kv = nullptr;
+    float* part = nullptr;
+    err = grab((size_t)count * stride * 2, (void**)&kv);
+    if (err == hipSuccess) err = grab((size_t)count * md.heads * 16 * 68 * 4, (void**)&part);
+    for (int z = 0; z < count && err == hipSuccess; z++)
+      err = hipMemcpyAsync(kv + (size_t)z * stride, cd.kv, elems * 2, hipMemcpyDeviceToDevice, s);
+    launch = [&, kv, part, stride]() { return qh::enqueue_attention_list(s, md, cd, kv, count, stride, part); };
+  } else {
+    const qh::LayerDev& l = md.layers_host[0];
+    const qh::DMat& w = role == QH_ROLE_HEAD ? md.lm_head
+                        : role == QH_ROLE_QKV ? l.qkv
+                        : role == QH_ROLE_OPROJ ? l.o
+                        : role == QH_ROLE_GATEUP ? l.gu : l.down;
+    const size_t data = (size_t)w.rows * w.row_bytes;
+    const size_t nscale = w.format == QH_FMT_INT4 ? (size_t)w.rows * w.gpr : w.format == QH_FMT_INT8 ? w.rows : 0;
+    const size_t per = data + nscale * 4 * (w.format == QH_FMT_INT4 ? 2 : 1);
+    count = (int)std::max<size_t>(1, (min_bytes + per - 1) / per);
+    const size_t dstride = round256(data), sstride = round256(nscale * 4) / 4;
+    const size_t out_len = role == QH_ROLE_HEAD ? md.vocab : role == QH_ROLE_GATEUP ? md.intermediate : md.hidden;
+    const size_t ostride = round256(out_len * 4) / 4;
+    uint8_t* d = nullptr;
+    float *sc = nullptr, *zr = nullptr, *out = nullptr;
+    void* partials = nullptr;
+    err = grab((size_t)count * dstride, (void**)&d);
+    if (err == hipSuccess && nscale) err = grab((size_t)count * sstride * 4, (void**)&sc);
+    if (err == hipSuccess && w.format == QH_FMT_INT4) err = grab((size_t)count * sstride * 4, (void**)&zr);
+    if (err == hipSuccess) err = grab((size_t)count * ostride * 4, (void**)&out);
+    if (err == hipSuccess) err = hipMemsetAsync(out, 0, (size_t)count * ostride * 4, s);
+    if (err == hipSuccess && role == QH_ROLE_HEAD) err = grab((size_t)count * qh::lm_partials_bytes(md), &partials);
+    for (int z = 0; z < count && err == hipSuccess; z++) {
+      err = hipMemcpyAsync(d + (size_t)z * dstride, w.data, data, hipMemcpyDeviceToDevice, s);
+      if (err == hipSuccess && sc)
+        err = hipMemcpyAsync(sc + (size_t)z * sstride, w.scales, nscale * 4, hipMemcpyDeviceToDevice, s);
+      if (err == hipSuccess && zr)
+        err = hipMemcpyAsync(zr + (size_t)z * sstride, w.zeros, nscale * 4, hipMemcpyDeviceToDevice, s);
+    }
+    list.w = w;
+    list.w.data = d;
+    list.w.scales = sc;
+    list.w.zeros = zr;
+    list.count = count;
+    list.w_stride = dstride;
+    list.s_stride = sstride;
+    list.out_stride = ostride;
+    list.part_stride = (size_t)qh::lm_head_blocks(md);  // argmax partial entries per copy
+    list.out = out;
+    list.partials = partials;
+    launch = [&]() { return qh::enqueue_role_list(s, md, cd, role, list); };
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (err == hipSuccess) err = hipEventCreate(&e0);
+  if (err == hipSuccess) err = hipEventCreate(&e1);
+  if (err == hipSuccess) err = launch();  // warm
+  if (err == hipSuccess) err = hipEventRecord(e0, s);
+  for (int r = 0; r < reps && err == hipSuccess; r++) err = launch();
+  if (err == hipSuccess) err = hipEventRecord(e1, s);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  hipStreamSynchronize(s);
+  for (void* p : held) hipFree(p);
+  QH_HIP(err);
+  *us_per_launch = ms * 1e3f / reps;
+  *copies = count;
   return QH_OK;
 }
 

@@ -117,6 +117,24 @@ hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int
 hipError_t enqueue_gather(hipStream_t s, const ModelDev& m, const CacheDev& c);
 // Launches in one step with logits (the events a StepTimer needs, minus the final one).
 int launches_per_step(const ModelDev& m, StepInput in);
+
+// A decode matrix launch over `count` copies of its weights (for timing it over a working set
+// larger than the last-level cache): copy z at w.data + z * w_stride bytes, its scales / zero
+// points + z * s_stride floats, its output at out + z * out_stride floats, its argmax partials
+// (the head) at partials + z * part_stride entries.
+struct RoleList {
+  DMat w;
+  int count;
+  size_t w_stride, s_stride, out_stride, part_stride;
+  float* out;
+  void* partials;
+};
+// The launch of QH_ROLE_QKV, OPROJ, GATEUP, DOWN (layer 0's operands otherwise) or HEAD over a list.
+hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list);
+// The decode step's split-K attention launch (fast numerics) over `count` copies of one layer's
+// cache (keys then values, copy_elems f16 apart from kv), partials per copy in `part`.
+hipError_t enqueue_attention_list(hipStream_t s, const ModelDev& m, const CacheDev& c, const uint16_t* kv,
+                                  int count, size_t copy_elems, float* part);
 // Blocks the lm_head launch uses (sizes lm_partials).
 int lm_head_blocks(const ModelDev& m);
 size_t lm_partials_bytes(const ModelDev& m);

@@ -677,3 +677,97 @@ hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, voi
 }
 
 }  // namespace qh
+
+namespace qh {
+
+// ------------------------------------------------------------ measurement --
+// What bounds a batch-1 decode launch on this device, measured beside the kernels: the
+// cost of a launch that does nothing, of one that reads a vector the previous launch
+// wrote (every decode launch does), and the rate of a pure streaming read.
+__global__ void k_probe_empty() {}
+
+// A dependent launch: each block reads the whole `n`-float vector the previous launch
+// wrote and writes its 4 entries of the next.
+__global__ __launch_bounds__(kBlock) void k_probe_phase(const float* __restrict__ in, float* __restrict__ out, int n) {
+  __shared__ float red[kBlock / kWave];
+  float v = 0.f;
+  for (int i = threadIdx.x; i < n; i += kBlock) v += in[i];
+  v = team_sum<64>(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  const int i = blockIdx.x * 4 + threadIdx.x;
+  if (threadIdx.x < 4 && i < n) out[i] = ((red[0] + red[1]) + (red[2] + red[3])) * 1e-3f + (float)threadIdx.x;
+}
+
+// Streams n16 16-byte units once (four independent loads in flight per thread per step);
+// one word per block is written so the loads are kept.
+__global__ __launch_bounds__(kBlock) void k_read_ceiling(const v4u* __restrict__ p, size_t n16, uint32_t* __restrict__ sink) {
+  const size_t stride = (size_t)gridDim.x * kBlock;
+  uint32_t acc = 0;
+  size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const v4u a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + stride);
+    const v4u c = __builtin_nontemporal_load(p + i + 2 * stride), d = __builtin_nontemporal_load(p + i + 3 * stride);
+    acc ^= (a.x ^ b.y) ^ (c.z ^ d.w);
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(p + i).x;
+  acc = __builtin_amdgcn_readfirstlane(acc) ^ (uint32_t)team_sum<64>((float)(acc & 0xffff));
+  if (threadIdx.x == 0) sink[blockIdx.x] = acc;
+}
+
+hipError_t probe_launch_floor(hipStream_t s, int kind, int blocks, int launches, float* buf, float* us_per_launch) {
+  hipGraph_t g = nullptr;
+  hipGraphExec_t ge = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+  for (int i = 0; i < launches && e == hipSuccess; i++) {
+    if (kind == 0) hipLaunchKernelGGL(k_probe_empty, dim3(blocks), dim3(kBlock), 0, s);
+    else hipLaunchKernelGGL(k_probe_phase, dim3(blocks), dim3(kBlock), 0, s, buf + (i & 1) * 4096,
+                            buf + ((i + 1) & 1) * 4096, kind == 1 ? 896 : 0);
+    e = hipGetLastError();
+  }
+  const hipError_t ec = hipStreamEndCapture(s, &g);
+  if (e == hipSuccess) e = ec;
+  if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  if (e == hipSuccess) e = hipGraphLaunch(ge, s);  // warm
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  const int reps = 10;
+  if (e == hipSuccess) e = hipEventRecord(e0, s);
+  for (int r = 0; r < reps && e == hipSuccess; r++) e = hipGraphLaunch(ge, s);
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (ge) hipGraphExecDestroy(ge);
+  if (g) hipGraphDestroy(g);
+  if (e == hipSuccess) *us_per_launch = ms * 1e3f / (reps * launches);
+  return e;
+}
+
+hipError_t read_ceiling(hipStream_t s, const void* p, size_t bytes, int reps, uint32_t* sink, float* ms_per_read) {
+  const int blocks = 4096;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  const v4u* v = static_cast<const v4u*>(p);
+  hipLaunchKernelGGL(k_read_ceiling, dim3(blocks), dim3(kBlock), 0, s, v, bytes / 16, sink);  // warm
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipEventRecord(e0, s);
+  for (int r = 0; r < reps && e == hipSuccess; r++) {
+    hipLaunchKernelGGL(k_read_ceiling, dim3(blocks), dim3(kBlock), 0, s, v, bytes / 16, sink);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  if (e0) hipEventDestroy(e0);
+  if (e1) hipEventDestroy(e1);
+  if (e == hipSuccess) *ms_per_read = ms / reps;
+  return e;
+}
+
+}  // namespace qh

@@ -167,6 +167,11 @@ size_t attention_list_partials_floats(int count, int heads, int ctx);
 // f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).
 void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
+// Measurement: `launches` launches captured as one graph and replayed (kind 0: empty; 1: each
+// reads the 896-float vector the previous one wrote, in buf [2][4096]; 2: the same launch reading
+// nothing), and a streaming read of `bytes` (sink: 4096 words).
+hipError_t probe_launch_floor(hipStream_t s, int kind, int blocks, int launches, float* buf, float* us_per_launch);
+hipError_t read_ceiling(hipStream_t s, const void* p, size_t bytes, int reps, uint32_t* sink, float* ms_per_read);
 hipError_t launch_add(hipStream_t s, float* x, const float* delta, int n);
 // dst[0, bytes) = src[0, bytes): 16-byte vector copies when both are 16-byte aligned,
 // bytes otherwise.

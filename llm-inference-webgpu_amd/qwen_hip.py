@@ -264,6 +264,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_model_load_tensor": [vp, ctypes.c_char_p, i32, i32, i32, vp, i32, i32],
         "qh_model_finalize": [vp], "qh_model_free": [vp], "qh_model_bytes": [vp, vp],
         "qh_model_config": [vp, vp],
+        "qh_decode_kernel_time_cold": [vp, vp, i32, sz, i32, vp, vp],
+        "qh_probe_launch_floor": [vp, i32, i32, i32, vp], "qh_read_ceiling": [vp, sz, i32, vp],
         "qh_model_set_numerics": [vp, i32], "qh_model_set_matmul": [vp, i32],
         "qh_cache_create": [vp, i32, vp], "qh_cache_free": [vp], "qh_cache_length": [vp, vp],
         "qh_cache_set_length": [vp, i32], "qh_cache_present": [vp, i32, vp, vp],
@@ -470,6 +472,19 @@ class GpuContext:
         if self.handle:
             _check(self.lib.qh_close(self.handle))
             self.handle = None
+
+    def launch_floor(self, kind: int, blocks: int = 224, launches: int = 200) -> float:
+        """Microseconds per launch of `launches` graph-replayed probe launches (qh_probe_launch_floor:
+        kind 0 empty, 1 reading the previous launch's output, 2 reading nothing)."""
+        us = ctypes.c_float()
+        _check(self.lib.qh_probe_launch_floor(self.handle, kind, blocks, launches, ctypes.byref(us)))
+        return us.value
+
+    def read_ceiling(self, nbytes: int = 1 << 30, reps: int = 10) -> float:
+        """GB/s of a pure streaming read of nbytes (qh_read_ceiling)."""
+        g = ctypes.c_float()
+        _check(self.lib.qh_read_ceiling(self.handle, nbytes, reps, ctypes.byref(g)))
+        return g.value
 
     def describe(self) -> str:
         buf = ctypes.create_string_buffer(512)
@@ -880,6 +895,14 @@ class GpuModel:
         _check(self.lib.qh_decode_kernel_time(self.handle, cache.handle, ROLES.index(role), reps,
                                               ctypes.byref(us)))
         return us.value
+
+    def kernel_time_cold(self, cache: GpuKVCache, role: str, min_bytes: int = 512 << 20, reps: int = 5):
+        """(microseconds per launch, copies): one launch of `role` over copies of its operands
+        exceeding min_bytes (see qh_decode_kernel_time_cold)."""
+        us, n = ctypes.c_float(), ctypes.c_int32()
+        _check(self.lib.qh_decode_kernel_time_cold(self.handle, cache.handle, ROLES.index(role), min_bytes, reps,
+                                                   ctypes.byref(us), ctypes.byref(n)))
+        return us.value, n.value
 
     def destroy(self) -> None:
         if self.handle:
