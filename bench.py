@@ -23,8 +23,18 @@ Also reported on the same JSON line:
   matvec_isolated  BASELINE config 2: int8 matvec with an f16 activation at the
                  five layer shapes, one list-driven launch over >= 512 MiB of
                  distinct matrices (larger than the 256 MB last-level cache)
+  attention_decode  BASELINE config 3: split-K GQA attention over f16 caches at contexts
+                 128 .. 32768, one list-driven launch over >= 512 MiB of distinct caches
+  prefill_512    BASELINE config 5: time to first token of a 512-token prompt through each
+                 matmul path (per-position matvec, 8-position batched tiles, MFMA)
   loader         the load path's conversion kernels (bf16 checkpoint -> int8 / int4 / f16
                  on the device) in GB/s, and the whole model load, host- vs device-converted
+  path_comparison  the same-session comparison of the matmul paths (web/scaling.html): the
+                 paths checked to compute the same model, then prompt time-to-logits at 1 ..
+                 512 tokens and single-token steps, median/min/max per path
+  greedy_match   every timed token against the CPU oracle continuing from the GPU's cache
+                 (teacher-forced), the smallest top-2 margin, and per layer the max-abs
+                 relative error and cosine of the K/V rows the decoded positions stored
   cpu_baseline   the reference's src/cpu path restated in JavaScript (oracle/cpu_model.js)
                  timed under Node on one host core over a bounded sample of the same
                  workload; cpu_baseline_c the C oracle on the same sample
@@ -168,8 +178,9 @@ def cold_decode_kernels(model, cache, cfg, ctx_len, ceiling, reps=5):
         nbytes = copies * per_copy[role]
         gbs = nbytes / (us * 1e-6) / 1e9
         out[role] = {"copies": copies, "bytes_per_launch": nbytes, "us_per_launch": round(us, 2),
-                     "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "frac_of_read_ceiling": round(gbs / ceiling, 4)}
+                     "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        if ceiling:
+            out[role]["frac_of_read_ceiling"] = round(gbs / ceiling, 4)
         log(f"cold {role}: {copies} copies, {us:.1f} us, {gbs:.0f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
     return out
 
@@ -335,9 +346,36 @@ def greedy_check(cfg, ckpt, cache, first, gpu_tokens, context):
         matched += int(O.argmax(logits) == gpu_tokens[i])
         top = np.partition(logits.astype(np.float64), -2)[-2:]
         margins.append(float(top[1] - top[0]))
+    seconds = time.perf_counter() - t0
     return {"matched_compared": f"{matched}/{len(fed)}", "min_top2_margin": round(min(margins), 6),
             "teacher_forced": True, "oracle": "oracle/liboracle.so (f64 sums)", "threads": threads,
-            "seconds": round(time.perf_counter() - t0, 1)}
+            "seconds": round(seconds, 1), "per_layer": per_layer_kv(cfg, cache, oc, context, len(fed))}
+
+
+def per_layer_kv(cfg, cache, oc, start, n):
+    """Each layer's output at the decoded positions start..start+n-1 -- the K and V rows it
+    stored -- on the GPU against the oracle's for the same fed tokens: max-abs relative (over
+    max |oracle|) and cosine per layer (test/model.test.js:39 holds layers to 5e-4). Both
+    caches hold f16 values; the oracle's were computed from its own f64 sums."""
+    def rel(a, b):
+        return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+    def cos(a, b):
+        return float(a.ravel() @ b.ravel() / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+    out = {"positions": [start, start + n - 1], "layers": cfg.layers}
+    for kind in ("key", "value"):
+        errs, coss = [], []
+        for L in range(cfg.layers):
+            a = cache.present(L)[kind][:, start:start + n].astype(np.float64)
+            b = oc.present(L)[kind][:, start:start + n].astype(np.float64)
+            errs.append(rel(a, b))
+            coss.append(cos(a, b))
+        out[f"{kind}_max_abs_rel"] = [float(f"{e:.3g}") for e in errs]
+        out[f"{kind}_cosine"] = [round(c, 9) for c in coss]
+    out["worst_max_abs_rel"] = max(max(out["key_max_abs_rel"]), max(out["value_max_abs_rel"]))
+    out["min_cosine"] = min(min(out["key_cosine"]), min(out["value_cosine"]))
+    return out
 
 
 def cpu_baseline(cfg, ckpt, cache, first, gpu_tokens, steps, context):
@@ -388,7 +426,7 @@ def mfma_same_f16_check(model, cfg, ckpt, hidden, seq):
 
 
 def scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 32, 52, 64, 128, 256, 512, 1024), repeats=5,
-                  decode_steps=24, paths=("matvec", "batched", "mfma")):
+                  decode_steps=24, paths=("matvec", "batched", "mfma"), oracle_check=True):
     """The same-session path comparison of web/scaling.html:40-194: time-to-logits of a prompt
     through each matmul path (median/min/max of `repeats`, the path order rotated every repeat),
     after a check at 52 tokens that the paths compute the same model (batched bit-identical to
@@ -423,7 +461,8 @@ def scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 32, 52, 64, 128, 256, 512, 1024
     if "mfma" in outs:
         agree["mfma_max_relative"] = float(np.max(np.abs(outs["mfma"]["logits"].astype(np.float64) - m))
                                            / np.max(np.abs(m)))
-        agree["mfma_vs_same_f16_cpu"] = mfma_same_f16_check(model, cfg, ckpt, hidden[:52 * d], 52)
+        if oracle_check:
+            agree["mfma_vs_same_f16_cpu"] = mfma_same_f16_check(model, cfg, ckpt, hidden[:52 * d], 52)
     ok = agree["batched_differing"] == 0 and len(set(agree["argmax"].values())) == 1 and \
         agree.get("mfma_vs_same_f16_cpu", 0.0) <= LOGIT_REL
     if not ok:
@@ -556,6 +595,9 @@ def main():
                     help="only the same-session comparison of the matmul paths over prompt lengths")
     ap.add_argument("--loader-only", action="store_true",
                     help="only the loader's conversion kernels and the two whole-model loads")
+    ap.add_argument("--cold-only", action="store_true",
+                    help="only the decode step's launches timed cold over >= 512 MiB of operand "
+                         "copies after the prompt, for the rocprofv3 counter passes over them")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
                     help="decode by hipGraph replay (default) or direct launches of the same "
                          "kernels (for profilers that do not follow graph launches)")
@@ -602,6 +644,14 @@ def main():
     prefill_s = time.perf_counter() - t0
     log(f"prefilled {args.context} positions in {prefill_s:.2f}s (8-position batched tiles)")
 
+    if args.cold_only:
+        print(json.dumps({"decode_kernels_cold": cold_decode_kernels(model, cache, cfg, args.context, None)}),
+              flush=True)
+        cache.destroy()
+        model.destroy()
+        ctx.close()
+        return
+
     # The decode graphs are captured and uploaded here, outside the timed region.
     model.decode_prepare(cache)
     if args.warmup:
@@ -621,6 +671,16 @@ def main():
     tok_s = args.steps / (ms / 1e3)
     log(f"decode: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms (wall): {tok_s:.0f} tok/s")
 
+    # Each role's own launches probed at the row after the timed tokens (they append K/V at
+    # their position, so the rows the decode stored stay as decoded): 240 of the step's launches
+    # of it back to back on the library's stream between two events (no event between launches;
+    # its 24 weight sets cache-resident), then one launch cold over >= 512 MiB of copies.
+    probe = args.context + args.steps
+    cache.length = probe
+    back_to_back = {r: round(model.kernel_time(cache, r, 240), 3)
+                    for r in ("qkv", "attention", "oproj", "gateup", "down", "head")}
+    cold = cold_decode_kernels(model, cache, cfg, probe, None)
+
     # In-situ per-kernel times over the same positions.
     cache.length = args.context
     psteps = min(args.profile_steps, args.steps)
@@ -636,14 +696,12 @@ def main():
                          "launches_per_token": n // psteps,
                          "GBps": round(rb[r] * n / (tot_ms * 1e-3) / 1e9, 1)}
     dominant = max(per_kernel, key=lambda r: per_kernel[r]["us_per_token"])
-    # The dominant kernel's own duration: 240 of the step's launches of it back to back on the
-    # library's stream between two events (no event between launches), at the next position.
-    cache.length = args.context + psteps
     for r in per_kernel:
-        if r != "embed":   # each role's own launches back to back (its 24 weight sets cache-resident)
-            per_kernel[r]["us_back_to_back"] = round(model.kernel_time(cache, r, 240), 3)
+        if r in back_to_back:
+            per_kernel[r]["us_back_to_back"] = back_to_back[r]
+    # The dominant kernel's own duration is its back-to-back launch time.
     kernel_us = per_kernel[dominant]["us_back_to_back"]
-    kbytes = role_bytes(cfg, args.context + psteps)[dominant]
+    kbytes = role_bytes(cfg, probe)[dominant]
     achieved = kbytes / (kernel_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
@@ -651,12 +709,12 @@ def main():
                 "us_per_launch": round(kernel_us, 3)}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
-    # What bounds the step, and the step's own launches timed cold (at the position the in-situ
-    # timing used, past the timed tokens, so the cache rows the CPU check reads stay as decoded).
+    # What bounds the step; the cold launches against the read ceiling.
     bounds = decode_bounds(ctx, sum(v["launches_per_token"] for v in per_kernel.values()))
-    cold = cold_decode_kernels(model, cache, cfg, args.context + psteps, bounds["read_ceiling_GBps"])
+    for v in cold.values():
+        v["frac_of_read_ceiling"] = round(v["GBps"] / bounds["read_ceiling_GBps"], 4)
 
-    iso = attn = prefill = loader = None
+    iso = attn = prefill = loader = paths = None
     if args.isolated == "all":
         d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
         iso = isolated_matvec(ctx, [("q_o", d, d), ("k_v", kv, d), ("gate_up", ffn, d),
@@ -664,6 +722,8 @@ def main():
         attn = attention_sweep(ctx)
         prefill = prefill_bench(ctx, cfg, ckpt, args.seed)
         loader = loader_bench(ctx, cfg, ckpt)
+        paths = scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 64, 256, 512), repeats=3, decode_steps=12,
+                              oracle_check=not args.no_cpu)
 
     cpu = match = cpu_c = match_c = greedy = None
     if not args.no_cpu:
@@ -703,6 +763,7 @@ def main():
         "attention_decode": attn,
         "prefill_512": prefill,
         "loader": loader,
+        "path_comparison": paths,
         "prefill_s": round(prefill_s, 3),
     }
     print(json.dumps(line), flush=True)
