@@ -374,6 +374,141 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs a) {
   }
 }
 
+// The int8 contraction with whole weight lines: a stage of 128 columns (two MFMA K steps)
+// per barrier, so a weight row's 128 bytes of the stage are one cache line, read by eight
+// consecutive lanes -- a wave's load instruction covers 8 whole lines instead of 32 halves
+// (the per-CU rate of line requests, not bytes, bounds this kernel). Same block tile,
+// fragments and exact integer sums as k_gemm<int8>, so a split's outputs are the same bits.
+constexpr int kSK = 2 * kGK;        // columns staged per barrier
+constexpr int kSRow = kSK + 16;     // bytes per LDS row: 128 + 16 of padding (rows 36 banks apart)
+constexpr int kSStages = 2;         // stages of global loads in flight
+constexpr int kSLoads = kGN * kSK / 16 / kGemmThreads;  // 16-byte weight loads per thread per stage
+
+__global__ __launch_bounds__(kGemmThreads) void k_gemm8w(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t Bs[2][kGN][kSRow];
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  // Tile of this block. Workgroups are dealt to the 8 XCDs (8 separate L2s) round-robin by
+  // linear id. With K split (gridDim.z > 1) and (position tiles x splits) a multiple of 8,
+  // the ids are remapped so that the X weight tiles of one (position tile, split) run on one
+  // XCD and an XCD's groups share a split: each L2 then holds one K slice of the weights and
+  // a few position tiles' digits (~2 MB for down at M = 512) instead of all of both.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  {
+    const int X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
+    if (Z > 1 && (Y * Z) % 8 == 0) {
+      const int b = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);
+      const int xcd = b & 7, r = b >> 3;
+      const int gi = xcd + 8 * (r / X);  // (position tile, split) group, = xcd mod 8
+      bx = r % X;
+      bz = gi % Z;
+      by = gi / Z;
+    }
+  }
+  const int m0 = by * kGM, n0 = bx * kGN;
+  const int s0 = bz * a.steps_per_split;  // even: splits fall on stage boundaries
+  const int s1 = min(s0 + a.steps_per_split, a.Kp / kGK);
+  const int g0 = s0 / 2, g1 = (s1 + 1) / 2;       // stages; the last may hold one step
+  const int fr = lane & 15, fg = lane >> 4;
+  const int mw = m0 + 16 * wave;
+  const bool active = mw < a.M;
+
+  const int Mp = digit_rows(a.M);
+  const int8_t* ar = a.digits + (size_t)min(mw, Mp - 16) * kGK + 16 * lane;
+  const size_t dplane = (size_t)Mp * kGK;
+  // Weight staging: load i of thread t is row 32 i + t / 8 of the tile, bytes 16 (t % 8) ..
+  // +15 of the stage (rows past N re-read the last row; their outputs are dropped).
+  const int wrow = tid >> 3, wcol = 16 * (tid & 7);
+  const uint8_t* wsrc[kSLoads];
+#pragma unroll
+  for (int i = 0; i < kSLoads; i++)
+    wsrc[i] = a.w.data + (size_t)min(n0 + 32 * i + wrow, a.N - 1) * a.w.row_bytes;
+
+  // The epilogue's factors, loaded before the K loop so that no memory round trip is left
+  // behind it: the four rows' factors, and each tile column's row scale and bias.
+  double rf[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) rf[r] = a.row_factor[min(mw + 4 * fg + r, a.M - 1)];
+  // Unconditional loads (a branch around one makes the compiler wait for each in turn):
+  // without a bias the scales are read in its place and multiplied by zero.
+  const float* bsrc = a.bias ? a.bias : a.w.scales;
+  const float bmul = a.bias ? 1.f : 0.f;
+  float cs[kNT], bias[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; j++) {
+    const int n = min(n0 + 16 * j + fr, a.N - 1);
+    cs[j] = a.w.scales[n];
+    bias[j] = bsrc[n];
+  }
+
+  v4i acc[kDigits][kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; j++)
+#pragma unroll
+    for (int d = 0; d < kDigits; d++) acc[d][j] = v4i{0, 0, 0, 0};
+
+  v4i xa[kSStages][2][kDigits];
+  v4u wv[kSStages][kSLoads];
+  // Unconditional, clamped loads: a stage past the split's last re-reads that last one (never
+  // used); a step past s1 re-reads step s1 - 1 (its MFMAs are skipped); weight columns past
+  // K re-read columns K - 16 .. K - 1, which meet zero digits.
+  auto issue = [&](int g, v4i (&x)[2][kDigits], v4u (&w)[kSLoads]) {
+    const int gg = min(g, g1 - 1);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int st = min(2 * gg + h, s1 - 1);
+#pragma unroll
+      for (int d = 0; d < kDigits; d++) x[h][d] = *reinterpret_cast<const v4i*>(ar + (size_t)(st * kDigits + d) * dplane);
+    }
+    const int col = min(gg * kSK + wcol, a.K - 16);
+#pragma unroll
+    for (int i = 0; i < kSLoads; i++) w[i] = *reinterpret_cast<const v4u*>(wsrc[i] + col);
+  };
+#pragma unroll
+  for (int u = 0; u < kSStages; u++) issue(g0 + u, xa[u], wv[u]);
+  auto stage = [&](auto U, int g) {
+    constexpr int u = decltype(U)::value;
+    const int buf = (g - g0) & 1;
+#pragma unroll
+    for (int i = 0; i < kSLoads; i++) *reinterpret_cast<v4u*>(&Bs[buf][32 * i + wrow][wcol]) = wv[u][i];
+    // One barrier per stage: Bs[buf] is complete, and every wave finished reading it two
+    // stages ago (each wave reads a buffer before it arrives at the next barrier).
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        if (2 * g + h < s1) {  // block-uniform
+          v4i fb[kNT];
+#pragma unroll
+          for (int j = 0; j < kNT; j++) fb[j] = *reinterpret_cast<const v4i*>(&Bs[buf][16 * j + fr][kGK * h + 16 * fg]);
+#pragma unroll
+          for (int d = 0; d < kDigits; d++)
+#pragma unroll
+            for (int j = 0; j < kNT; j++)
+              acc[d][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[u][h][d], fb[j], acc[d][j], 0, 0, 0);
+        }
+      }
+    }
+    issue(g + kSStages, xa[u], wv[u]);
+  };
+  int g = g0;
+  for (; g + kSStages <= g1; g += kSStages) step_group(stage, g, g1, std::make_integer_sequence<int, kSStages>{});
+  step_group(stage, g, g1, std::make_integer_sequence<int, kSStages - 1>{});
+  if (!active) return;
+
+  float* dst = a.out + (size_t)bz * a.M * a.N;
+#pragma unroll
+  for (int j = 0; j < kNT; j++) {
+    const int n = n0 + 16 * j + fr;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = mw + 4 * fg + r;
+      const double v = (double)acc[2][j][r] * 65536.0 + (double)acc[1][j][r] * 256.0 + (double)acc[0][j][r];
+      if (m < a.M) dst[(size_t)m * a.N + n] = (float)(v * rf[r] * (double)cs[j] + (double)(bias[j] * bmul));
+    }
+  }
+}
+
 // Y = sum over splits of the partial tiles (in split order) + bias.
 __global__ void k_gemm_finish(const float* __restrict__ part, int splits, const float* __restrict__ bias,
                               float* __restrict__ y, int M, int N) {
@@ -395,10 +530,11 @@ bool matmul_prefill_supported(const DMat& w) {
 // CU, int4 splits on group boundaries. A CU holding two blocks runs each at well under half
 // speed (its L2 load rate is the bound), and every split adds an M x N partial that the
 // consumer row kernel reads back: 512-token prefill 3.6 ms at two blocks per CU, 3.4 ms at one.
+// int8 splits fall on whole 128-column stages (k_gemm8w).
 static int gemm_steps_per_split(const DMat& w, int M) {
   const int steps = padded_k(w.cols) / kGK;
   const int tiles = ((M + kGM - 1) / kGM) * ((w.rows + kGN - 1) / kGN);
-  const int unit = w.format == QH_FMT_INT4 ? w.cpg / 2 : 1;
+  const int unit = w.format == QH_FMT_INT4 ? w.cpg / 2 : kSK / kGK;
   int splits = 256 / tiles;
   splits = std::max(1, std::min(splits, steps / unit));
   int per = (steps + splits - 1) / splits;
@@ -447,7 +583,7 @@ hipError_t launch_gemm_digits(hipStream_t s, const DMat& w, const int8_t* digits
   a.Kp = Kp;
   a.steps_per_split = gemm_steps_per_split(w, M);
   const dim3 grid((w.rows + kGN - 1) / kGN, (M + kGM - 1) / kGM, splits);
-  if (w.format == QH_FMT_INT8) hipLaunchKernelGGL(k_gemm<QH_FMT_INT8>, grid, dim3(kGemmThreads), 0, s, a);
+  if (w.format == QH_FMT_INT8) hipLaunchKernelGGL(k_gemm8w, grid, dim3(kGemmThreads), 0, s, a);
   else hipLaunchKernelGGL(k_gemm<QH_FMT_INT4>, grid, dim3(kGemmThreads), 0, s, a);
   *splits_out = splits;
   return hipGetLastError();
