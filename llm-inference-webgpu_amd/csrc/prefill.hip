@@ -73,64 +73,102 @@ __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v 
 // next contraction: s = max|y| / 127, X = rint(y * 2^16 / s) in three balanced base-256
 // digits (step-major, digit_offset), zeros past n, and the row factor s * 2^-16 (NaN for a
 // row holding an infinity or a NaN, whose digits are zero).
-template <int OP>
+//
+// Every load is issued before any is used, from a clamped address (a lane past the row re-reads
+// its last group and masks it out): a load behind a branch, or inside a loop whose count is
+// only known at run time, makes the compiler wait for each in turn. J = float4 groups per
+// thread (rows of up to 1024 J values); the splits are read U at a time (four for the split
+// contractions' rows; the gate|up contraction is not split) and added in order.
+template <int OP, int J>
 __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   __shared__ float red[kBlock / kWave];
-  constexpr int kMaxVec = 8;  // float4 per thread: 8192 values
+  constexpr int W = OP == ROW_SWIGLU ? 2 : 1;  // float4 loads per group and split
+  constexpr int U = OP == ROW_SWIGLU ? 1 : 4;  // splits read together
   const int m = blockIdx.x, tid = threadIdx.x;
   const int n4 = a.n / 4;
-  const int in_len = OP == ROW_SWIGLU ? 2 * a.n : a.n;
+  const int in_len = W * a.n;
   const size_t plane_in = (size_t)a.M * in_len;
   const float* in_row = a.in + (size_t)m * in_len;
-  v4f v[kMaxVec];
+  int idx[J];
+  bool ok[J];
 #pragma unroll
-  for (int j = 0; j < kMaxVec; j++) {
-    const int i4 = tid + j * kBlock;
-    v[j] = v4f{0.f, 0.f, 0.f, 0.f};
-    if (i4 >= n4) continue;
-    if constexpr (OP == ROW_SWIGLU) {
-      v4f g0 = {0.f, 0.f, 0.f, 0.f}, g1 = g0;
-      for (int sp = 0; sp < a.splits; sp++) {
-        g0 += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 8 * i4);
-        g1 += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 8 * i4 + 4);
-      }
-      if (a.bias) {
-        g0 += *reinterpret_cast<const v4f*>(a.bias + 8 * i4);
-        g1 += *reinterpret_cast<const v4f*>(a.bias + 8 * i4 + 4);
-      }
-      v[j] = v4f{swiglu_f32(g0[0], g0[1]), swiglu_f32(g0[2], g0[3]), swiglu_f32(g1[0], g1[1]),
-                 swiglu_f32(g1[2], g1[3])};
-    } else {
-      v4f x = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < a.splits; sp++) x += *reinterpret_cast<const v4f*>(in_row + sp * plane_in + 4 * i4);
-      if (a.bias) x += *reinterpret_cast<const v4f*>(a.bias + 4 * i4);
-      v[j] = x;
+  for (int j = 0; j < J; j++) {
+    ok[j] = tid + j * kBlock < n4;
+    idx[j] = min(tid + j * kBlock, n4 - 1);
+  }
+  // Residual, gain and bias first (read from the row itself where there is none).
+  float* resid_row = a.resid ? a.resid + (size_t)m * a.n : nullptr;
+  const float* rsrc = a.resid ? resid_row : in_row;
+  const float* gsrc = OP == ROW_RMSNORM ? a.gain : in_row;
+  const float* bsrc = a.bias ? a.bias : in_row;
+  v4f res[J], gain[J], bias[J][W];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    res[j] = *reinterpret_cast<const v4f*>(rsrc + 4 * idx[j]);
+    if constexpr (OP == ROW_RMSNORM) gain[j] = *reinterpret_cast<const v4f*>(gsrc + 4 * idx[j]);
+#pragma unroll
+    for (int w = 0; w < W; w++) bias[j][w] = *reinterpret_cast<const v4f*>(bsrc + 4 * (W * idx[j] + w));
+  }
+  v4f sum[J][W];
+#pragma unroll
+  for (int j = 0; j < J; j++)
+#pragma unroll
+    for (int w = 0; w < W; w++) sum[j][w] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = 0; sp0 < a.splits; sp0 += U) {
+    v4f t[U][J][W];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float* src = in_row + (size_t)min(sp0 + u, a.splits - 1) * plane_in;
+#pragma unroll
+      for (int j = 0; j < J; j++)
+#pragma unroll
+        for (int w = 0; w < W; w++) t[u][j][w] = *reinterpret_cast<const v4f*>(src + 4 * (W * idx[j] + w));
     }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (sp0 + u < a.splits) {  // block-uniform
+#pragma unroll
+        for (int j = 0; j < J; j++)
+#pragma unroll
+          for (int w = 0; w < W; w++) sum[j][w] += t[u][j][w];
+      }
+    }
+  }
+  v4f v[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    if (a.bias) {
+#pragma unroll
+      for (int w = 0; w < W; w++) sum[j][w] += bias[j][w];
+    }
+    if constexpr (OP == ROW_SWIGLU)
+      v[j] = v4f{swiglu_f32(sum[j][0][0], sum[j][0][1]), swiglu_f32(sum[j][0][2], sum[j][0][3]),
+                 swiglu_f32(sum[j][1][0], sum[j][1][1]), swiglu_f32(sum[j][1][2], sum[j][1][3])};
+    else
+      v[j] = sum[j][0];
     if (a.resid) {
-      v4f* r = reinterpret_cast<v4f*>(a.resid + (size_t)m * a.n + 4 * i4);
-      v[j] = *r + v[j];
-      *r = v[j];
+      v[j] = res[j] + v[j];
+      if (ok[j]) *reinterpret_cast<v4f*>(resid_row + 4 * idx[j]) = v[j];
     }
+    if (!ok[j]) v[j] = v4f{0.f, 0.f, 0.f, 0.f};
   }
   if constexpr (OP == ROW_RMSNORM) {
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxVec; j++)
+    for (int j = 0; j < J; j++)
 #pragma unroll
       for (int e = 0; e < 4; e++) ss = fmaf(v[j][e], v[j][e], ss);
     ss = block_sum_f32(ss, red);
     const float scale = __builtin_amdgcn_rsqf(ss / (float)a.n + a.eps);
     __syncthreads();  // red is reused below
 #pragma unroll
-    for (int j = 0; j < kMaxVec; j++) {
-      const int i4 = tid + j * kBlock;
-      if (i4 < n4) v[j] = rms_apply_f32(v[j], scale, *reinterpret_cast<const v4f*>(a.gain + 4 * i4));
-    }
+    for (int j = 0; j < J; j++)
+      if (ok[j]) v[j] = rms_apply_f32(v[j], scale, gain[j]);
   }
   if (!a.digits) return;
   float peak = 0.f;
 #pragma unroll
-  for (int j = 0; j < kMaxVec; j++)
+  for (int j = 0; j < J; j++)
 #pragma unroll
     for (int e = 0; e < 4; e++) peak = peak_of(peak, fabsf(v[j][e]));
   for (int off = kWave / 2; off > 0; off >>= 1) peak = peak_of(peak, __shfl_xor(peak, off));
@@ -144,17 +182,15 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   const double inv = finite && peak > 0.f ? 65536.0 / s : 0.0;
   if (tid == 0) a.row_factor[m] = finite ? s / 65536.0 : (double)NAN;
   const int Mp = digit_rows(a.M);
-  for (int j = 0; 4 * (tid + j * kBlock) < a.Kp; j++) {
+#pragma unroll
+  for (int j = 0; j < J; j++) {
     const int i4 = tid + j * kBlock;
+    if (4 * i4 >= a.Kp) break;
     uint32_t w[kDigits] = {0, 0, 0};
     if (i4 < n4 && inv != 0.0) {
-      v4f x = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jj = 0; jj < kMaxVec; jj++)
-        if (jj == j) x = v[jj];
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        int q = (int)rint((double)x[e] * inv);  // |q| <= 127 * 2^16
+        int q = (int)rint((double)v[j][e] * inv);  // |q| <= 127 * 2^16
 #pragma unroll
         for (int d = 0; d < kDigits; d++) {
           const int dig = (int)(int8_t)(uint8_t)(q & 0xff);  // balanced: [-128, 127]
@@ -169,15 +205,25 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   }
 }
 
+template <int OP>
+static hipError_t launch_rows_op(hipStream_t s, const RowArgs& a) {
+  const int groups = (a.n / 4 + kBlock - 1) / kBlock;  // float4 groups per thread
+  if (groups <= 1) hipLaunchKernelGGL((k_rows<OP, 1>), dim3(a.M), dim3(kBlock), 0, s, a);
+  else if (groups <= 2) hipLaunchKernelGGL((k_rows<OP, 2>), dim3(a.M), dim3(kBlock), 0, s, a);
+  else if (groups <= 4) hipLaunchKernelGGL((k_rows<OP, 4>), dim3(a.M), dim3(kBlock), 0, s, a);
+  else if (groups <= 5) hipLaunchKernelGGL((k_rows<OP, 5>), dim3(a.M), dim3(kBlock), 0, s, a);
+  else hipLaunchKernelGGL((k_rows<OP, 8>), dim3(a.M), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_rows(hipStream_t s, int op, const RowArgs& a) {
-  if (a.n % 4 || a.n > 8192 || (a.digits && a.Kp != padded_k(a.n))) return hipErrorInvalidValue;
+  if (a.n % 4 || a.n > 8192 || a.splits < 1 || (a.digits && a.Kp != padded_k(a.n))) return hipErrorInvalidValue;
   switch (op) {
-    case ROW_PLAIN: hipLaunchKernelGGL(k_rows<ROW_PLAIN>, dim3(a.M), dim3(kBlock), 0, s, a); break;
-    case ROW_RMSNORM: hipLaunchKernelGGL(k_rows<ROW_RMSNORM>, dim3(a.M), dim3(kBlock), 0, s, a); break;
-    case ROW_SWIGLU: hipLaunchKernelGGL(k_rows<ROW_SWIGLU>, dim3(a.M), dim3(kBlock), 0, s, a); break;
+    case ROW_PLAIN: return launch_rows_op<ROW_PLAIN>(s, a);
+    case ROW_RMSNORM: return launch_rows_op<ROW_RMSNORM>(s, a);
+    case ROW_SWIGLU: return launch_rows_op<ROW_SWIGLU>(s, a);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ weight tile --
