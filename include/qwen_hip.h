@@ -336,9 +336,11 @@ int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens
  * reference, which records every step anew (src/gpu/model.js:261). */
 int qh_decode_prepare(qh_model* m, qh_cache* c);
 /* use_graph = 0: later decodes on this cache enqueue every kernel of a step directly instead
- * of replaying the captured graph (same kernels, same tokens), for tools that cannot follow
- * graph launches. No counterpart in the reference, which re-encodes every step
- * (src/gpu/model.js:261). Default 1. */
+ * of replaying the captured graph (same kernels, same tokens), and batched forwards enqueue
+ * every layer's kernels directly instead of replaying the graph of a prompt shape (first
+ * position, length, matmul path, numerics) this cache has run before -- a shape is captured on
+ * its second use, up to 8 shapes per cache. For tools that cannot follow graph launches. No
+ * counterpart in the reference, which re-encodes every step (src/gpu/model.js:261). Default 1. */
 int qh_decode_use_graph(qh_cache* c, int32_t use_graph);
 
 /* Kernel roles of one decode step, the grouping of the reference's in-situ profile

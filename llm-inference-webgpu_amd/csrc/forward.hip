@@ -28,6 +28,41 @@ namespace qh {
 // (bias included) -- with q and k heads rotated as the decode step's QKV epilogue does
 // (rope_pair over f64 angles), q to `q`, k and v to the f16 caches.
 // grid (ceil(items / 256), seq).
+// Columns col[0..N) of a row summed over `splits` partial rows (`plane` floats apart) in split
+// order, + bias. Every load is issued before any is used -- the splits four at a time from
+// clamped indices, the bias (or the row itself where there is none) up front -- since a load
+// inside a loop of run-time count, or behind a branch, makes the compiler wait for each in turn.
+template <int N>
+__device__ __forceinline__ void split_sum_cols(const float* row, size_t plane, int splits, const float* bias,
+                                               const int (&col)[N], float (&v)[N]) {
+  const float* bsrc = bias ? bias : row;
+  float b[N];
+#pragma unroll
+  for (int k = 0; k < N; k++) {
+    b[k] = bsrc[col[k]];
+    v[k] = 0.f;
+  }
+  for (int sp0 = 0; sp0 < splits; sp0 += 4) {
+    float x[4][N];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const float* src = row + (size_t)min(sp0 + u, splits - 1) * plane;
+#pragma unroll
+      for (int k = 0; k < N; k++) x[u][k] = src[col[k]];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (sp0 + u < splits) {
+#pragma unroll
+        for (int k = 0; k < N; k++) v[k] += x[u][k];
+      }
+  }
+  if (bias) {
+#pragma unroll
+    for (int k = 0; k < N; k++) v[k] += b[k];
+  }
+}
+
 __global__ void k_rope_kv(const float* __restrict__ qkv, int splits, const float* __restrict__ bias,
                           float* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vt,
                           const double* __restrict__ rope_cos, const double* __restrict__ rope_sin, int past,
@@ -38,18 +73,15 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, int splits, const float
   const int width = hidden + 2 * kvd;
   const size_t plane = (size_t)gridDim.y * width;
   const float* row = qkv + (size_t)t * width;
-  auto at = [&](int c) {
-    float v = 0.f;
-    for (int sp = 0; sp < splits; sp++) v += row[sp * plane + c];
-    return bias ? v + bias[c] : v;
-  };
   const int rope_pairs = (heads + kv_heads) * 32;
   if (i < rope_pairs) {
     const int head = i / 32, j = i % 32;
     const int base = head < heads ? head * kHeadDim : hidden + (head - heads) * kHeadDim;
-    float lo, hi;
-    rope_pair(at(base + j), at(base + j + 32), rope_cos[(size_t)pos * 32 + j], rope_sin[(size_t)pos * 32 + j],
-              &lo, &hi);
+    const double cs = rope_cos[(size_t)pos * 32 + j], sn = rope_sin[(size_t)pos * 32 + j];
+    const int col[2] = {base + j, base + j + 32};
+    float x[2], lo, hi;
+    split_sum_cols<2>(row, plane, splits, bias, col, x);
+    rope_pair(x[0], x[1], cs, sn, &lo, &hi);
     if (head < heads) {
       q[(size_t)t * hidden + head * kHeadDim + j] = lo;
       q[(size_t)t * hidden + head * kHeadDim + j + 32] = hi;
@@ -60,7 +92,10 @@ __global__ void k_rope_kv(const float* __restrict__ qkv, int splits, const float
     }
   } else if (i < rope_pairs + kvd) {
     const int e = i - rope_pairs;  // kv head e/64, dimension e%64
-    vt[(size_t)e * vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)at(hidden + kvd + e));
+    const int col[1] = {hidden + kvd + e};
+    float x[1];
+    split_sum_cols<1>(row, plane, splits, bias, col, x);
+    vt[(size_t)e * vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)x[0]);
   }
 }
 

@@ -105,6 +105,18 @@ struct qh_model {
   }
 };
 
+// One batched-prefill chunk's launches (embedding gather, every layer) captured as a graph,
+// keyed by what the launches bake in: the first position, the chunk length, the matmul path
+// and numerics, and whether the rows are gathered from token ids.
+struct PrefillGraph {
+  int past, n, matmul, numerics, tokens;
+  int uses;            // times the shape was run; it is captured on its second use
+  uint64_t last;       // least-recently-used stamp
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+};
+constexpr int kPrefillGraphs = 8;  // shapes kept per cache
+
 struct qh_cache {
   qh_model* m = nullptr;
   qh::CacheDev dev{};
@@ -120,6 +132,9 @@ struct qh_cache {
   float* d_hidden = nullptr;
   size_t hidden_cap = 0;
   int32_t* h_pinned = nullptr;  // [0..1] state staging, [2] argmax readback
+  // Prefill chunks seen, and graphs of those run twice (all valid while pw_mem is).
+  std::vector<PrefillGraph> pgraphs;
+  uint64_t pclock = 0;
   // Batched-prefill workspace (allocated at the first batched forward).
   qh::PrefillDev pw{};
   qh::PrefillBytes pw_bytes{};
@@ -131,6 +146,15 @@ struct qh_cache {
     return QH_OK;
   }
 };
+
+// Destroys the cache's prefill graphs (the caller has synchronized the stream).
+static void drop_prefill_graphs(qh_cache* c) {
+  for (PrefillGraph& g : c->pgraphs) {
+    if (g.exec) hipGraphExecDestroy(g.exec);
+    if (g.graph) hipGraphDestroy(g.graph);
+  }
+  c->pgraphs.clear();
+}
 
 static void free_staged(Staged& s) {
   hipFree(s.data);
@@ -617,6 +641,7 @@ int qh_cache_free(qh_cache* c) {
   if (c->graph) hipGraphDestroy(c->graph);
   if (c->exec_run) hipGraphExecDestroy(c->exec_run);
   if (c->graph_run) hipGraphDestroy(c->graph_run);
+  drop_prefill_graphs(c);
   for (void* p : c->allocs) hipFree(p);
   hipFree(c->d_hidden);
   if (c->pw_mem) hipFree(c->pw_mem);
@@ -709,6 +734,7 @@ int ensure_prefill(qh_cache* c) {
     return QH_OK;
   hipStream_t s = m->ctx->stream;
   QH_HIP(hipStreamSynchronize(s));
+  drop_prefill_graphs(c);  // they address the workspace being replaced
   if (c->pw_mem) hipFree(c->pw_mem);
   c->pw_mem = nullptr;
   const size_t fbytes = (b.floats * 4 + 255) & ~(size_t)255, cbytes = (b.counters * 4 + 255) & ~(size_t)255;
@@ -739,6 +765,66 @@ int ensure_prefill(qh_cache* c) {
   return QH_OK;
 }
 
+// One chunk's launches (the gather from token ids, unless the rows came from the host, and
+// every layer). A shape run before is replayed from its graph (captured on its second use,
+// so a one-off length pays no capture), which removes the host's per-launch cost and the
+// device's gaps between the ~250 launches; the least recently used of kPrefillGraphs shapes
+// makes room for a new one. use_graph = 0 (qh_decode_use_graph) enqueues directly.
+static int prefill_chunk(qh_cache* c, bool tokens, int past, int n) {
+  qh_model* m = c->m;
+  hipStream_t s = m->ctx->stream;
+  const qh::ModelDev& d = m->dev;
+  auto enqueue = [&]() -> hipError_t {
+    if (tokens) {
+      const hipError_t e = qh::enqueue_embed_rows(s, d, c->dev, c->pw, past, n);
+      if (e != hipSuccess) return e;
+    }
+    return qh::enqueue_prefill_layers(s, d, c->dev, c->pw, m->matmul, past, n);
+  };
+  if (!c->use_graph) {
+    QH_HIP(enqueue());
+    return QH_OK;
+  }
+  PrefillGraph* g = nullptr;
+  for (PrefillGraph& e : c->pgraphs)
+    if (e.past == past && e.n == n && e.matmul == m->matmul && e.numerics == d.numerics && e.tokens == tokens) g = &e;
+  if (!g) {
+    if ((int)c->pgraphs.size() >= kPrefillGraphs) {
+      auto lru = std::min_element(c->pgraphs.begin(), c->pgraphs.end(),
+                                  [](const PrefillGraph& a, const PrefillGraph& b) { return a.last < b.last; });
+      QH_HIP(hipStreamSynchronize(s));
+      if (lru->exec) hipGraphExecDestroy(lru->exec);
+      if (lru->graph) hipGraphDestroy(lru->graph);
+      c->pgraphs.erase(lru);
+    }
+    c->pgraphs.push_back(PrefillGraph{past, n, m->matmul, d.numerics, tokens, 0, 0, nullptr, nullptr});
+    g = &c->pgraphs.back();
+  }
+  g->last = ++c->pclock;
+  if (!g->exec && ++g->uses >= 2) {
+    QH_HIP(hipStreamSynchronize(s));
+    QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
+    const hipError_t e = enqueue();
+    hipGraph_t graph = nullptr;
+    const hipError_t e2 = hipStreamEndCapture(s, &graph);
+    if (e != hipSuccess || e2 != hipSuccess) {
+      if (graph) hipGraphDestroy(graph);
+      QH_HIP(e != hipSuccess ? e : e2);
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e3 = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (e3 != hipSuccess) {
+      hipGraphDestroy(graph);
+      QH_HIP(e3);
+    }
+    g->graph = graph;
+    g->exec = exec;
+  }
+  if (g->exec) QH_HIP(hipGraphLaunch(g->exec, s));
+  else QH_HIP(enqueue());
+  return QH_OK;
+}
+
 // forward() over seq > 1 positions, batched: the input rows (host `h_hidden`, else the
 // cache's tokens) pass through the layers in chunks, then the last row through the head.
 int batched_forward(qh_cache* c, const float* h_hidden, int seq, bool want, int forced) {
@@ -755,10 +841,8 @@ int batched_forward(qh_cache* c, const float* h_hidden, int seq, bool want, int 
     if (h_hidden) {
       QH_HIP(hipMemcpyAsync(c->pw.X, h_hidden + (size_t)done * d.hidden, (size_t)n * d.hidden * 4,
                             hipMemcpyHostToDevice, s));
-    } else {
-      QH_HIP(qh::enqueue_embed_rows(s, d, c->dev, c->pw, past, n));
     }
-    QH_HIP(qh::enqueue_prefill_layers(s, d, c->dev, c->pw, m->matmul, past, n));
+    if ((rc = prefill_chunk(c, h_hidden == nullptr, past, n))) return rc;
   }
   QH_HIP(hipMemcpyAsync(c->dev.x, c->pw.X + (size_t)(n - 1) * d.hidden, (size_t)d.hidden * 4,
                         hipMemcpyDeviceToDevice, s));

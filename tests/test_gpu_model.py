@@ -364,3 +364,36 @@ def test_mfma_prefill_shorter_than_its_workspace(ctx, hip, full_ckpt, capacity, 
     assert err <= LOGIT_REL
     assert res["mfma"]["argmax"] == res["batched"]["argmax"] == O.argmax(ref)
     model.destroy()
+
+
+@pytest.mark.parametrize("path", ["batched", "mfma"])
+def test_prefill_graph_replays_equal_direct_launches(ctx, hip, path):
+    """A prompt shape run again is replayed from a graph captured on its second use: every run
+    (direct, capturing, replayed) stores the same K/V and returns the same logits, bit for bit,
+    as a cache that launches every kernel directly, with other work on the stream and host
+    synchronizations between the replays."""
+    cfg = tiny(hip)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=21)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "int8", 128, "int8"), cfg, maxPositions=128)
+    model.set_matmul(path)
+    prompt = hip.synth_tokens(21, "graph.prompt", cfg.vocab, 40)
+    direct = model.newCache(64)
+    model.decode_use_graph(direct, False)
+    ref = model.forward_tokens(prompt, direct)
+    other = model.newCache(64)
+    replayed = model.newCache(64)
+    for run in range(4):
+        replayed.length = 0
+        out = model.forward_tokens(prompt, replayed)
+        np.testing.assert_array_equal(out["logits"].view(np.uint32), ref["logits"].view(np.uint32))
+        assert out["argmax"] == ref["argmax"]
+        for L in (0, cfg.layers - 1):
+            a, b = replayed.present(L), direct.present(L)
+            np.testing.assert_array_equal(a["key"].view(np.uint32), b["key"].view(np.uint32))
+            np.testing.assert_array_equal(a["value"].view(np.uint32), b["value"].view(np.uint32))
+        other.length = 0
+        model.forward_tokens(prompt[: 7 + run], other)   # eager work between the replays
+        ctx.done()
+    for c in (direct, other, replayed):
+        c.destroy()
+    model.destroy()
