@@ -32,6 +32,9 @@ Also reported on the same JSON line:
   path_comparison  the same-session comparison of the matmul paths (web/scaling.html): the
                  paths checked to compute the same model, then prompt time-to-logits at 1 ..
                  512 tokens and single-token steps, median/min/max per path
+  perplexity     the reference's perplexity protocol on a seeded 48-token passage (no tokenizer
+                 or checkpoint here): f16 / int8 / int4-g128 / int4-g32 scored one token at a time
+                 on the decode kernels, paired NLL change vs f16 +- SE, and |dNLL| vs the oracle
   greedy_match   every timed token against the CPU oracle continuing from the GPU's cache
                  (teacher-forced), the smallest top-2 margin, and per layer the max-abs
                  relative error and cosine of the K/V rows the decoded positions stored
@@ -281,6 +284,55 @@ def prefill_bench(ctx, cfg, ckpt, seed, prompt_len=512, modes=("matvec", "batche
         res["mfma_linear_tflops_lower_bound"] = round(lin / (res["mfma"]["ttft_ms"] * 1e-3) / 1e12, 1)
     model.destroy()
     return res
+
+
+def perplexity_bench(ctx, cfg, ckpt, seed, n=48, oracle_check=True):
+    """The reference's perplexity protocol (web/perplexity.html:125-215, validate/perplexity.js)
+    on a seeded n-token passage of this synthetic model -- no tokenizer or checkpoint is here:
+    every scheme scores the same n - 1 positions one token at a time through the cache
+    (qh_score: the decode kernels reading the int8/int4 codes), perplexity = exp(mean NLL), and
+    the paired per-position NLL change against f16 with its standard error (the reference's
+    "not distinguishable" test at 2 SE). Layers and head use the scheme, as the reference's
+    round trip covers the tied embedding; input rows are the bf16 rows. With the oracle check,
+    the C oracle scores the same positions on the same quantized weights: the largest |dNLL|
+    is the device arithmetic's own effect."""
+    ids = H.synth_tokens(seed, "perplexity.passage", cfg.vocab, n)
+    if oracle_check:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        import oracle_lib as O
+        O.lib().or_set_threads(host_cpu()[1])
+    schemes = [("f16", "f16", 128, 16.0), ("int8", "int8", 128, 8 + 32 / cfg.hidden),
+               ("int4-g128", "int4", 128, 4 + 64 / 128), ("int4-g32", "int4", 32, 4 + 64 / 32)]
+    rows, base = {}, None
+    for label, scheme, group, bits in schemes:
+        model = H.GpuModel.load_checkpoint(ctx, ckpt, cfg, scheme, group, scheme, maxPositions=n + 8)
+        cache = model.newCache(n + 2)
+        t0 = time.perf_counter()
+        nll = model.score(ids, cache)
+        dt = time.perf_counter() - t0
+        cache.destroy()
+        model.destroy()
+        row = {"bits_per_weight": round(bits, 3), "perplexity": round(float(np.exp(nll.mean())), 4),
+               "mean_nll": round(float(nll.mean()), 6), "scored": int(nll.size), "seconds": round(dt, 3)}
+        if base is None:
+            base = nll
+        else:
+            d = nll - base
+            se = float(np.std(d, ddof=1) / np.sqrt(d.size))
+            row["paired_mean_nll_delta_vs_f16"] = round(float(d.mean()), 6)
+            row["paired_standard_error"] = round(se, 6)
+            row["distinguishable_at_2se"] = bool(abs(d.mean()) >= 2 * se)
+        if oracle_check:
+            oracle = O.OracleModel(cfg, ckpt, scheme=scheme, group=group, lm_head=scheme, kv_f16=True)
+            oc = oracle.new_cache(n + 2)
+            ref = np.array([O.nll(oracle.forward([ids[t]], oc), ids[t + 1]) for t in range(n - 1)])
+            row["oracle_perplexity"] = round(float(np.exp(ref.mean())), 4)
+            row["max_abs_nll_vs_oracle"] = float(f"{np.max(np.abs(nll - ref)):.3g}")
+        rows[label] = row
+        log(f"perplexity {label}: {row['perplexity']} over {row['scored']} positions"
+            + (f", |dNLL| vs oracle <= {row['max_abs_nll_vs_oracle']}" if oracle_check else ""))
+    return {"protocol": f"seeded {n}-token passage, full left context, one token at a time, nothing scored twice, "
+                        f"{n - 1} positions", "schemes": rows}
 
 
 def host_cpu():
@@ -608,6 +660,8 @@ def main():
                     help="only the same-session comparison of the matmul paths over prompt lengths")
     ap.add_argument("--loader-only", action="store_true",
                     help="only the loader's conversion kernels and the two whole-model loads")
+    ap.add_argument("--perplexity-only", action="store_true",
+                    help="only the perplexity protocol over the four weight schemes")
     ap.add_argument("--cold-only", action="store_true",
                     help="only the decode step's launches timed cold over >= 512 MiB of operand "
                          "copies after the prompt, for the rocprofv3 counter passes over them")
@@ -642,6 +696,11 @@ def main():
         return
     if args.scaling:
         print(json.dumps({"scaling": scaling_bench(ctx, cfg, ckpt)}), flush=True)
+        ctx.close()
+        return
+    if args.perplexity_only:
+        print(json.dumps({"perplexity": perplexity_bench(ctx, cfg, ckpt, args.seed, oracle_check=not args.no_cpu)}),
+              flush=True)
         ctx.close()
         return
     extra = max(args.steps, args.warmup, args.profile_steps, args.cpu_steps) + 1
@@ -727,7 +786,7 @@ def main():
     for v in cold.values():
         v["frac_of_read_ceiling"] = round(v["GBps"] / bounds["read_ceiling_GBps"], 4)
 
-    iso = attn = prefill = loader = paths = None
+    iso = attn = prefill = loader = paths = ppl = None
     if args.isolated == "all":
         d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
         iso = isolated_matvec(ctx, [("q_o", d, d), ("k_v", kv, d), ("gate_up", ffn, d),
@@ -737,6 +796,7 @@ def main():
         loader = loader_bench(ctx, cfg, ckpt)
         paths = scaling_bench(ctx, cfg, ckpt, lengths=(1, 8, 64, 256, 512), repeats=3, decode_steps=12,
                               oracle_check=not args.no_cpu)
+        ppl = perplexity_bench(ctx, cfg, ckpt, args.seed, oracle_check=not args.no_cpu)
 
     cpu = match = cpu_c = match_c = greedy = None
     if not args.no_cpu:
@@ -777,6 +837,7 @@ def main():
         "prefill_512": prefill,
         "loader": loader,
         "path_comparison": paths,
+        "perplexity": ppl,
         "prefill_s": round(prefill_s, 3),
     }
     print(json.dumps(line), flush=True)

@@ -335,6 +335,14 @@ int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens
  * resident. Optional: qh_decode_launch captures whatever is missing. No counterpart in the
  * reference, which records every step anew (src/gpu/model.js:261). */
 int qh_decode_prepare(qh_model* m, qh_cache* c);
+/* Scores a token sequence the way the reference's perplexity page does
+ * (web/perplexity.html:146-170): ids[0..n-2] are fed one position at a time through the cache
+ * (each step's input forced, as forward() of one token), and h_nll[t] (n - 1 doubles) receives
+ * the negative log-likelihood of ids[t+1] under step t's logits, -(l[target] - max - log(sum
+ * exp(l - max))) in f64 on the device. Perplexity is exp(mean(h_nll)). The cache advances by
+ * n - 1 positions; QH_ERR_RANGE for ids outside the vocabulary or a cache without room. */
+int qh_score(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t n, double* h_nll);
+
 /* use_graph = 0: later decodes on this cache enqueue every kernel of a step directly instead
  * of replaying the captured graph (same kernels, same tokens), and batched forwards enqueue
  * every layer's kernels directly instead of replaying the graph of a prompt shape (first

@@ -926,6 +926,43 @@ int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t se
   return finish_forward(c, seq, h_logits, h_argmax);
 }
 
+int qh_score(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t n, double* h_nll) {
+  QH_CHECK(m && c && h_ids && h_nll && c->m == m, QH_ERR_INVALID, "score needs a model, its cache, ids and an output");
+  QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
+  QH_CHECK(n >= 2, QH_ERR_INVALID, "score needs at least two tokens (the first is context only)");
+  for (int t = 0; t < n; t++) {
+    QH_CHECK(h_ids[t] >= 0 && h_ids[t] < m->dev.vocab, QH_ERR_RANGE,
+             "token %d at position %d is outside the vocabulary", h_ids[t], t);
+  }
+  int rc = check_room(c, n - 1);
+  if (rc) return rc;
+  BusyGuard guard(c);
+  QH_HIP(hipSetDevice(m->ctx->device));
+  hipStream_t s = m->ctx->stream;
+  struct Scratch {
+    int32_t* ids = nullptr;
+    double* nll = nullptr;
+    ~Scratch() {
+      hipFree(ids);
+      hipFree(nll);
+    }
+  } d;
+  QH_HIP(hipMalloc((void**)&d.ids, (size_t)n * 4));
+  QH_HIP(hipMalloc((void**)&d.nll, (size_t)(n - 1) * 8));
+  QH_HIP(hipMemcpyAsync(d.ids, h_ids, (size_t)n * 4, hipMemcpyHostToDevice, s));
+  // ids[0..n-2] are fed (teacher-forced); ids[t+1] is scored under step t's logits.
+  QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, d.ids, (size_t)(n - 1) * 4, hipMemcpyDeviceToDevice, s));
+  if ((rc = set_state(c, c->length, c->length + n - 1))) return rc;
+  for (int t = 0; t < n - 1; t++) {
+    QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_GATHER, true));
+    QH_HIP(qh::launch_nll(s, c->dev.logits, m->dev.vocab, d.ids + t + 1, d.nll + t));
+  }
+  QH_HIP(hipMemcpyAsync(h_nll, d.nll, (size_t)(n - 1) * 8, hipMemcpyDeviceToHost, s));
+  QH_HIP(hipStreamSynchronize(s));
+  c->length += n - 1;
+  return QH_OK;
+}
+
 constexpr int kGraphRun = 8;  // decode steps per replayed run graph
 
 // Captures the cache's decode graphs that are not captured yet: one carried step, and

@@ -676,6 +676,52 @@ hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, voi
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------ perplexity --
+// The negative log-likelihood of *target under one position's logits, as the reference's
+// perplexity page computes it (web/perplexity.html:158-166): the largest logit (a NaN is
+// skipped, as `>` skips it), the f64 sum of exp(l - max) over the vocabulary, then
+// -(l[target] - max - log(sum)). One block of 1024 threads; per-thread strided f64 sums
+// combined in a fixed tree, so every run gives the same bits.
+constexpr int kNllThreads = 1024;
+__global__ __launch_bounds__(kNllThreads) void k_nll(const float* __restrict__ logits, int vocab,
+                                                     const int32_t* __restrict__ target, double* __restrict__ out) {
+  __shared__ float wmax[kNllThreads / kWave];
+  __shared__ double wsum[kNllThreads / kWave];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  float mx = -INFINITY;
+  for (int i = tid; i < vocab; i += kNllThreads) {
+    const float l = logits[i];
+    if (l > mx) mx = l;
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off);
+    if (o > mx) mx = o;
+  }
+  if (lane == 0) wmax[wave] = mx;
+  __syncthreads();
+  mx = wmax[0];
+#pragma unroll
+  for (int w = 1; w < kNllThreads / kWave; w++)
+    if (wmax[w] > mx) mx = wmax[w];
+  const double m = (double)mx;
+  double sum = 0.0;
+  for (int i = tid; i < vocab; i += kNllThreads) sum += exp((double)logits[i] - m);
+  for (int off = kWave / 2; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if (lane == 0) wsum[wave] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < kNllThreads / kWave; w++) total += wsum[w];
+    *out = -((double)logits[*target] - m - log(total));
+  }
+}
+
+hipError_t launch_nll(hipStream_t s, const float* logits, int vocab, const int32_t* target, double* out) {
+  hipLaunchKernelGGL(k_nll, dim3(1), dim3(kNllThreads), 0, s, logits, vocab, target, out);
+  return hipGetLastError();
+}
+
 }  // namespace qh
 
 namespace qh {

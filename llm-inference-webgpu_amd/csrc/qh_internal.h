@@ -186,4 +186,6 @@ hipError_t launch_convert(hipStream_t s, bool bf16, const void* src, int rows, i
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int* counter, void* partials,
                          int32_t* d_out);
 size_t argmax_partials_bytes(int n);
+// out[0] = -log softmax(logits[0..vocab))[*target] in f64 (the reference perplexity's expression).
+hipError_t launch_nll(hipStream_t s, const float* logits, int vocab, const int32_t* target, double* out);
 }  // namespace qh

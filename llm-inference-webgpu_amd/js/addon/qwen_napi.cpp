@@ -460,6 +460,31 @@ napi_value Forward(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// (model, cache, Int32Array ids) -> Float64Array of ids.length - 1 negative log-likelihoods
+// (qh_score: ids[t + 1] under the step that feeds ids[t], web/perplexity.html:146-170).
+napi_value Score(napi_env env, napi_callback_info info) {
+  Args a;
+  qh_model* m;
+  qh_cache* c;
+  if (!get_args(env, info, a, 3) || !to_handle(env, a.v[0], &m) || !to_handle(env, a.v[1], &c)) return nullptr;
+  bool is_ta = false;
+  napi_is_typedarray(env, a.v[2], &is_ta);
+  size_t n = 0;
+  if (is_ta) {
+    napi_typedarray_type type;
+    void* data;
+    napi_value ab;
+    size_t off;
+    napi_get_typedarray_info(env, a.v[2], &type, &n, &data, &ab, &off);
+  }
+  void* ids = nullptr;
+  if (!to_array(env, a.v[2], napi_int32_array, "token ids", n, false, &ids)) return nullptr;
+  void* out_data = nullptr;
+  napi_value out = typed(env, napi_float64_array, n > 1 ? n - 1 : 0, 8, &out_data);
+  QH_CALL(qh_score(m, c, static_cast<const int32_t*>(ids), (int32_t)n, static_cast<double*>(out_data)));
+  return out;
+}
+
 napi_value Decode(napi_env env, napi_callback_info info) {  // (model, cache, firstToken, steps) -> Int32Array
   Args a;
   qh_model* m;
@@ -517,7 +542,8 @@ static napi_value Init(napi_env env, napi_value exports) {
              {"modelFree", ModelFree},     {"cacheCreate", CacheCreate},
              {"cacheFree", CacheFree},     {"cacheLength", CacheLength},
              {"cachePresent", CachePresent},
-             {"forward", Forward},         {"decode", Decode}};
+             {"forward", Forward},         {"decode", Decode},
+             {"score", Score}};
   for (const auto& f : fns) {
     napi_value v;
     napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.fn, nullptr, &v);

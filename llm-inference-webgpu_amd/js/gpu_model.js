@@ -286,6 +286,14 @@ class GpuModel {
   // Greedy decode of `steps` tokens, every step on the device (hipGraph replay).
   decode(cache, firstToken, steps) { return addon.decode(this.handle, cache.handle, firstToken, steps); }
 
+  // The negative log-likelihood of ids[t + 1] given ids[0..t], for every t, scored one token at
+  // a time through `cache` as web/perplexity.html:146-170 does (the log-softmax on the device, in
+  // f64): a Float64Array of ids.length - 1; perplexity is exp of its mean.
+  score(ids, cache) {
+    const a = ids instanceof Int32Array ? ids : Int32Array.from(ids);
+    return addon.score(this.handle, cache.handle, a);
+  }
+
   setMatmul(mode) { addon.modelSetMode(this.handle, 'matmul', matmulMode(mode)); }
 
   destroy() {

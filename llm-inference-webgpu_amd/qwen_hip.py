@@ -263,6 +263,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_model_set_tensor": [vp, ctypes.c_char_p, i32, i32, i32, i32, vp, vp, vp],
         "qh_model_load_tensor": [vp, ctypes.c_char_p, i32, i32, i32, vp, i32, i32],
         "qh_model_finalize": [vp], "qh_model_free": [vp], "qh_model_bytes": [vp, vp],
+        "qh_score": [vp, vp, vp, i32, vp],
         "qh_model_config": [vp, vp],
         "qh_decode_kernel_time_cold": [vp, vp, i32, sz, i32, vp, vp],
         "qh_probe_launch_floor": [vp, i32, i32, i32, vp], "qh_read_ceiling": [vp, sz, i32, vp],
@@ -888,6 +889,14 @@ class GpuModel:
         tok = ctypes.c_int32(-1)
         _check(self.lib.qh_decode_role(self.handle, cache.handle, ROLES.index(role), layer, ctypes.byref(tok)))
         return tok.value if role == "head" else None
+
+    def score(self, ids, cache: GpuKVCache) -> np.ndarray:
+        """Negative log-likelihood of ids[1:] given their left context (qh_score: one position at
+        a time through `cache`, web/perplexity.html:146-170); perplexity = exp(mean)."""
+        a = np.ascontiguousarray(np.asarray(ids, dtype=np.int32))
+        out = np.empty(max(len(a) - 1, 0), np.float64)
+        _check(self.lib.qh_score(self.handle, cache.handle, _ptr(a), len(a), _ptr(out)))
+        return out
 
     def kernel_time(self, cache: GpuKVCache, role: str, reps: int = 240) -> float:
         """Microseconds per back-to-back launch of one decode role's kernel (see the C ABI)."""

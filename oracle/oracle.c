@@ -530,6 +530,16 @@ int32_t or_argmax(const float* v, int n) {       /* model.js:181-182 */
   return best;
 }
 
+/* web/perplexity.html:158-166: -log softmax(logits)[target] with the max shift, in doubles,
+ * the exps summed in index order. */
+double or_nll(const float* logits, int n, int target) {
+  double max = -INFINITY;
+  for (int i = 0; i < n; i++) if (logits[i] > max) max = logits[i];
+  double sum_exp = 0;
+  for (int i = 0; i < n; i++) sum_exp += exp((double)logits[i] - max);
+  return -((double)logits[target] - max - log(sum_exp));
+}
+
 /* model.js:55-166 with the embedded input supplied by the caller. */
 int or_forward_hidden(const or_model* m, or_cache* cache, const float* hidden, int seq,
                       float* logits) {

@@ -125,6 +125,9 @@ int or_forward_hidden(const or_model* m, or_cache* cache, const float* hidden, i
                       float* logits);
 /* Strict-'>' argmax, lowest index on ties (model.js:181-182, web/bench.html:129-131). */
 int32_t or_argmax(const float* v, int n);
+/* Negative log-likelihood of `target` under logits[0..n), as the reference's perplexity page
+ * computes it (web/perplexity.html:158-166). */
+double or_nll(const float* logits, int n, int target);
 /* ReferenceModel.generate (model.js:174-187) with greedy tokens written to `tokens` [max_tokens]. */
 int or_generate(const or_model* m, or_cache* cache, const int32_t* prompt, int prompt_len,
                 int max_tokens, int32_t* tokens);

@@ -29,15 +29,19 @@ async function main() {
     hidden.set(qh.bf16ToF32Array(emb.data.subarray(prompt[t] * cfg.hidden, (prompt[t] + 1) * cfg.hidden)), t * cfg.hidden);
   }
   const viaHidden = await model.forward(hidden, prompt.length, { cache: c2 });
+  const c3 = model.newCache(64);
+  const nll = model.score(prompt, c3);   // web/perplexity.html's per-token NLLs
   let rangeError = null;
   try { model.forwardTokens([cfg.vocab], c2); } catch (e) { rangeError = e instanceof RangeError ? e.message : 'other'; }
   process.stdout.write(JSON.stringify({
     argmax: out.argmax, tokens: Array.from(gen), logits: Buffer.from(out.logits.buffer).toString('base64'),
     hiddenArgmax: viaHidden.argmax, hiddenLogits: Buffer.from(viaHidden.logits.buffer).toString('base64'),
     cacheLength: cache.length, rangeError: rangeError, bytes: model.byteLength,
+    score: Buffer.from(nll.buffer).toString('base64'), scoredLength: c3.length,
   }) + '\n');
   cache.destroy();
   c2.destroy();
+  c3.destroy();
   model.destroy();
   ctx.destroy();
 }

@@ -63,6 +63,7 @@ def lib() -> ctypes.CDLL:
         "or_forward": ([vp, vp, vp, i32, vp], i32),
         "or_forward_hidden": ([vp, vp, vp, i32, vp], i32),
         "or_argmax": ([vp, i32], ctypes.c_int32),
+        "or_nll": ([vp, i32, i32], ctypes.c_double),
         "or_generate": ([vp, vp, vp, i32, i32, vp], i32),
         "or_set_threads": ([i32], None),
     }
@@ -239,6 +240,12 @@ def kv_head_for(h, nh, nkv):
 
 def argmax(v):
     return int(lib().or_argmax(P(c32(v)), np.asarray(v).size))
+
+
+def nll(logits, target):
+    """-log softmax(logits)[target] (web/perplexity.html:158-166), the oracle's f64 expression."""
+    v = c32(logits)
+    return float(lib().or_nll(P(v), v.size, int(target)))
 
 
 # -------------------------------------------------------------------- model --

@@ -35,7 +35,7 @@ def test_addon_exports_the_driver_surface(addon_built):
     keys = json.loads(node("const a=require('./addon/qwen_napi.node'); console.log(JSON.stringify(Object.keys(a)))"))
     assert set(keys) == {"abiVersion", "open", "close", "describe", "synthBf16", "synthTokens", "quantizeInt8",
                          "quantizeInt4", "modelCreate", "modelSetMode", "modelSetTensor", "modelLoadTensor", "modelFinalize",
-                         "modelFree", "cacheCreate", "cacheFree", "cacheLength", "cachePresent", "forward", "decode"}
+                         "modelFree", "cacheCreate", "cacheFree", "cacheLength", "cachePresent", "forward", "decode", "score"}
     assert node("console.log(require('./addon/qwen_napi.node').abiVersion())").strip() == "1"
 
 
@@ -121,6 +121,11 @@ def test_js_driver_matches_python_binding(addon_built, ctx, hip, scheme, numeric
     assert js["hiddenArgmax"] == out["argmax"]
     np.testing.assert_array_equal(np.frombuffer(base64.b64decode(js["hiddenLogits"]), np.float32), js_logits)
     assert js["cacheLength"] == 20 and js["rangeError"] is not None
+    scored = model.newCache(64)
+    np.testing.assert_array_equal(np.frombuffer(base64.b64decode(js["score"]), np.float64),
+                                  model.score(prompt, scored))
+    assert js["scoredLength"] == scored.length == 11
+    scored.destroy()
     cache.destroy()
     model.destroy()
 

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from conftest import lcg
+from conftest import lcg, lcg_fast
 
 
 def close(a, b, tol):
@@ -250,6 +250,31 @@ def test_argmax_strict_greater_semantics():
     assert O.argmax([-0.0, 0.0]) == 0            # -0 == +0
     assert O.argmax([-np.inf, -np.inf]) == 0
     assert O.argmax([1, np.inf, np.inf]) == 1
+
+
+@pytest.mark.parametrize("n", [2, 1000, 151936])
+def test_nll_matches_log_softmax(n):
+    """The oracle's perplexity term (web/perplexity.html:158-166) against scipy's log_softmax of
+    the same f32 logits in f64, at several targets including the largest and smallest logit."""
+    from scipy.special import log_softmax
+    logits = lcg_fast(n, 7) * 12
+    ref = log_softmax(logits.astype(np.float64))
+    for t in sorted({0, n - 1, int(np.argmax(logits)), int(np.argmin(logits)), n // 3}):
+        assert O.nll(logits, t) == pytest.approx(-ref[t], rel=1e-13, abs=1e-13)
+
+
+def test_nll_closed_forms():
+    # equal logits: the uniform distribution, -log(1/n) = log(n)
+    assert O.nll(np.full(151936, 3.25, np.float32), 17) == pytest.approx(np.log(151936), rel=1e-15)
+    # two logits a, b: -log softmax = log(1 + exp(b - a)) for the target a
+    a, b = np.float32(1.5), np.float32(-2.0)
+    assert O.nll([a, b], 0) == pytest.approx(np.log1p(np.exp(np.float64(b) - np.float64(a))), rel=1e-15)
+    assert O.nll([a, b], 1) == pytest.approx(np.log1p(np.exp(np.float64(a) - np.float64(b))), rel=1e-15)
+    # the max shift keeps large logits finite
+    assert np.isfinite(O.nll([1e30, 0.0, -1e30], 1))
+    assert O.nll([1e30, 0.0], 0) == 0.0
+    # a NaN logit is skipped by the max but enters the sum (as the reference's loops do)
+    assert np.isnan(O.nll([1.0, np.nan, 2.0], 2))
 
 
 @pytest.mark.parametrize("n", [1, 17, 4864])
