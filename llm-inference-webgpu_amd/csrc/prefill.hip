@@ -67,8 +67,8 @@ __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v 
 // One row kernel in front of every contraction (one block per row m, rows of n <= 8192
 // values): the row is the sum of `splits` partial rows (+ bias) -- a previous contraction's
 // split-K output, summed in the order k_gemm_finish sums it -- or, for ROW_SWIGLU,
-// silu(g) * u of such a row of interleaved gate|up pairs; optionally added into the
-// residual stream `resid` (f32, as the batched path's add); for ROW_RMSNORM normalized
+// silu(g) * u of such a row of interleaved gate|up pairs (no bias, no residual); optionally
+// added into the residual stream `resid` (f32, as the batched path's add); for ROW_RMSNORM normalized
 // as the f32 rmsnorm does; and, when `digits` is set, written as the digit planes of the
 // next contraction: s = max|y| / 127, X = rint(y * 2^16 / s) in three balanced base-256
 // digits (step-major, digit_offset), zeros past n, and the row factor s * 2^-16 (NaN for a
@@ -79,12 +79,23 @@ __device__ __forceinline__ float peak_of(float p, float v) { return (v > p || v 
 // only known at run time, makes the compiler wait for each in turn. J = float4 groups per
 // thread (rows of up to 1024 J values); the splits are read U at a time (four for the split
 // contractions' rows; the gate|up contraction is not split) and added in order.
+//
+// Rows are dealt to blocks so that the 16 rows of a digit tile run on one XCD (workgroups go to
+// the 8 XCDs round-robin by linear id): a 128-byte line of a digit plane holds 16 bytes of each
+// of 8 rows, and one L2 then merges the line's parts instead of eight L2s each writing one back.
+// Needs M to be a multiple of 128; otherwise block b handles row b.
+__device__ __forceinline__ int row_of_block(int b, int M) {
+  if (M % 128) return b;
+  const int xcd = b & 7, r = b >> 3;
+  return 16 * (xcd + 8 * (r >> 4)) + (r & 15);
+}
+
 template <int OP, int J>
 __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   __shared__ float red[kBlock / kWave];
   constexpr int W = OP == ROW_SWIGLU ? 2 : 1;  // float4 loads per group and split
   constexpr int U = OP == ROW_SWIGLU ? 1 : 4;  // splits read together
-  const int m = blockIdx.x, tid = threadIdx.x;
+  const int m = row_of_block(blockIdx.x, a.M), tid = threadIdx.x;
   const int n4 = a.n / 4;
   const int in_len = W * a.n;
   const size_t plane_in = (size_t)a.M * in_len;
@@ -101,13 +112,17 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   const float* rsrc = a.resid ? resid_row : in_row;
   const float* gsrc = OP == ROW_RMSNORM ? a.gain : in_row;
   const float* bsrc = a.bias ? a.bias : in_row;
+  // (the swiglu row has neither: launch_rows refuses one with a residual or bias)
+  constexpr bool kAdds = OP != ROW_SWIGLU;
   v4f res[J], gain[J], bias[J][W];
 #pragma unroll
   for (int j = 0; j < J; j++) {
-    res[j] = *reinterpret_cast<const v4f*>(rsrc + 4 * idx[j]);
+    if constexpr (kAdds) res[j] = *reinterpret_cast<const v4f*>(rsrc + 4 * idx[j]);
     if constexpr (OP == ROW_RMSNORM) gain[j] = *reinterpret_cast<const v4f*>(gsrc + 4 * idx[j]);
+    if constexpr (kAdds) {
 #pragma unroll
-    for (int w = 0; w < W; w++) bias[j][w] = *reinterpret_cast<const v4f*>(bsrc + 4 * (W * idx[j] + w));
+      for (int w = 0; w < W; w++) bias[j][w] = *reinterpret_cast<const v4f*>(bsrc + 4 * (W * idx[j] + w));
+    }
   }
   v4f sum[J][W];
 #pragma unroll
@@ -137,7 +152,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   v4f v[J];
 #pragma unroll
   for (int j = 0; j < J; j++) {
-    if (a.bias) {
+    if (kAdds && a.bias) {
 #pragma unroll
       for (int w = 0; w < W; w++) sum[j][w] += bias[j][w];
     }
@@ -146,7 +161,7 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
                  swiglu_f32(sum[j][1][0], sum[j][1][1]), swiglu_f32(sum[j][1][2], sum[j][1][3])};
     else
       v[j] = sum[j][0];
-    if (a.resid) {
+    if (kAdds && a.resid) {
       v[j] = res[j] + v[j];
       if (ok[j]) *reinterpret_cast<v4f*>(resid_row + 4 * idx[j]) = v[j];
     }
@@ -218,6 +233,7 @@ static hipError_t launch_rows_op(hipStream_t s, const RowArgs& a) {
 
 hipError_t launch_rows(hipStream_t s, int op, const RowArgs& a) {
   if (a.n % 4 || a.n > 8192 || a.splits < 1 || (a.digits && a.Kp != padded_k(a.n))) return hipErrorInvalidValue;
+  if (op == ROW_SWIGLU && (a.bias || a.resid)) return hipErrorInvalidValue;
   switch (op) {
     case ROW_PLAIN: return launch_rows_op<ROW_PLAIN>(s, a);
     case ROW_RMSNORM: return launch_rows_op<ROW_RMSNORM>(s, a);
