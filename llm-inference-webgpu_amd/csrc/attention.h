@@ -843,16 +843,15 @@ static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a)
   return hipGetLastError();
 }
 
-// ------------------------------------- one query, GQA group on the matrix cores --
-// The split-K slots of k_attn_slots for a single query, with a whole GQA group per
-// wave: the group's query heads are the columns of the MFMA products of the flash
-// kernel above (heads/kv_heads of the 16 used, the rest repeat head 0 and are
-// dropped), so each key/value position is read once for the group instead of once
-// per query head. A slot's chunks are walked in steps of 32 keys -- S^T for 2 tiles
-// of 16 keys (8 MFMAs), the online softmax per head column, O^T += V^T P^T (8
-// MFMAs) -- with the next step's loads issued before each step's arithmetic (two
-// 32-key buffers). Writes (m, l, o) slot partials in the layout of k_attn_slots, with
-// the maxima in base-2 units (merged by k_attn_combine<true>). q and p are split into
+// --------------------------------------- GQA group per slot on the matrix cores --
+// The split-K slots of k_attn_slots with a whole GQA group per block: the group's query
+// heads are the columns of the MFMA products of the flash kernel above (heads/kv_heads
+// of the 16 used, the rest repeat head 0 and are dropped), so each key/value position
+// is read once for the group instead of once per query head. A slot's chunks are
+// walked in steps of 32 keys -- S^T for 2 tiles of 16 keys (8 MFMAs), the online
+// softmax per head column, O^T += V^T P^T (8 MFMAs). Writes (m, l, o) slot partials in
+// the layout of k_attn_slots, with the maxima in base-2 units (merged by CombineIn in
+// the decode step, k_attn_combine<true> for the list operator). q and p are split into
 // two f16 terms as in the flash kernel (~1e-6 of the output).
 // Step i of slot sl: 32 keys starting at p0 (chunk sl + (i/2)*MAXS, half i%2).
 template <int MAXS>
@@ -860,63 +859,117 @@ __device__ __forceinline__ int gqa_p0(int sl, int i) {
   return (sl + (i >> 1) * MAXS) * kChunk + (i & 1) * 32;
 }
 
-// grid (kv_heads * MAXS, 1, list entries); SlotArgs as for k_attn_slots (one query).
-template <int MAXS>
-static __global__ __launch_bounds__(kWave) void k_attn_gqa(SlotArgs a) {
-  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+// grid (kv_heads * MAXS, queries, list entries), W waves per block; SlotArgs as for
+// k_attn_slots. Block (kv head, slot) walks the slot's steps with step i on wave i % W
+// (each wave with the next step's loads in flight), and the waves' (m, l, o) states merge
+// through LDS in wave order, as in k_flash_prefill; the merged state is the slot's
+// partial. Query t (blockIdx.y) is at position past + t, and its blocks do exactly what a
+// launch for that query alone does, so a batch of queries gets the bits of one-query
+// launches. The decode step runs W = 4 (at contexts up to 2048 each wave has at most one
+// step, so a slot costs one step's latency), the list operator W = 1 (throughput).
+template <int MAXS, int W>
+static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
+  __shared__ v4f sh_o[W][4][kWave];
+  __shared__ float sh_m[W][16], sh_l[W][16];
+  const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, n = lane & 15, g = lane >> 4;
   const int group = a.heads / a.kv_heads;
   const int kvh = blockIdx.x / MAXS, sl = blockIdx.x % MAXS;
+  const int t = blockIdx.y;
   const size_t z = blockIdx.z;
   const int h = kvh * group + (n < group ? n : 0);
   f16x8 qh[2], ql[2];
-  load_query_split(a.q + (size_t)h * kHeadDim, g, qh, ql);
+  load_query_split(a.q + ((size_t)t * a.heads + h) * kHeadDim, g, qh, ql);
   const uint16_t* kb = a.kc + z * a.list_k + (size_t)kvh * a.capacity * kHeadDim;
   const uint16_t* vb = a.vt + z * a.list_v + (size_t)kvh * kHeadDim * a.vstride;
   KvStep A, B;
-  kv_load(kb, vb, gqa_p0<MAXS>(sl, 0), a.capacity, a.vstride, n, g, A);  // in bounds whatever the position
-  const int pos = a.d_pos ? *a.d_pos : a.past;
-  if (pos >= a.capacity) return;  // the host keeps positions inside the cache
+  int i = w;
+  kv_load(kb, vb, gqa_p0<MAXS>(sl, i), a.capacity, a.vstride, n, g, A);
+  const int pos = (a.d_pos ? *a.d_pos : a.past) + t;
+  if (pos >= a.capacity) return;  // block-uniform
   const int ctx = pos + 1, nch = attn_chunks(ctx);
   float m = -INFINITY, l = 0.f;
   f32x4 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  // Steps of this slot: two per chunk, but none that starts at or past the context.
-  int left = 0;
+  int steps = 0;
   if (sl < nch) {
     const int chunks = (nch - 1 - sl) / MAXS + 1;
     const int last = sl + (chunks - 1) * MAXS;
-    left = 2 * chunks - (last * kChunk + 32 >= ctx ? 1 : 0);
+    steps = 2 * chunks - (last * kChunk + 32 >= ctx ? 1 : 0);
   }
-  int i = 0;
+  int left = i < steps ? (steps - 1 - i) / W + 1 : 0;
   while (left > 0) {
     if (left == 1) {
       kv_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
       break;
     }
-    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, B);
-    __builtin_amdgcn_sched_barrier(0);  // the next step's loads before this step's arithmetic
+    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + W), a.capacity, a.vstride, n, g, B);
+    __builtin_amdgcn_sched_barrier(0);
     kv_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
-    ++i;
+    i += W;
     if (--left == 1) {
       kv_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
       break;
     }
-    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + 1), a.capacity, a.vstride, n, g, A);
+    kv_load(kb, vb, gqa_p0<MAXS>(sl, i + W), a.capacity, a.vstride, n, g, A);
     __builtin_amdgcn_sched_barrier(0);
     kv_step(qh, ql, B, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);
-    ++i;
+    i += W;
     --left;
   }
-  if (n < group) {
-    float* dst = a.part + z * a.list_part + ((size_t)h * MAXS + sl) * kPartStride;
+  float* dst = a.part + z * a.list_part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
+  if constexpr (W == 1) {  // the merge below would scale by exactly 1
+    if (n < group) {
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++) *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = (v4f)o[dt];
-    if (g == 0) {
-      dst[0] = m;
-      dst[1] = l;
+      for (int dt = 0; dt < 4; dt++) *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = (v4f)o[dt];
+      if (g == 0) {
+        dst[0] = m;
+        dst[1] = l;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; dt++) sh_o[w][dt][lane] = (v4f)o[dt];
+  if (g == 0) {
+    sh_m[w][n] = m;
+    sh_l[w][n] = l;
+  }
+  __syncthreads();
+  float mx = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < W; v++) mx = fmaxf(mx, sh_m[v][n]);
+  for (int dt = w; dt < 4; dt += W) {
+    float lt = 0.f;
+    v4f ot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < W; v++) {
+      const float mv = sh_m[v][n];
+      const float wt = mv == -INFINITY ? 0.f : exp2_reduced(mv - mx);
+      lt = fmaf(sh_l[v][n], wt, lt);
+      const v4f ov = sh_o[v][dt][lane];
+#pragma unroll
+      for (int r = 0; r < 4; r++) ot[r] = fmaf(ov[r], wt, ot[r]);
+    }
+    if (n < group) {
+      *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = ot;
+      if (dt == 0 && g == 0) {
+        dst[0] = mx;
+        dst[1] = lt;
+      }
     }
   }
+}
+
+// The decode step's attention over `seq` queries (grid.y) and `count` list entries
+// (grid.z): k_attn_gqa with kDecodeSlots slots per head and four waves per slot, the
+// partials the decode combine (CombineIn) merges.
+constexpr int kDecodeWaves = 4;
+static inline hipError_t launch_attn_decode(hipStream_t s, SlotArgs a, int seq, int count) {
+  a.max_slots = kDecodeSlots;
+  hipLaunchKernelGGL((k_attn_gqa<kDecodeSlots, kDecodeWaves>), dim3(a.kv_heads * kDecodeSlots, seq, count),
+                     dim3(kDecodeWaves * kWave), 0, s, a);
+  return hipGetLastError();
 }
 
 // out[t][h][d] from the slot partials of (t, h): one 64-lane block per (h, t) (and list
@@ -946,10 +999,11 @@ static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __re
 
 // The decode step's combine, run by the o-projection while it stages its input:
 // xs[lay.pos(i)] = attention output i (i = h*64 + d) as f64, for a single query
-// whose slot partials (kDecodeSlots = 16 per head, empty ones neutral) are at
-// `part`. Thread i < heads*16 owns head h = i/16: it reads the (m, l) of slot
-// i%16 and the four output dimensions 4*(i%16) .. +3 of every slot; the 16 lanes
-// of a head form one DPP team, so M, L and the slot weights e^(m_s - M) / L stay
+// whose slot partials (kDecodeSlots = 16 per head, empty ones neutral, written by
+// k_attn_gqa with the maxima in base-2 units) are at `part`. Thread i < heads*16
+// owns head h = i/16: it reads the (m, l) of slot i%16 and the four output
+// dimensions 4*(i%16) .. +3 of every slot; the 16 lanes of a head form one DPP
+// team, so M, L and the slot weights 2^(m_s - M) / L stay
 // inside it (shared through the wave's own LDS slice). Nothing here depends on
 // the position. heads <= 16. Loads (CombineIn::load) and arithmetic are split as
 // for StageIn.
@@ -973,8 +1027,9 @@ struct CombineIn {
 // LDS of kBlock floats.
 __device__ __forceinline__ v4f attn_combine_quad(const CombineIn& in, float* wl) {
   const int i = threadIdx.x;
-  const float M = team_max<16>(in.mv);     // slot 0 always holds position 0
-  const float w = expf(in.mv - M);         // 0 for an empty slot (m = -inf)
+  const float M = team_max<16>(in.mv);  // slot 0 always holds position 0
+  // maxima in base-2 units (k_attn_gqa); an empty slot (m = -inf) weighs 0
+  const float w = in.mv == -INFINITY ? 0.f : exp2_reduced(in.mv - M);
   const float L = team_sum<16>(w * in.lv);
   wl[i] = w / L;
   __builtin_amdgcn_wave_barrier();

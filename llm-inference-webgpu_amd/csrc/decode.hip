@@ -297,6 +297,10 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   }
 }
 
+constexpr int kLmRows = 4;          // rows per team in the output head
+constexpr int kLmMaxBlocks = 1024;  // the head's teams take ceil(items / (teams * blocks)) items each
+constexpr int kPickLoads = 4;       // partial loads per thread of k_pick
+
 // The end of a step with logits: the best of the head's block partials is the
 // token (lowest index among equal maxima, NaN logits -> 0, the reference's
 // host-side scan of src/gpu/model.js:372-382); it is recorded, the position
@@ -308,34 +312,49 @@ __global__ __launch_bounds__(kBlock) void k_pick(const ArgPair* __restrict__ par
                                                  int* tokens, int* pred, int capacity,
                                                  const uint16_t* __restrict__ embed, int hidden,
                                                  int vocab, float* __restrict__ x) {
+  static_assert(kLmMaxBlocks <= kPickLoads * kBlock, "one round of partial loads");
   __shared__ ArgPair wred[kBlock / kWave];
-  __shared__ int next;
-  // What does not depend on the argmax is read first, alongside the partials: the
-  // position, the forced length and the caller's token at the next position.
+  // Every load that does not depend on the argmax is issued first: the partials (all
+  // of them at once, from clamped indices -- a repeated pair does not change the
+  // best), the position, the forced length and the caller's token at the next position.
+  ArgPair q[kPickLoads];
+#pragma unroll
+  for (int k = 0; k < kPickLoads; k++) q[k] = partials[min((int)threadIdx.x + k * kBlock, nparts - 1)];
   const int p = state[0], forced = state[1];
   const bool caller = p + 1 < forced && p + 1 <= capacity;  // the next input is the caller's token
-  const int given = caller ? tokens[p + 1] : 0;
+  const int given = tokens[min(p + 1, capacity)];
   const float first = logits[0];
-  float v = NAN;
-  int i = 0x7fffffff;
-  for (int b = threadIdx.x; b < nparts; b += kBlock) {
-    const ArgPair q = partials[b];
-    if (argmax_better(q.v, q.i, v, i)) {
-      v = q.v;
-      i = q.i;
+  float v = q[0].v;
+  int i = q[0].i;
+#pragma unroll
+  for (int k = 1; k < kPickLoads; k++) {
+    if (argmax_better(q[k].v, q[k].i, v, i)) {
+      v = q[k].v;
+      i = q[k].i;
     }
   }
-  argmax_block(v, i, wred);
+  // The block's best, known to every thread after one barrier (each reduces the waves' bests).
+  argmax_wave(v, i);
+  if ((threadIdx.x & (kWave - 1)) == 0) wred[threadIdx.x / kWave] = {v, i};
+  __syncthreads();
+  v = wred[0].v;
+  i = wred[0].i;
+#pragma unroll
+  for (int w = 1; w < kBlock / kWave; w++) {
+    if (argmax_better(wred[w].v, wred[w].i, v, i)) {
+      v = wred[w].v;
+      i = wred[w].i;
+    }
+  }
+  const int tok = (first != first) ? 0 : i;
   if (threadIdx.x == 0) {
-    const int tok = (first != first) ? 0 : i;
     if (p < capacity) pred[p] = tok;
     if (p + 1 >= forced && p + 1 <= capacity) tokens[p + 1] = tok;
     state[0] = p + 1;
-    const int t = caller ? given : tok;
-    next = (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
   }
-  __syncthreads();
-  const uint16_t* row = embed + (size_t)next * hidden;
+  int t = caller ? given : tok;
+  t = (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
+  const uint16_t* row = embed + (size_t)t * hidden;
   for (int k = threadIdx.x; k < hidden; k += kBlock) x[k] = __builtin_bit_cast(float, (uint32_t)row[k] << 16);
 }
 
@@ -357,8 +376,6 @@ __global__ void k_advance(int* state) {
   if (threadIdx.x == 0) state[0] = state[0] + 1;
 }
 
-constexpr int kLmRows = 4;          // rows per team in the output head
-constexpr int kLmMaxBlocks = 1024;  // the head's teams take ceil(items / (teams * blocks)) items each
 
 // Chunks per lane a kernel is built for: the smallest instantiated count that
 // covers ceil(nchunks / TL).
@@ -506,8 +523,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         a.vstride = c.vstride;
         a.heads = m.heads;
         a.kv_heads = m.kv_heads;
-        a.max_slots = kDecodeSlots;
-        return launch_attn_slots<kDecodeSlots>(s, a, 1, 1);
+        return launch_attn_decode(s, a, 1, 1);
       } else {
         ExactArgs a{};
         a.q = c.q;
@@ -595,11 +611,10 @@ hipError_t enqueue_attention_list(hipStream_t s, const ModelDev& m, const CacheD
   a.vstride = c.vstride;
   a.heads = m.heads;
   a.kv_heads = m.kv_heads;
-  a.max_slots = kDecodeSlots;
   a.list_k = copy_elems;
   a.list_v = copy_elems;
   a.list_part = (size_t)m.heads * kDecodeSlots * kPartStride;
-  return launch_attn_slots<kDecodeSlots>(s, a, 1, count);
+  return launch_attn_decode(s, a, 1, count);
 }
 
 hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer) {

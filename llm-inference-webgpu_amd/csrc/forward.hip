@@ -327,8 +327,7 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
       a.vstride = c.vstride;
       a.heads = m.heads;
       a.kv_heads = m.kv_heads;
-      a.max_slots = kDecodeSlots;
-      if ((e = launch_attn_slots<kDecodeSlots>(s, a, seq, 1)) != hipSuccess) return e;
+      if ((e = launch_attn_decode(s, a, seq, 1)) != hipSuccess) return e;
       hipLaunchKernelGGL(k_attn_merge_rows, dim3(seq), dim3(kBlock), 0, s, p.part, m.heads, p.ATT);
     } else {
       ExactArgs a{};

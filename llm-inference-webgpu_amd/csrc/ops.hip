@@ -536,7 +536,7 @@ template <int MAXS>
 static hipError_t list_t(hipStream_t s, SlotArgs a, int count, float* out) {
   a.max_slots = MAXS;
   a.list_part = (size_t)a.heads * MAXS * kPartStride;
-  hipLaunchKernelGGL(k_attn_gqa<MAXS>, dim3(a.kv_heads * MAXS, 1, count), dim3(kWave), 0, s, a);
+  hipLaunchKernelGGL((k_attn_gqa<MAXS, 1>), dim3(a.kv_heads * MAXS, 1, count), dim3(kWave), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine<true>, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
