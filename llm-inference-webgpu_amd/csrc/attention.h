@@ -625,6 +625,7 @@ struct FlashArgs {
   const uint16_t* vt;    // [kv_heads][64][vstride] f16
   float* out;            // [seq][heads*64]
   int past, seq, capacity, vstride, heads, kv_heads;
+  int first;             // blocks of the first round: the device's compute units (launch_flash_prefill)
 };
 
 // x as hi + lo, two f16 values: hi = f16(x), lo = f16(x - hi) (x - hi is exact in f32).
@@ -766,9 +767,17 @@ static __global__ __launch_bounds__(kWave * kFlashWaves) void k_flash_prefill(Fl
   __shared__ v4f sh_o[kFlashWaves][4][kWave];
   __shared__ float sh_m[kFlashWaves][kFlashQ], sh_l[kFlashWaves][kFlashQ];
   const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave, n = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y;
+  // Block order (a bijection of the (query tile, head) pairs): a causal tile's work grows with
+  // its index, and the blocks of a launch are dealt to the CUs in turn, block b and b + CUs
+  // sharing a CU. So the first `first` blocks (one per CU) take the heaviest tiles, heaviest
+  // first, and the rest the lightest, lightest first: a CU's two blocks then sum to about the
+  // same work everywhere (in tile order, block b and b + 256 were the same tile of two heads).
+  const int tiles = (a.seq + kFlashQ - 1) / kFlashQ, nb = tiles * a.heads;
+  const int first = min(nb, a.first), b = blockIdx.x;
+  const int k = b < first ? b : nb - 1 - (b - first);
+  const int h = k % a.heads;
   const int kvh = h / (a.heads / a.kv_heads);
-  const int t0 = blockIdx.x * kFlashQ;
+  const int t0 = (tiles - 1 - k / a.heads) * kFlashQ;
   const int tn = min(t0 + n, a.seq - 1);  // this lane's query; past the end, a copy of the last
   const int qpos = a.past + tn;
   const int kmax = a.past + min(t0 + kFlashQ - 1, a.seq - 1);  // the tile's last key
@@ -837,8 +846,13 @@ static __global__ __launch_bounds__(kWave * kFlashWaves) void k_flash_prefill(Fl
   }
 }
 
-static inline hipError_t launch_flash_prefill(hipStream_t s, const FlashArgs& a) {
-  hipLaunchKernelGGL(k_flash_prefill, dim3((a.seq + kFlashQ - 1) / kFlashQ, a.heads), dim3(kWave * kFlashWaves), 0,
+static inline hipError_t launch_flash_prefill(hipStream_t s, FlashArgs a) {
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  a.first = cus > 0 ? cus : 1;
+  hipLaunchKernelGGL(k_flash_prefill, dim3((a.seq + kFlashQ - 1) / kFlashQ * a.heads), dim3(kWave * kFlashWaves), 0,
                      s, a);
   return hipGetLastError();
 }
