@@ -145,12 +145,17 @@ def isolated_matvec(ctx, shapes, reps=5):
     return out
 
 
-def decode_bounds(ctx, launches_per_step):
+def decode_bounds(ctx, launches_per_step, graphs=True):
     """What bounds the batch-1 decode step on this device: the pure streaming-read ceiling
     (1 GiB), and the cost of a graph-replayed launch of 224 blocks that does nothing, reads
     nothing it depends on, or reads the vector the previous launch wrote (as each decode launch
-    reads its predecessor's output) -- times the step's launches, the step's latency floor."""
+    reads its predecessor's output) -- times the step's latency floor. graphs=False (the
+    --launch direct runs made for profilers that do not follow graph launches) leaves the
+    launch probes out."""
     ceiling = ctx.read_ceiling(1 << 30, 10)
+    if not graphs:
+        return {"read_ceiling_GBps": round(ceiling, 1), "read_ceiling_frac": round(ceiling / PEAK_HBM_GBS, 4),
+                "launch_us": None, "step_launches": launches_per_step, "step_floor_us": None}
     empty = ctx.launch_floor(0)
     static = ctx.launch_floor(2)
     dependent = ctx.launch_floor(1)
@@ -725,7 +730,8 @@ def main():
         return
 
     # The decode graphs are captured and uploaded here, outside the timed region.
-    model.decode_prepare(cache)
+    if args.launch == "graph":
+        model.decode_prepare(cache)
     if args.warmup:
         model.decode(cache, first, args.warmup)
         cache.length = args.context
@@ -782,7 +788,8 @@ def main():
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
     # What bounds the step; the cold launches against the read ceiling.
-    bounds = decode_bounds(ctx, sum(v["launches_per_token"] for v in per_kernel.values()))
+    bounds = decode_bounds(ctx, sum(v["launches_per_token"] for v in per_kernel.values()),
+                           graphs=args.launch == "graph")
     for v in cold.values():
         v["frac_of_read_ceiling"] = round(v["GBps"] / bounds["read_ceiling_GBps"], 4)
 

@@ -251,8 +251,10 @@ int qh_model_create(qh_ctx* ctx, const qh_config* cfg, qh_model** out);
 /* Arithmetic of the model's forward/decode kernels.
  *   QH_NUMERICS_FAST (default): the arithmetic of the reference's WebGPU kernels -- matvecs
  *     summed in f32 (the quantization scale factored out of each 16-byte chunk), rmsnorm and
- *     swiglu in f32, split-K online-softmax attention in f32 (one pass over the f16 cache,
- *     slots merged in the o-projection's staging). Each launch agrees with the CPU path's
+ *     swiglu in f32, split-K online-softmax attention (one pass over the f16 cache, each K/V
+ *     chunk read once per kv head for the whole GQA group, q.k and p.v on f16 MFMA with q and p
+ *     split into two f16 terms and f32 sums; slots merged in the o-projection's staging).
+ *     Each launch agrees with the CPU path's
  *     arithmetic to ~1e-6 relative; logits of a whole forward within the reference's 1e-4
  *     (an f16 cache entry that rounds the other way moves later layers slightly).
  *   QH_NUMERICS_EXACT: every kernel evaluates the CPU path's arithmetic in its order (f64

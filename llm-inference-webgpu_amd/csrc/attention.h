@@ -897,7 +897,11 @@ static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
   const uint16_t* vb = a.vt + z * a.list_v + (size_t)kvh * kHeadDim * a.vstride;
   KvStep A, B;
   int i = w;
-  kv_load(kb, vb, gqa_p0<MAXS>(sl, i), a.capacity, a.vstride, n, g, A);
+  // A step in the slot's first chunk (sl < MAXS, so below 64 MAXS positions) is loaded before
+  // the position arrives; a later one only once the position says the context reaches it
+  // (loading it blind would fetch rows past the context whenever it does not).
+  const bool early = i < 2;
+  if (early) kv_load(kb, vb, gqa_p0<MAXS>(sl, i), a.capacity, a.vstride, n, g, A);
   const int pos = (a.d_pos ? *a.d_pos : a.past) + t;
   if (pos >= a.capacity) return;  // block-uniform
   const int ctx = pos + 1, nch = attn_chunks(ctx);
@@ -912,6 +916,7 @@ static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
     steps = 2 * chunks - (last * kChunk + 32 >= ctx ? 1 : 0);
   }
   int left = i < steps ? (steps - 1 - i) / W + 1 : 0;
+  if (!early && left > 0) kv_load(kb, vb, gqa_p0<MAXS>(sl, i), a.capacity, a.vstride, n, g, A);
   while (left > 0) {
     if (left == 1) {
       kv_step(qh, ql, A, gqa_p0<MAXS>(sl, i), ctx, ctx, g, m, l, o);

@@ -293,3 +293,37 @@ def test_decode_launches_match_oracle_at_full_shape(ctx, hip, full_ckpt, numeric
     say(f"decode launches ({numerics}) worst rel vs the CPU: " + ", ".join(f"{k} {v:.2e}" for k, v in worst.items()))
     cache.destroy()
     model.destroy()
+
+
+@pytest.mark.parametrize("P", [2600, 4700])
+def test_decode_attention_launch_past_2048_at_full_shape(ctx, hip, full_ckpt, P):
+    """The fast decode attention at the full shape (14 query heads over 2 kv heads) where a
+    slot holds more 32-key steps than its block has waves (past 2048 positions each wave walks
+    two or more steps before the waves merge), then the o-projection's slot merge: against the
+    CPU path's attention and o-projection on the same q and cache rows, within 1e-5."""
+    cfg = hip.QWEN25_05B
+    d, kv = cfg.hidden, cfg.kv_dim
+    model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int4", 128, "int8", maxPositions=P + 8)
+    cache = model.newCache(P + 4)
+    model.forward_tokens(hip.synth_tokens(5, "long.prompt", cfg.vocab, P), cache)
+    rng = np.random.default_rng(11)
+    L = 5
+    p = f"model.layers.{L}."
+    cache.vector("x", (rng.standard_normal(d) * 0.7).astype(np.float32))
+    model.decode_role(cache, "qkv", L)
+    q_g, k_g, v_g = cache.vector("q"), cache.vector("key", layer=L), cache.vector("value", layer=L)
+    cache.vector("x", np.zeros(d, np.float32))
+    model.decode_role(cache, "attention", L)
+    model.decode_role(cache, "oproj", L)
+    x_g = cache.vector("x")
+    pres = cache.present(L)
+    keys = np.concatenate([pres["key"].transpose(1, 0, 2).reshape(P, kv), k_g[None]], 0)
+    vals = np.concatenate([pres["value"].transpose(1, 0, 2).reshape(P, kv), v_g[None]], 0)
+    att = O.grouped_attention(q_g, keys, vals, 1, P, cfg.heads, cfg.kv_heads, 64)
+    wo = O.round_trip(O.bf16_to_f32(full_ckpt[p + "self_attn.o_proj.weight"]), "int4", 128)
+    want = O.matvec(wo, att, d, d)
+    e = rel_err(x_g, want)
+    say(f"decode attention + o-projection at context {P + 1}: rel {e:.2e}")
+    assert e <= KERNEL_REL
+    cache.destroy()
+    model.destroy()

@@ -240,17 +240,19 @@ def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt, numerics):
     model.destroy()
 
 
-def test_fast_numerics_long_context_matches_exact(ctx, hip):
-    """Past 16 x 64 positions each split-K slot of the fast path spans several chunks
-    (slot_plan); the fast step must stay within the logit tolerance of the exact one and
-    choose the same greedy tokens."""
+@pytest.mark.parametrize("prompt_len", [1400, 3000])
+def test_fast_numerics_long_context_matches_exact(ctx, hip, prompt_len):
+    """Past 16 x 64 positions each split-K slot of the fast path spans several chunks, and past
+    2048 a slot has more 32-key steps than its block has waves (each wave then walks several);
+    the fast step must stay within the logit tolerance of the exact one and choose the same
+    greedy tokens."""
     cfg = tiny(hip)
     ckpt = hip.synthesize_checkpoint(cfg, seed=11)
     tensors = hip.device_tensors(ckpt, cfg, "int4", 128, "int8")
-    fast = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=1600, numerics="fast")
-    exact = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=1600, numerics="exact")
-    prompt = hip.synth_tokens(11, "long", cfg.vocab, 1400)
-    cf, ce = fast.newCache(1500), exact.newCache(1500)
+    fast = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=prompt_len + 200, numerics="fast")
+    exact = hip.GpuModel.load(ctx, tensors, cfg, maxPositions=prompt_len + 200, numerics="exact")
+    prompt = hip.synth_tokens(11, "long", cfg.vocab, prompt_len)
+    cf, ce = fast.newCache(prompt_len + 100), exact.newCache(prompt_len + 100)
     a = fast.forward_tokens(prompt, cf)
     b = exact.forward_tokens(prompt, ce)
     print(f"long context fast vs exact logits rel {rel_err(a['logits'], b['logits']):.2e}")
