@@ -9,7 +9,7 @@
 // dimension's values over positions are contiguous, so the lane that owns
 // output dimension d reads 8 positions in one 16-byte load).
 //
-// Two algorithms:
+// Three algorithms:
 //
 // Exact order (k_attn_block up to kPLds positions, k_attn_exact beyond), the
 // model's QH_NUMERICS_EXACT path. It evaluates groupedAttention (src/core/attention.js:
@@ -23,10 +23,17 @@
 // result matches the CPU to the bit apart from f64-order noise, so a device f16
 // cache and the CPU's same-f16 cache stay identical.
 //
-// Split-K online softmax (k_attn_slots + a combine), the decode step's path
-// (QH_NUMERICS_FAST) and qh_attention_splitk: one wave per (query, head, run of
-// 64-position chunks), partials merged afterwards. Exact to f32 rounding, not to
-// the CPU's order; checked within the kernel tolerance.
+// Split-K online softmax (k_attn_slots + a combine), qh_attention_splitk: one
+// wave per (query, head, run of 64-position chunks), partials merged afterwards.
+// Exact to f32 rounding, not to the CPU's order; checked within the kernel
+// tolerance.
+//
+// The same split-K slots with the GQA group on the matrix cores (k_attn_gqa), the
+// decode step's and batched prefill's path (QH_NUMERICS_FAST) and the list
+// operator's: one block per (query, kv head, run of chunks), the group's query
+// heads as the columns of f16 MFMA products, so each K/V chunk is read once per kv
+// head. q and p go in as two f16 terms each (~1e-6 of the output). A flash form of
+// the same products (k_flash_prefill) serves the MFMA prompt path.
 #pragma once
 
 #include "device_common.h"

@@ -6,9 +6,10 @@
 //
 // Per layer (the order of src/cpu/model.js:89-143):
 //   1. rmsnorm(x) -> q|k|v matvec + bias -> rope (f64) -> q, f16 K/V append
-//   2. attention: QH_NUMERICS_FAST, split-K slot partials (one wave per head and
-//      run of 64 positions); QH_NUMERICS_EXACT, per head in the CPU's order
-//      (f64 dots, global-max softmax, sequential PV sum)
+//   2. attention: QH_NUMERICS_FAST, split-K slot partials (a block of four waves
+//      per kv head and run of 64-position chunks, the GQA group's query heads as
+//      f16 MFMA columns); QH_NUMERICS_EXACT, per head in the CPU's order (f64
+//      dots, global-max softmax, sequential PV sum)
 //   3. [FAST: merge the attention slots while staging] o-proj matvec, residual add into x
 //   4. rmsnorm(x) -> gate|up matvec -> swiglu (f64)
 //   5. down matvec, residual add into x

@@ -92,7 +92,8 @@ size_t matvec_x64_bytes(const DMat& m, int seq);
 hipError_t launch_matvec_f32(hipStream_t s, const DMat& m, const float* x, const float* bias, float* y,
                              int seq);
 bool matvec_f32_supported(const DMat& m);
-// The batched-prefill contraction on bf16 MFMA (int8 / int4 weights): y [M, rows] = x [M, cols] . W^T
+// The batched-prefill contraction on the int8 matrix cores over exact activation digits (int8 /
+// int4 weights): y [M, rows] = x [M, cols] . W^T
 // (+ bias). `scratch` holds `scratch_bytes` bytes; a launch that needs more returns
 // hipErrorInvalidValue before any work. matmul_prefill_scratch_bytes(w, M) covers every
 // launch of up to M rows.

@@ -681,10 +681,11 @@ class GpuModel:
     def load(ctx: GpuContext, tensors: dict, config: ModelConfig, maxPositions: int = 2048,
              onProgress=None, numerics: str = "fast", matmul: str = "batched") -> "GpuModel":
         """Upload device tensors (see device_tensors) and finalize. numerics: "fast"
-        (split-K f32 attention) or "exact" (the CPU path's arithmetic, bit for bit).
-        matmul: how forward() runs several positions -- "batched" (8-position weight
-        tiles, bitwise equal to decoding them one by one), "matvec" (one decode step per
-        position) or "mfma" (bf16 matrix cores for int8/int4 weights)."""
+        (f32 sums, split-K attention on the f16 matrix cores) or "exact" (the CPU path's
+        arithmetic, bit for bit). matmul: how forward() runs several positions --
+        "batched" (8-position weight tiles, bitwise equal to decoding them one by one),
+        "matvec" (one decode step per position) or "mfma" (int8 matrix cores over exact
+        activation digits, for int8/int4 weights)."""
         def upload(lib, handle):
             total = len(tensors)
             for i, (name, (fmt, rows, cols, group, data, scales, zeros)) in enumerate(tensors.items()):
