@@ -299,7 +299,7 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
 }
 
 constexpr int kLmRows = 4;          // rows per team in the output head
-constexpr int kLmMaxBlocks = 1024;  // the head's teams take ceil(items / (teams * blocks)) items each
+constexpr int kLmMaxBlocks = 1024;  // the head's blocks (see fused_blocks)
 constexpr int kPickLoads = 4;       // partial loads per thread of k_pick
 
 // The end of a step with logits: the best of the head's block partials is the
@@ -388,13 +388,13 @@ static int kc_for(int nchunks) {
   return 0;
 }
 
+// One item per team, or for more items than max_blocks' teams (the output head) max_blocks blocks
+// whose teams take every stride-th item: floor or ceil(items / teams) each, so each CU's blocks
+// (1024 = four per CU) stream nearly the same number of rows (950 blocks of equal counts left a
+// quarter of the CUs with three blocks where the rest had four).
 static int fused_blocks(int items, int teams, int max_blocks) {
-  int blocks = (items + teams - 1) / teams;
-  if (blocks > max_blocks) {
-    const int per_team = (items + teams * max_blocks - 1) / (teams * max_blocks);
-    blocks = (items + teams * per_team - 1) / (teams * per_team);
-  }
-  return blocks;
+  const int blocks = (items + teams - 1) / teams;
+  return blocks > max_blocks ? max_blocks : blocks;
 }
 
 template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool F32>
