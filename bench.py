@@ -200,6 +200,37 @@ class _Ptr:
         self.ptr = ptr
 
 
+def stream_decode_kernels(model, cache, cfg, ctx_len, ceiling, reps=5, totals=(512, 1024, 2048)):
+    """The decode step's matrix kernels over the same >= 512 MiB of operand copies as
+    cold_decode_kernels, on a grid sized for streaming instead of for one step's latency
+    (qh_decode_kernel_time_stream): blocks_per_copy blocks per copy, so that the launch has about
+    `total` blocks; each block stages its activation once and walks many rows with the next rows'
+    loads in flight. Same kernel code and arithmetic as the step; the best total is reported."""
+    d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
+    int4 = lambda r, c: r * c // 2 + r * (c // 128) * 8
+    per_copy = {"qkv": int4(d + 2 * kv, d), "oproj": int4(d, d), "gateup": int4(2 * ffn, d),
+                "down": int4(d, ffn), "head": V * d + 4 * V}
+    out = {}
+    cache.length = ctx_len
+    for role in ("qkv", "oproj", "gateup", "down", "head"):
+        best = None
+        for total in totals:
+            copies = int(np.ceil((512 << 20) / per_copy[role]))
+            bpc = max(1, int(round(total / copies)))
+            us, copies = model.kernel_time_stream(cache, role, bpc, 512 << 20, reps)
+            gbs = copies * per_copy[role] / (us * 1e-6) / 1e9
+            if best is None or gbs > best["GBps"]:
+                best = {"blocks_per_copy": bpc, "blocks": bpc * copies, "copies": copies,
+                        "bytes_per_launch": copies * per_copy[role], "us_per_launch": round(us, 2),
+                        "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        if ceiling:
+            best["frac_of_read_ceiling"] = round(best["GBps"] / ceiling, 4)
+        out[role] = best
+        log(f"stream {role}: {best['blocks_per_copy']} blocks per copy, {best['GBps']:.0f} GB/s "
+            f"({best['frac']:.1%} of 8 TB/s)")
+    return out
+
+
 def attention_sweep(ctx, contexts=(128, 1024, 4096, 32768), heads=14, kv_heads=2, reps=5):
     """Config 3: one query (position ctx-1) against f16 K/V caches of N(0,1) values, through the
     list form of the split-K operator: one launch over a rotation of distinct caches totalling
@@ -669,7 +700,8 @@ def main():
                     help="only the perplexity protocol over the four weight schemes")
     ap.add_argument("--cold-only", action="store_true",
                     help="only the decode step's launches timed cold over >= 512 MiB of operand "
-                         "copies after the prompt, for the rocprofv3 counter passes over them")
+                         "copies after the prompt (step grids, then streaming grids), for the "
+                         "rocprofv3 counter passes over them")
     ap.add_argument("--launch", choices=["graph", "direct"], default="graph",
                     help="decode by hipGraph replay (default) or direct launches of the same "
                          "kernels (for profilers that do not follow graph launches)")
@@ -722,7 +754,8 @@ def main():
     log(f"prefilled {args.context} positions in {prefill_s:.2f}s (8-position batched tiles)")
 
     if args.cold_only:
-        print(json.dumps({"decode_kernels_cold": cold_decode_kernels(model, cache, cfg, args.context, None)}),
+        print(json.dumps({"decode_kernels_cold": cold_decode_kernels(model, cache, cfg, args.context, None),
+                          "decode_kernels_streaming": stream_decode_kernels(model, cache, cfg, args.context, None)}),
               flush=True)
         cache.destroy()
         model.destroy()
@@ -758,6 +791,7 @@ def main():
     back_to_back = {r: round(model.kernel_time(cache, r, 240), 3)
                     for r in ("qkv", "attention", "oproj", "gateup", "down", "head")}
     cold = cold_decode_kernels(model, cache, cfg, probe, None)
+    stream = stream_decode_kernels(model, cache, cfg, probe, None)
 
     # In-situ per-kernel times over the same positions.
     cache.length = args.context
@@ -790,7 +824,7 @@ def main():
     # What bounds the step; the cold launches against the read ceiling.
     bounds = decode_bounds(ctx, sum(v["launches_per_token"] for v in per_kernel.values()),
                            graphs=args.launch == "graph")
-    for v in cold.values():
+    for v in list(cold.values()) + list(stream.values()):
         v["frac_of_read_ceiling"] = round(v["GBps"] / bounds["read_ceiling_GBps"], 4)
 
     iso = attn = prefill = loader = paths = ppl = None
@@ -839,6 +873,7 @@ def main():
         "greedy_match_cpu_c_sample": match_c,
         "decode_bounds": bounds,
         "decode_kernels_cold": cold,
+        "decode_kernels_streaming": stream,
         "matvec_isolated": iso,
         "attention_decode": attn,
         "prefill_512": prefill,

@@ -386,6 +386,14 @@ int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, 
  * copies are allocated, filled and freed by the call; *us_per_launch covers all copies. */
 int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
                                float* us_per_launch, int32_t* copies);
+/* qh_decode_kernel_time_cold with the launch's grid sized for streaming instead of for one
+ * step's latency: blocks_per_copy blocks per copy (matrix roles; 0 = the step's own grid), each
+ * staging its activation vector once and then walking many rows with the next rows' loads in
+ * flight -- the same kernel and arithmetic as the step (the decode kernel's multi-item form, as
+ * the output head runs in the step), showing what it streams when its grid is not bound by
+ * latency. No counterpart in the reference. */
+int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
+                                 int32_t blocks_per_copy, float* us_per_launch, int32_t* copies);
 /* What bounds a batch-1 launch, measured on this device (no counterpart in the reference, which
  * measures the same bounds in web/decode-profile.html:288-327): `launches` launches of `blocks`
  * 256-thread blocks captured as one graph and replayed -- kind 0 does nothing; kind 1 reads the

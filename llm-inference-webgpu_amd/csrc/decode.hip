@@ -23,6 +23,7 @@
 // (WTile) before the block stages its activation vector, and a team with more
 // than one work item loads the next item's weights before the current item's
 // arithmetic.
+#include <algorithm>
 #include <type_traits>
 
 #include "attention.h"
@@ -486,6 +487,7 @@ static void apply_list(FusedArgs& f, const RoleList* list) {
 // same launch over a list of copies of its weights (matrix roles only).
 static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role,
                              const RoleList* list = nullptr) {
+  const int mb = list && list->max_blocks > 0 ? list->max_blocks : 1 << 30;  // blocks per copy
   const int kv_dim = m.kv_heads * m.head_dim;
   const LayerDev& l = m.layers_host[L];
   uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
@@ -511,7 +513,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.state = c.state;
       f.capacity = c.capacity;
       apply_list(f, list);
-      return fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2);
+      return fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2, mb);
     case QH_ROLE_ATTENTION:
       if (m.numerics == QH_NUMERICS_FAST) {
         SlotArgs a{};
@@ -556,11 +558,11 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         f.heads = m.heads;
         f.state = c.state;
         apply_list(f, list);
-        return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows);
+        return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows, mb);
       }
       f.in = c.attn;
       apply_list(f, list);
-      return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2);
+      return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2, mb);
     case QH_ROLE_GATEUP:
       f.eps = m.eps;
       f.w = l.gu;
@@ -568,13 +570,13 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.gain = l.post_norm;
       f.out = c.h;
       apply_list(f, list);
-      return fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2);
+      return fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2, mb);
     case QH_ROLE_DOWN:
       f.w = l.down;
       f.in = c.h;
       f.out = c.x;
       apply_list(f, list);
-      return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows);
+      return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows, mb);
     default:
       return hipErrorInvalidValue;
   }
@@ -591,7 +593,8 @@ static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& 
   f.out = c.logits;
   f.partials = static_cast<ArgPair*>(c.lm_partials);
   apply_list(f, list);
-  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, kLmMaxBlocks);
+  const int mb = list && list->max_blocks > 0 ? std::min(list->max_blocks, kLmMaxBlocks) : kLmMaxBlocks;
+  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, mb);
 }
 
 hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list) {

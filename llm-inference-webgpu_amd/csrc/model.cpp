@@ -1097,8 +1097,15 @@ int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, 
 // QH_ROLE_ATTENTION. The copies and their outputs are allocated here and freed before return.
 int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
                                float* us_per_launch, int32_t* copies) {
+  return qh_decode_kernel_time_stream(m, c, role, min_bytes, reps, 0, us_per_launch, copies);
+}
+
+int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
+                                 int32_t blocks_per_copy, float* us_per_launch, int32_t* copies) {
   QH_CHECK(m && c && c->m == m && us_per_launch && copies, QH_ERR_INVALID,
            "kernel_time_cold needs a model, its cache and outputs");
+  QH_CHECK(blocks_per_copy >= 0 && (blocks_per_copy == 0 || role != QH_ROLE_ATTENTION), QH_ERR_INVALID,
+           "blocks_per_copy must be >= 0, and 0 for the attention (its grid is one block per slot)");
   QH_CHECK(!c->busy, QH_ERR_BUSY, "forward() is already running; await it first");
   QH_CHECK(role >= QH_ROLE_QKV && role <= QH_ROLE_HEAD, QH_ERR_INVALID, "role %d has no single decode kernel", role);
   QH_CHECK(role != QH_ROLE_ATTENTION || m->dev.numerics == QH_NUMERICS_FAST, QH_ERR_INVALID,
@@ -1173,6 +1180,7 @@ int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t mi
     list.part_stride = (size_t)qh::lm_head_blocks(md);  // argmax partial entries per copy
     list.out = out;
     list.partials = partials;
+    list.max_blocks = blocks_per_copy;
     launch = [&]() { return qh::enqueue_role_list(s, md, cd, role, list); };
   }
   hipEvent_t e0 = nullptr, e1 = nullptr;

@@ -128,6 +128,7 @@ struct RoleList {
   size_t w_stride, s_stride, out_stride, part_stride;
   float* out;
   void* partials;
+  int max_blocks;  // blocks per copy (0: the decode step's own grid)
 };
 // The launch of QH_ROLE_QKV, OPROJ, GATEUP, DOWN (layer 0's operands otherwise) or HEAD over a list.
 hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list);

@@ -266,6 +266,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_score": [vp, vp, vp, i32, vp],
         "qh_model_config": [vp, vp],
         "qh_decode_kernel_time_cold": [vp, vp, i32, sz, i32, vp, vp],
+        "qh_decode_kernel_time_stream": [vp, vp, i32, sz, i32, i32, vp, vp],
         "qh_probe_launch_floor": [vp, i32, i32, i32, vp], "qh_read_ceiling": [vp, sz, i32, vp],
         "qh_model_set_numerics": [vp, i32], "qh_model_set_matmul": [vp, i32],
         "qh_cache_create": [vp, i32, vp], "qh_cache_free": [vp], "qh_cache_length": [vp, vp],
@@ -912,6 +913,15 @@ class GpuModel:
         us, n = ctypes.c_float(), ctypes.c_int32()
         _check(self.lib.qh_decode_kernel_time_cold(self.handle, cache.handle, ROLES.index(role), min_bytes, reps,
                                                    ctypes.byref(us), ctypes.byref(n)))
+        return us.value, n.value
+
+    def kernel_time_stream(self, cache: GpuKVCache, role: str, blocks_per_copy: int, min_bytes: int = 512 << 20,
+                           reps: int = 5):
+        """kernel_time_cold with blocks_per_copy blocks per copy: the same kernel on a grid sized for
+        streaming (see qh_decode_kernel_time_stream)."""
+        us, n = ctypes.c_float(), ctypes.c_int32()
+        _check(self.lib.qh_decode_kernel_time_stream(self.handle, cache.handle, ROLES.index(role), min_bytes, reps,
+                                                     blocks_per_copy, ctypes.byref(us), ctypes.byref(n)))
         return us.value, n.value
 
     def destroy(self) -> None:

@@ -1,5 +1,6 @@
 """The measurement entry points bench.py reports beside the decode step: a decode launch timed
-cold over copies of its operands (qh_decode_kernel_time_cold), the pure-read ceiling and the
+cold over copies of its operands (qh_decode_kernel_time_cold, and on streaming grids
+qh_decode_kernel_time_stream), the pure-read ceiling and the
 launch floor probes. They must run every role, report sane figures and leave the model and its
 cache as they were (the cold timing writes only the position's own decode scratch)."""
 import numpy as np
@@ -20,6 +21,13 @@ def test_cold_timing_runs_every_role_and_leaves_the_decode_intact(ctx, hip):
         us, copies = model.kernel_time_cold(a, role, 4 << 20, 2)
         print(f"cold {role}: {copies} copies, {us:.2f} us")
         assert us > 0 and copies >= 2, (role, us, copies)
+    for role in ("qkv", "oproj", "gateup", "down", "head"):
+        for bpc in (1, 3):  # streaming grids: each team walks several rows (the multi-item form)
+            us, copies = model.kernel_time_stream(a, role, bpc, 4 << 20, 2)
+            print(f"stream {role} x{bpc}: {copies} copies, {us:.2f} us")
+            assert us > 0 and copies >= 2, (role, bpc, us, copies)
+    with pytest.raises(hip.QwenHipError, match="blocks_per_copy"):
+        model.kernel_time_stream(a, "attention", 2, 4 << 20, 1)
     a.length = len(prompt)
     assert list(model.decode(a, first, 12)) == list(model.decode(b, first, 12))
     a.destroy()
