@@ -522,7 +522,7 @@ int qh_attention_splitk_list(qh_ctx* ctx, const float* d_q, const uint16_t* d_ke
   QH_CHECK(count == 1 || (key_stride >= kel && value_stride >= vel && key_stride % 8 == 0 && value_stride % 8 == 0),
            QH_ERR_INVALID, "cache strides overlap the caches or break 16-byte alignment");
   void* tmp = nullptr;
-  QH_HIP(hipMallocAsync(&tmp, qh::attention_list_partials_floats(count, heads, past + 1) * sizeof(float), ctx->stream));
+  QH_HIP(hipMallocAsync(&tmp, qh::attention_list_partials_floats(count, heads, kv_heads, past + 1) * sizeof(float), ctx->stream));
   hipError_t e = qh::launch_attention_splitk_list(ctx->stream, d_q, d_key_cache, d_value_cache, key_stride,
                                                   value_stride, count, capacity, d_out, past, heads, kv_heads,
                                                   static_cast<float*>(tmp));

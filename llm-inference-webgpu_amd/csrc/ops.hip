@@ -519,24 +519,40 @@ hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* 
   return launch_flash_prefill(s, a);
 }
 
-// Slots per head of the list operator: about four chunks per slot (a slot pipelines its
-// steps), up to 64 slots (the combine walks a head's slots in sequence).
-static int list_slots(int ctx) {
-  const int n = attn_chunks(ctx);
-  return n <= 16 ? 4 : n <= 64 ? 16 : kOpSlots;
+// Slots per head and waves per slot of the list operator. Each (cache, kv head) is one block
+// of W waves unless the context is long -- a slot of up to 256 32-key steps -- or the list
+// too short to give the device ~256 blocks; W gives each wave about eight steps (one wave for
+// the 4 steps of 128 positions, up to 8). Measured over >= 512 MiB of caches (14 heads / 2 kv
+// heads; GB/s against K/V bytes): 128 positions 1 x 1 4.2 TB/s (4 slots x 1: 2.5), 1024
+// 1 x 4 5.1 (4 x 1: 4.1), 4096 1 x 4 5.1 (16 x 1: 3.2), 32768 4 x 8 4.7 (64 x 1: 2.9):
+// fewer slots write and re-read fewer partials and merge in fewer terms.
+struct ListPlan {
+  int slots, waves;
+};
+static ListPlan list_plan(int ctx, int count, int kv_heads) {
+  const int steps = 2 * attn_chunks(ctx);
+  int slots = std::min(kOpSlots, std::max(1, steps / 256));
+  while (slots < kOpSlots && slots < steps && (long long)count * kv_heads * slots < 256) slots *= 2;
+  slots = slots <= 1 ? 1 : slots <= 4 ? 4 : slots <= 16 ? 16 : kOpSlots;  // the instantiated counts
+  const int per = (steps + slots - 1) / slots;
+  const int waves = per <= 8 ? 1 : per <= 32 ? 4 : 8;
+  return {slots, waves};
 }
 
-size_t attention_list_partials_floats(int count, int heads, int ctx) {
-  return (size_t)count * heads * list_slots(ctx) * kPartStride;
+size_t attention_list_partials_floats(int count, int heads, int kv_heads, int ctx) {
+  return (size_t)count * heads * list_plan(ctx, count, kv_heads).slots * kPartStride;
 }
 
 // The list runs the GQA-group MFMA form of the slots (one read of each K/V chunk per kv
 // head), then the slot combine.
 template <int MAXS>
-static hipError_t list_t(hipStream_t s, SlotArgs a, int count, float* out) {
+static hipError_t list_t(hipStream_t s, SlotArgs a, int count, int waves, float* out) {
   a.max_slots = MAXS;
   a.list_part = (size_t)a.heads * MAXS * kPartStride;
-  hipLaunchKernelGGL((k_attn_gqa<MAXS, 1>), dim3(a.kv_heads * MAXS, 1, count), dim3(kWave), 0, s, a);
+  const dim3 grid(a.kv_heads * MAXS, 1, count);
+  if (waves == 8) hipLaunchKernelGGL((k_attn_gqa<MAXS, 8>), grid, dim3(8 * kWave), 0, s, a);
+  else if (waves == 4) hipLaunchKernelGGL((k_attn_gqa<MAXS, 4>), grid, dim3(4 * kWave), 0, s, a);
+  else hipLaunchKernelGGL((k_attn_gqa<MAXS, 1>), grid, dim3(kWave), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_combine<true>, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
@@ -559,10 +575,12 @@ hipError_t launch_attention_splitk_list(hipStream_t s, const float* q, const uin
   a.kv_heads = kv_heads;
   a.list_k = list_k;
   a.list_v = list_v;
-  switch (list_slots(past + 1)) {
-    case 4: return list_t<4>(s, a, count, out);
-    case 16: return list_t<16>(s, a, count, out);
-    default: return list_t<kOpSlots>(s, a, count, out);
+  const ListPlan plan = list_plan(past + 1, count, kv_heads);
+  switch (plan.slots) {
+    case 1: return list_t<1>(s, a, count, plan.waves, out);
+    case 4: return list_t<4>(s, a, count, plan.waves, out);
+    case 16: return list_t<16>(s, a, count, plan.waves, out);
+    default: return list_t<kOpSlots>(s, a, count, plan.waves, out);
   }
 }
 

@@ -160,11 +160,11 @@ hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* 
                                  int capacity, float* out, int seq, int past, int heads, int kv_heads);
 // One query (position past) against `count` same-shape caches: key cache i at kc + i*list_k,
 // value cache i at vt + i*list_v (elements); out [count][heads*64]; `partials` holds
-// attention_list_partials_floats(count, heads, past + 1) floats.
+// attention_list_partials_floats(count, heads, kv_heads, past + 1) floats.
 hipError_t launch_attention_splitk_list(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
                                         size_t list_k, size_t list_v, int count, int capacity, float* out,
                                         int past, int heads, int kv_heads, float* partials);
-size_t attention_list_partials_floats(int count, int heads, int ctx);
+size_t attention_list_partials_floats(int count, int heads, int kv_heads, int ctx);
 // f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).
 void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);
