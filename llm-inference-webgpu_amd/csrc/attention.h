@@ -987,14 +987,82 @@ static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
   }
 }
 
-// The decode step's attention over `seq` queries (grid.y) and `count` list entries
-// (grid.z): k_attn_gqa with kDecodeSlots slots per head and four waves per slot, the
-// partials the decode combine (CombineIn) merges.
+// Slots per head of the decode attention for a cache of `capacity` positions. Up to
+// kLongCapacity: kDecodeSlots, merged in the o-projection's staging (CombineIn). Past it the
+// 2 x 16 blocks of that form stream the context through 32 CUs (19 us per launch at 32k
+// positions), so a long cache takes kLongSlots slots (256 blocks), merged by k_attn_merge_long
+// into the attention output before an o-projection that stages it as it is: one launch more
+// per layer, which costs more than it saves below ~8k positions. The choice depends on the
+// capacity only, so a cache's decode step and batched prefill merge alike.
 constexpr int kDecodeWaves = 4;
-static inline hipError_t launch_attn_decode(hipStream_t s, SlotArgs a, int seq, int count) {
-  a.max_slots = kDecodeSlots;
-  hipLaunchKernelGGL((k_attn_gqa<kDecodeSlots, kDecodeWaves>), dim3(a.kv_heads * kDecodeSlots, seq, count),
+constexpr int kLongSlots = 128;
+constexpr int kLongCapacity = 8192;
+__host__ __device__ inline bool decode_attn_long(int capacity) { return capacity > kLongCapacity; }
+__host__ __device__ inline int decode_attn_slots(int capacity) {
+  return decode_attn_long(capacity) ? kLongSlots : kDecodeSlots;
+}
+
+// out[z][t][h*64 + d] = the merge of the kLongSlots slot partials of (query t, head h): one
+// 64-lane block per (h, t, list entry z). Every load is issued before any is used (the slots
+// are a compile-time count; empty slots are neutral: m = -inf, l = 0, o = 0); the weights
+// 2^(m_s - M) are shared through LDS and the output sums the slots in order.
+template <int MAXS>
+static __global__ __launch_bounds__(kWave) void k_attn_merge_long(const float* __restrict__ part,
+                                                                  float* __restrict__ out, int heads,
+                                                                  size_t list_part) {
+  static_assert(MAXS % kWave == 0, "whole slots per lane");
+  constexpr int kPer = MAXS / kWave;
+  __shared__ float wl[MAXS];
+  const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const size_t z = blockIdx.z;
+  const float* p = part + z * list_part + ((size_t)t * heads + h) * MAXS * kPartStride;
+  float ms[kPer], ls[kPer], ov[MAXS];
+#pragma unroll
+  for (int k = 0; k < kPer; k++) {
+    ms[k] = p[(size_t)(d + k * kWave) * kPartStride];
+    ls[k] = p[(size_t)(d + k * kWave) * kPartStride + 1];
+  }
+#pragma unroll
+  for (int s2 = 0; s2 < MAXS; s2++) ov[s2] = p[(size_t)s2 * kPartStride + 4 + d];
+  float M = ms[0];
+#pragma unroll
+  for (int k = 1; k < kPer; k++) M = fmaxf(M, ms[k]);
+  M = team_max<64>(M);  // slot 0 always holds position 0
+  float L = 0.f;
+#pragma unroll
+  for (int k = 0; k < kPer; k++) {
+    const float w = ms[k] == -INFINITY ? 0.f : exp2_reduced(ms[k] - M);
+    wl[d + k * kWave] = w;
+    L = fmaf(w, ls[k], L);
+  }
+  L = team_sum<64>(L);
+  __builtin_amdgcn_wave_barrier();  // one wave: its LDS writes land before its reads
+  float A = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < MAXS; s2++) A = fmaf(wl[s2], ov[s2], A);
+  out[((z * gridDim.y + t) * heads + h) * kHeadDim + d] = A / L;
+}
+
+// The decode step's attention over `seq` queries (grid.y) and `count` list entries (grid.z):
+// k_attn_gqa with decode_attn_slots(capacity) slots per head and four waves per slot. Short
+// caches leave the slot partials for the decode combine (CombineIn); long ones merge them
+// into `merged` ([count][seq][heads*64]) when it is given (the cold list times the slots
+// alone).
+static inline hipError_t launch_attn_decode(hipStream_t s, SlotArgs a, int seq, int count,
+                                            float* merged = nullptr) {
+  if (!decode_attn_long(a.capacity)) {
+    a.max_slots = kDecodeSlots;
+    hipLaunchKernelGGL((k_attn_gqa<kDecodeSlots, kDecodeWaves>), dim3(a.kv_heads * kDecodeSlots, seq, count),
+                       dim3(kDecodeWaves * kWave), 0, s, a);
+    return hipGetLastError();
+  }
+  a.max_slots = kLongSlots;
+  hipLaunchKernelGGL((k_attn_gqa<kLongSlots, kDecodeWaves>), dim3(a.kv_heads * kLongSlots, seq, count),
                      dim3(kDecodeWaves * kWave), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !merged) return e;
+  hipLaunchKernelGGL(k_attn_merge_long<kLongSlots>, dim3(a.heads, seq, count), dim3(kWave), 0, s, a.part, merged,
+                     a.heads, a.list_part);
   return hipGetLastError();
 }
 

@@ -450,7 +450,9 @@ int lm_head_blocks(const ModelDev& m) {
 
 size_t lm_partials_bytes(const ModelDev& m) { return (size_t)lm_head_blocks(m) * sizeof(ArgPair); }
 
-size_t attn_part_bytes(const ModelDev& m) { return (size_t)m.heads * kDecodeSlots * kPartStride * sizeof(float); }
+size_t attn_part_bytes(const ModelDev& m, int capacity) {
+  return (size_t)m.heads * decode_attn_slots(capacity) * kPartStride * sizeof(float);
+}
 
 int launches_per_step(const ModelDev& m, StepInput in) {
   return (in == STEP_GATHER ? 1 : 0) + 5 * m.layers + 2;
@@ -526,7 +528,7 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         a.vstride = c.vstride;
         a.heads = m.heads;
         a.kv_heads = m.kv_heads;
-        return launch_attn_decode(s, a, 1, 1);
+        return launch_attn_decode(s, a, 1, 1, c.attn);  // a long cache merges into c.attn
       } else {
         ExactArgs a{};
         a.q = c.q;
@@ -553,12 +555,17 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
     case QH_ROLE_OPROJ:
       f.w = l.o;
       f.out = c.x;
-      if (m.numerics == QH_NUMERICS_FAST) {
+      if (m.numerics == QH_NUMERICS_FAST && !decode_attn_long(c.capacity)) {
         f.in = c.part;
         f.heads = m.heads;
         f.state = c.state;
         apply_list(f, list);
         return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows, mb);
+      }
+      if (m.numerics == QH_NUMERICS_FAST) {  // a long cache: the attention output is merged already
+        f.in = c.attn;
+        apply_list(f, list);
+        return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.o.rows, mb);
       }
       f.in = c.attn;
       apply_list(f, list);
@@ -617,8 +624,8 @@ hipError_t enqueue_attention_list(hipStream_t s, const ModelDev& m, const CacheD
   a.kv_heads = m.kv_heads;
   a.list_k = copy_elems;
   a.list_v = copy_elems;
-  a.list_part = (size_t)m.heads * kDecodeSlots * kPartStride;
-  return launch_attn_decode(s, a, 1, count);
+  a.list_part = (size_t)m.heads * decode_attn_slots(c.capacity) * kPartStride;
+  return launch_attn_decode(s, a, 1, count);  // the slots alone
 }
 
 hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer) {

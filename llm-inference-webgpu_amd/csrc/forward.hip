@@ -327,8 +327,22 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
       a.vstride = c.vstride;
       a.heads = m.heads;
       a.kv_heads = m.kv_heads;
-      if ((e = launch_attn_decode(s, a, seq, 1)) != hipSuccess) return e;
-      hipLaunchKernelGGL(k_attn_merge_rows, dim3(seq), dim3(kBlock), 0, s, p.part, m.heads, p.ATT);
+      if (!decode_attn_long(c.capacity)) {
+        if ((e = launch_attn_decode(s, a, seq, 1)) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_attn_merge_rows, dim3(seq), dim3(kBlock), 0, s, p.part, m.heads, p.ATT);
+      } else {
+        // a long cache's kLongSlots partials per query, a share of the rows at a time so that
+        // they fit the workspace sized for kDecodeSlots (each query's result is its own)
+        const int share = std::max(1, (int)p.positions * kDecodeSlots / kLongSlots);
+        for (int t0 = 0; t0 < seq; t0 += share) {
+          SlotArgs b = a;
+          b.q = p.Q + (size_t)t0 * m.heads * kHeadDim;
+          b.past = past + t0;
+          if ((e = launch_attn_decode(s, b, std::min(share, seq - t0), 1, p.ATT + (size_t)t0 * m.heads * kHeadDim)) !=
+              hipSuccess)
+            return e;
+        }
+      }
     } else {
       ExactArgs a{};
       a.q = p.Q;

@@ -607,7 +607,7 @@ int qh_cache_create(qh_model* m, int32_t capacity, qh_cache** out) {
   A((size_t)md.heads * d.score_stride * 4, (void**)&d.scores);
   A((size_t)md.heads * spans * 4, (void**)&d.maxes);
   A(256, (void**)&d.attn_counters);
-  A(qh::attn_part_bytes(md), (void**)&d.part);
+  A(qh::attn_part_bytes(md, capacity), (void**)&d.part);
   A(qh::lm_partials_bytes(md), &d.lm_partials);
   if (!rc && hipHostMalloc((void**)&c->h_pinned, 64, hipHostMallocDefault) != hipSuccess) {
     rc = fail(QH_ERR_NOMEM, "pinned allocation failed");
@@ -1136,7 +1136,7 @@ int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t 
     uint16_t* kv = nullptr;
     float* part = nullptr;
     err = grab((size_t)count * stride * 2, (void**)&kv);
-    if (err == hipSuccess) err = grab((size_t)count * md.heads * 16 * 68 * 4, (void**)&part);
+    if (err == hipSuccess) err = grab((size_t)count * qh::attn_part_bytes(md, cd.capacity), (void**)&part);
     for (int z = 0; z < count && err == hipSuccess; z++)
       err = hipMemcpyAsync(kv + (size_t)z * stride, cd.kv, elems * 2, hipMemcpyDeviceToDevice, s);
     launch = [&, kv, part, stride]() { return qh::enqueue_attention_list(s, md, cd, kv, count, stride, part); };

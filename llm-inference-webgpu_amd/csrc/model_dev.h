@@ -52,7 +52,7 @@ struct CacheDev {
   float* maxes;        // [heads][spans(capacity)]: per-span score maxima
   int score_stride;    // capacity rounded up to 4
   int* attn_counters;  // [heads], zero between launches
-  float* part;         // [heads][kDecodeSlots][kPartStride]: split-K attention slot partials
+  float* part;         // [heads][decode_attn_slots(capacity)][kPartStride]: split-K attention slot partials
   void* lm_partials;   // argmax block partials
   int lm_blocks;
 };
@@ -140,6 +140,6 @@ hipError_t enqueue_attention_list(hipStream_t s, const ModelDev& m, const CacheD
 int lm_head_blocks(const ModelDev& m);
 size_t lm_partials_bytes(const ModelDev& m);
 // Bytes of the split-K attention slot partials of one position (CacheDev::part).
-size_t attn_part_bytes(const ModelDev& m);
+size_t attn_part_bytes(const ModelDev& m, int capacity);
 
 }  // namespace qh

@@ -295,12 +295,14 @@ def test_decode_launches_match_oracle_at_full_shape(ctx, hip, full_ckpt, numeric
     model.destroy()
 
 
-@pytest.mark.parametrize("P", [2600, 4700])
+@pytest.mark.parametrize("P", [2600, 4700, 9000])
 def test_decode_attention_launch_past_2048_at_full_shape(ctx, hip, full_ckpt, P):
     """The fast decode attention at the full shape (14 query heads over 2 kv heads) where a
     slot holds more 32-key steps than its block has waves (past 2048 positions each wave walks
-    two or more steps before the waves merge), then the o-projection's slot merge: against the
-    CPU path's attention and o-projection on the same q and cache rows, within 1e-5."""
+    two or more steps before the waves merge), then the o-projection's slot merge -- past 8192
+    positions the long form's 128 slots and their merge launch, then the o-projection of the
+    merged output: against the CPU path's attention and o-projection on the same q and cache
+    rows, within 1e-5."""
     cfg = hip.QWEN25_05B
     d, kv = cfg.hidden, cfg.kv_dim
     model = hip.GpuModel.load_checkpoint(ctx, full_ckpt, cfg, "int4", 128, "int8", maxPositions=P + 8)

@@ -240,12 +240,13 @@ def test_config4_full_shape_int4_matches_oracle(ctx, hip, full_ckpt, numerics):
     model.destroy()
 
 
-@pytest.mark.parametrize("prompt_len", [1400, 3000])
+@pytest.mark.parametrize("prompt_len", [1400, 3000, 9000])
 def test_fast_numerics_long_context_matches_exact(ctx, hip, prompt_len):
-    """Past 16 x 64 positions each split-K slot of the fast path spans several chunks, and past
-    2048 a slot has more 32-key steps than its block has waves (each wave then walks several);
-    the fast step must stay within the logit tolerance of the exact one and choose the same
-    greedy tokens."""
+    """Past 16 x 64 positions each split-K slot of the fast path spans several chunks, past
+    2048 a slot has more 32-key steps than its block has waves (each wave then walks several),
+    and past 8192 the cache takes the long form (128 slots, merged by a launch of its own); the
+    fast step must stay within the logit tolerance of the exact one and choose the same greedy
+    tokens."""
     cfg = tiny(hip)
     ckpt = hip.synthesize_checkpoint(cfg, seed=11)
     tensors = hip.device_tensors(ckpt, cfg, "int4", 128, "int8")
@@ -290,6 +291,30 @@ def test_batched_prefill_equals_one_position_steps_bitwise(ctx, hip, numerics, s
         np.testing.assert_array_equal(pa["key"].view(np.uint32), pb["key"].view(np.uint32))
         np.testing.assert_array_equal(pa["value"].view(np.uint32), pb["value"].view(np.uint32))
     # and decoding on from either cache continues identically
+    assert list(model.decode(cb, a["argmax"], 6)) == list(model.decode(cs, b["argmax"], 6))
+    cb.destroy()
+    cs.destroy()
+    model.destroy()
+
+
+def test_long_cache_batched_prefill_equals_one_position_steps_bitwise(ctx, hip):
+    """A cache past 8192 positions takes the long attention form (128 slots per head, merged
+    by their own launch before the o-projection); the batched prefill (the slots of a share
+    of the rows at a time) still equals single decode steps bit for bit, and decoding on
+    matches."""
+    cfg = tiny(hip)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=23)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "int4", 128, "int8"), cfg, maxPositions=8400)
+    ids = hip.synth_tokens(23, "long.batched", cfg.vocab, 700)
+    cb, cs = model.newCache(8300), model.newCache(8300)
+    a = model.forward_tokens(ids, cb)
+    model.set_matmul("matvec")
+    b = model.forward_tokens(ids, cs)
+    np.testing.assert_array_equal(a["logits"].view(np.uint32), b["logits"].view(np.uint32))
+    for L in range(cfg.layers):
+        pa, pb = cb.present(L), cs.present(L)
+        np.testing.assert_array_equal(pa["key"].view(np.uint32), pb["key"].view(np.uint32))
+        np.testing.assert_array_equal(pa["value"].view(np.uint32), pb["value"].view(np.uint32))
     assert list(model.decode(cb, a["argmax"], 6)) == list(model.decode(cs, b["argmax"], 6))
     cb.destroy()
     cs.destroy()
