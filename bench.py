@@ -696,6 +696,8 @@ def main():
                     help="only the same-session comparison of the matmul paths over prompt lengths")
     ap.add_argument("--loader-only", action="store_true",
                     help="only the loader's conversion kernels and the two whole-model loads")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the config-3 attention list over contexts 128..32768 (for profiling it)")
     ap.add_argument("--perplexity-only", action="store_true",
                     help="only the perplexity protocol over the four weight schemes")
     ap.add_argument("--cold-only", action="store_true",
@@ -733,6 +735,10 @@ def main():
         return
     if args.scaling:
         print(json.dumps({"scaling": scaling_bench(ctx, cfg, ckpt)}), flush=True)
+        ctx.close()
+        return
+    if args.attention_only:
+        print(json.dumps({"attention_decode": attention_sweep(ctx)}), flush=True)
         ctx.close()
         return
     if args.perplexity_only:

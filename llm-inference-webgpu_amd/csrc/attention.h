@@ -410,6 +410,7 @@ struct SlotArgs {
   const uint16_t* vt;    // [kv_heads][64][vstride] f16
   const int* d_pos;      // when set, past is read from the device (decode)
   float* part;           // [seq][heads][max_slots][kPartStride]
+  float* out;            // k_attn_gqa with one slot: the output [list][seq][heads*64] in place of partials
   int past, capacity, vstride, heads, kv_heads, max_slots;
   // A list of same-shape caches, one per blockIdx.z (0 apart from the list operator):
   // element strides between consecutive key caches, value caches, and partial sets.
@@ -944,7 +945,23 @@ static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
     --left;
   }
   float* dst = a.part + z * a.list_part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
+  // One slot and an output buffer: the slot's state is the result, written as o / l (what the
+  // combine of a single slot computes, bit for bit) with no partials and no combine launch.
+  float* res = nullptr;
+  if constexpr (MAXS == 1) {
+    if (a.out) res = a.out + (((size_t)z * gridDim.y + t) * a.heads + h) * kHeadDim;
+  }
   if constexpr (W == 1) {  // the merge below would scale by exactly 1
+    if (res) {
+      if (n < group) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+          const v4f r4 = {o[dt][0] / l, o[dt][1] / l, o[dt][2] / l, o[dt][3] / l};
+          *reinterpret_cast<v4f*>(res + 16 * dt + 4 * g) = r4;
+        }
+      }
+      return;
+    }
     if (n < group) {
 #pragma unroll
       for (int dt = 0; dt < 4; dt++) *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = (v4f)o[dt];
@@ -977,7 +994,9 @@ static __global__ __launch_bounds__(kWave * W) void k_attn_gqa(SlotArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) ot[r] = fmaf(ov[r], wt, ot[r]);
     }
-    if (n < group) {
+    if (res) {
+      if (n < group) *reinterpret_cast<v4f*>(res + 16 * dt + 4 * g) = v4f{ot[0] / lt, ot[1] / lt, ot[2] / lt, ot[3] / lt};
+    } else if (n < group) {
       *reinterpret_cast<v4f*>(dst + 4 + 16 * dt + 4 * g) = ot;
       if (dt == 0 && g == 0) {
         dst[0] = mx;

@@ -525,7 +525,8 @@ hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* 
 // the 4 steps of 128 positions, up to 8). Measured over >= 512 MiB of caches (14 heads / 2 kv
 // heads; GB/s against K/V bytes): 128 positions 1 x 1 4.2 TB/s (4 slots x 1: 2.5), 1024
 // 1 x 4 5.1 (4 x 1: 4.1), 4096 1 x 4 5.1 (16 x 1: 3.2), 32768 4 x 8 4.7 (64 x 1: 2.9):
-// fewer slots write and re-read fewer partials and merge in fewer terms.
+// fewer slots write and re-read fewer partials and merge in fewer terms. With one slot the
+// block writes the output itself and the combine launch goes (128 positions: 4.2 -> 5.5).
 struct ListPlan {
   int slots, waves;
 };
@@ -549,12 +550,13 @@ template <int MAXS>
 static hipError_t list_t(hipStream_t s, SlotArgs a, int count, int waves, float* out) {
   a.max_slots = MAXS;
   a.list_part = (size_t)a.heads * MAXS * kPartStride;
+  if (MAXS == 1) a.out = out;  // a single slot's state is the result: no partials, no combine
   const dim3 grid(a.kv_heads * MAXS, 1, count);
   if (waves == 8) hipLaunchKernelGGL((k_attn_gqa<MAXS, 8>), grid, dim3(8 * kWave), 0, s, a);
   else if (waves == 4) hipLaunchKernelGGL((k_attn_gqa<MAXS, 4>), grid, dim3(4 * kWave), 0, s, a);
   else hipLaunchKernelGGL((k_attn_gqa<MAXS, 1>), grid, dim3(kWave), 0, s, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || MAXS == 1) return e;
   hipLaunchKernelGGL(k_attn_combine<true>, dim3(a.heads, 1, count), dim3(kWave), 0, s, a.part, out, a.past, a.heads, MAXS,
                      a.list_part);
   return hipGetLastError();
