@@ -139,6 +139,7 @@ struct qh_cache {
   qh::PrefillDev pw{};
   qh::PrefillBytes pw_bytes{};
   void* pw_mem = nullptr;
+  int pw_matmul = -1;  // the matmul mode the workspace was last checked for
 
   int alloc(size_t n, void** p) {
     if (hipMalloc(p, n ? n : 4) != hipSuccess) return fail(QH_ERR_NOMEM, "hipMalloc of %zu bytes failed", n);
@@ -728,10 +729,15 @@ int finish_forward(qh_cache* c, int seq, float* h_logits, int32_t* h_argmax) {
 // carved in the order prefill_bytes() counts it.
 int ensure_prefill(qh_cache* c) {
   qh_model* m = c->m;
+  // The sizes depend on the model, the cache and the matmul mode only: checked once per mode
+  // (they walk every layer matrix on the host, in front of the forward's first launch).
+  if (c->pw_mem && c->pw_matmul == m->matmul) return QH_OK;
   const qh::PrefillBytes b = qh::prefill_bytes(m->dev, c->dev, m->matmul);
   if (c->pw_mem && b.floats <= c->pw_bytes.floats && b.counters <= c->pw_bytes.counters &&
-      b.scratch <= c->pw_bytes.scratch)
+      b.scratch <= c->pw_bytes.scratch) {
+    c->pw_matmul = m->matmul;
     return QH_OK;
+  }
   hipStream_t s = m->ctx->stream;
   QH_HIP(hipStreamSynchronize(s));
   drop_prefill_graphs(c);  // they address the workspace being replaced
@@ -744,6 +750,7 @@ int ensure_prefill(qh_cache* c) {
   }
   QH_HIP(hipMemsetAsync(static_cast<char*>(c->pw_mem) + fbytes, 0, cbytes, s));
   c->pw_bytes = b;
+  c->pw_matmul = m->matmul;
   const qh::ModelDev& d = m->dev;
   const size_t P = qh::prefill_chunk(d, c->dev);
   const size_t hd = d.hidden, kv = (size_t)d.kv_heads * d.head_dim, f = d.intermediate;

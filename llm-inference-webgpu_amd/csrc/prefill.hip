@@ -617,12 +617,14 @@ int digits_width(int K) { return padded_k(K); }
 
 // Split partials of every launch of 1..M rows. Not the M-row figure alone: below a 64-row
 // tile boundary there are fewer tiles and so more splits, and the partials of a smaller M
-// can outgrow M's own.
+// can outgrow M's own. The split count depends on m only through its 64-row tiles, so within
+// each band of 64 rows the largest m holds the most: one evaluation per band (this runs on
+// the host before every batched forward).
 size_t gemm_partials_bytes(const DMat& w, int M) {
   size_t most = 0;
-  for (int m = 1; m <= M; m++) {
-    const int splits = gemm_splits(w, m);
-    if (splits > 1) most = std::max(most, (size_t)splits * m * w.rows * sizeof(float));
+  for (int hi = std::min(M, kGM); hi >= 1; hi = hi == M ? 0 : std::min(M, hi + kGM)) {
+    const int splits = gemm_splits(w, hi);
+    if (splits > 1) most = std::max(most, (size_t)splits * hi * w.rows * sizeof(float));
   }
   return most;
 }
