@@ -448,10 +448,16 @@ __device__ __forceinline__ void wtile_dot(const DMat& m, const WTile<FMT, R, KC>
 //
 // Quantized chunks take the scale out of the sum: an int8 chunk contributes
 // sum((q+128) x) - 128 sum(x), an int4 chunk scale * (sum(level x) - zero sum(x)),
-// with the codes converted by one v_cvt_f32_ubyte each (int8 biased by an xor,
-// int4 even nibbles masked in place and odd ones masked as 16*level, rescaled by
-// the exact 1/16 once per chunk), so a weight costs one conversion and one f32
-// fma. sum(x) over each chunk (the "chunk sum") is computed once, while staging,
+// with the int8 codes converted by one v_cvt_f32_ubyte each (biased by an xor), so
+// an int8 weight costs one conversion and one f32 fma. int4 codes need no
+// conversion: a nibble masked in place in the low byte of a 16-bit half is the f16
+// subnormal level * 2^-24 (odd nibbles, masked as 16*level, rescaled by the exact
+// 1/16 once per chunk), which v_fma_mix_f32 reads directly; four masks and one
+// shift unpack 8 levels, so 8 int4 weights cost 13 VALU ops instead of 18. The sums
+// run 2^-24 below the scale of the f32 form, and scaling by a power of two commutes
+// with rounding, so they carry the same bits (the scale folds 2^24 back in) while
+// every partial sum stays a normal f32 (|partial| >= 2^-102, or zero).
+// sum(x) over each chunk (the "chunk sum") is computed once, while staging,
 // as a pairwise tree: ((x0+x1)+(x2+x3)) per 4-element group, then a butterfly
 // over the chunk's groups. A row's chunk contributions are added in ascending
 // chunk order per lane, then across the team by team_sum, so every path over a
@@ -546,10 +552,11 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] += d[r];
   } else {
+    // The sums below are the f32 form's sums times 2^-24 (see the f32 core's notes).
     float pe[R], po[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-      pe[r] = -z[r] * sx;
+      pe[r] = -z[r] * sx * 0x1p-24f;
       po[r] = 0.f;
     }
     v4f xg[8];  // the chunk's activations, all read before any arithmetic
@@ -557,23 +564,26 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
     for (int k = 0; k < 8; k++) xg[k] = *reinterpret_cast<const v4f*>(p + k * gs);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      // dword k holds elements 8k .. 8k+7: byte b = (element 8k+2b) | (element 8k+2b+1) << 4
+      // dword k holds elements 8k .. 8k+7: byte b = (element 8k+2b) | (element 8k+2b+1) << 4.
+      // Halves of m0: elements 8k, 8k+4; m1: 16x 8k+1, 8k+5; m2: 8k+2, 8k+6; m3: 16x 8k+3, 8k+7.
       const v4f xa = xg[2 * k], xb = xg[2 * k + 1];
 #pragma unroll
       for (int r = 0; r < R; r++) {
-        const uint32_t lo = w[r][k] & 0x0F0F0F0Fu, hi = w[r][k] & 0xF0F0F0F0u;
-        pe[r] = fmaf(ubyte<0>(lo), xa.x, pe[r]);
-        po[r] = fmaf(ubyte<0>(hi), xa.y, po[r]);
-        pe[r] = fmaf(ubyte<1>(lo), xa.z, pe[r]);
-        po[r] = fmaf(ubyte<1>(hi), xa.w, po[r]);
-        pe[r] = fmaf(ubyte<2>(lo), xb.x, pe[r]);
-        po[r] = fmaf(ubyte<2>(hi), xb.y, po[r]);
-        pe[r] = fmaf(ubyte<3>(lo), xb.z, pe[r]);
-        po[r] = fmaf(ubyte<3>(hi), xb.w, po[r]);
+        const uint32_t d = w[r][k], d8 = d >> 8;
+        const uint32_t m0 = d & 0x000F000Fu, m1 = d & 0x00F000F0u;
+        const uint32_t m2 = d8 & 0x000F000Fu, m3 = d8 & 0x00F000F0u;
+        pe[r] = fmaf(f16_lo(m0), xa.x, pe[r]);
+        po[r] = fmaf(f16_lo(m1), xa.y, po[r]);
+        pe[r] = fmaf(f16_lo(m2), xa.z, pe[r]);
+        po[r] = fmaf(f16_lo(m3), xa.w, po[r]);
+        pe[r] = fmaf(f16_hi(m0), xb.x, pe[r]);
+        po[r] = fmaf(f16_hi(m1), xb.y, po[r]);
+        pe[r] = fmaf(f16_hi(m2), xb.z, pe[r]);
+        po[r] = fmaf(f16_hi(m3), xb.w, po[r]);
       }
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = fmaf(s[r], fmaf(po[r], 0.0625f, pe[r]), acc[r]);
+    for (int r = 0; r < R; r++) acc[r] = fmaf(s[r] * 0x1p24f, fmaf(po[r], 0.0625f, pe[r]), acc[r]);
   }
 }
 
