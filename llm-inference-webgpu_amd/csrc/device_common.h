@@ -848,11 +848,17 @@ __device__ __forceinline__ void stage_copy_finish_f32(const StageIn& in, int n, 
   __syncthreads();
 }
 
-// silu(g) * u in f32, as the reference's WGSL SWIGLU evaluates it
-// (src/gpu/kernels.js:502-514): g / (1 + e^-g) * up, each operation rounded alone.
+// silu(g) * u in f32 for the reference's WGSL SWIGLU (src/gpu/kernels.js:502-514), g / (1 + e^-g)
+// * up: WGSL bounds exp and division by a few ulps rather than rounding them correctly, and here
+// e^-g is the hardware exp2 of a fraction in [-0.5, 0.5] scaled by 2^rint (the range where
+// v_exp_f32 is accurate to about an ulp) and the division the hardware reciprocal -- ~9 VALU
+// instructions against ~30 for a correctly rounded expf and division, a few ulps from them. A
+// large negative g gives e = inf and -0; a non-finite g or u gives a non-finite value.
 __device__ __forceinline__ float swiglu_f32(float g, float u) {
-#pragma clang fp contract(off)
-  return g / (1.0f + expf(-g)) * u;
+  const float t = -g * 1.44269504088896340736f;
+  const float n = __builtin_rintf(t);
+  const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f(t - n), (int)n);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 struct ArgPair {

@@ -90,20 +90,6 @@ __device__ __forceinline__ int row_of_block(int b, int M) {
   return 16 * (xcd + 8 * (r >> 4)) + (r & 15);
 }
 
-// silu(g) * u for the swiglu row, whose values only feed the next contraction's digits (an
-// absolute error up to max|row| * 2^-17 / 127 each): e^-g as the hardware exp2 of a fraction in
-// [-0.5, 0.5] scaled by 2^rint (the range where v_exp_f32 is accurate to about an ulp) and the
-// hardware reciprocal, a few ulps in all, against the ~30 instructions of the correctly rounded
-// expf and division that swiglu_f32 spends for the decode and batched paths. A large negative g
-// gives e = inf and -0 as swiglu_f32 does; a non-finite g or u gives a non-finite value (NaN
-// where swiglu_f32 may give inf), and either makes the row's digits zero and its factor NaN.
-__device__ __forceinline__ float swiglu_row(float g, float u) {
-  const float t = -g * 1.44269504088896340736f;
-  const float n = __builtin_rintf(t);
-  const float e = __builtin_ldexpf(__builtin_amdgcn_exp2f(t - n), (int)n);
-  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
-}
-
 template <int OP, int J>
 __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
   __shared__ float red[kBlock / kWave];
@@ -171,8 +157,8 @@ __global__ __launch_bounds__(kBlock) void k_rows(RowArgs a) {
       for (int w = 0; w < W; w++) sum[j][w] += bias[j][w];
     }
     if constexpr (OP == ROW_SWIGLU)
-      v[j] = v4f{swiglu_row(sum[j][0][0], sum[j][0][1]), swiglu_row(sum[j][0][2], sum[j][0][3]),
-                 swiglu_row(sum[j][1][0], sum[j][1][1]), swiglu_row(sum[j][1][2], sum[j][1][3])};
+      v[j] = v4f{swiglu_f32(sum[j][0][0], sum[j][0][1]), swiglu_f32(sum[j][0][2], sum[j][0][3]),
+                 swiglu_f32(sum[j][1][0], sum[j][1][1]), swiglu_f32(sum[j][1][2], sum[j][1][3])};
     else
       v[j] = sum[j][0];
     if (kAdds && a.resid) {
