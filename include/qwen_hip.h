@@ -173,9 +173,12 @@ size_t qh_value_cache_bytes(int32_t capacity, int32_t kv_heads, int32_t head_dim
 int qh_attention(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
                  const uint16_t* d_value_cache, int32_t capacity, float* d_out, int32_t seq,
                  int32_t past, int32_t heads, int32_t kv_heads, int32_t head_dim);
-/* As qh_attention with a split-K online softmax over 64-position chunks: one pass over K/V
- * shared by the query heads of a kv head, splits combined in order. Exact only to f32
- * rounding; the fast form for long contexts. */
+/* As qh_attention with a split-K online softmax over 64-position chunks: the decode step's
+ * attention, one block per (query, kv head, run of chunks) with the kv head's query heads as
+ * the columns of f16 matrix-core products, so each K/V chunk is read once per kv head; 16 runs
+ * per head up to 8192 positions of capacity, 128 past it; the runs are merged in order.
+ * Exact only to f32 rounding (~1e-6 of the output); the fast form for long contexts. A
+ * query's result does not depend on `seq`: prefill rows equal one-query calls bit for bit. */
 int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cache,
                         const uint16_t* d_value_cache, int32_t capacity, float* d_out,
                         int32_t seq, int32_t past, int32_t heads, int32_t kv_heads,
@@ -197,6 +200,13 @@ int qh_attention_splitk_list(qh_ctx* ctx, const float* d_q, const uint16_t* d_ke
                              const uint16_t* d_value_cache, size_t key_stride, size_t value_stride,
                              int32_t count, int32_t capacity, float* d_out, int32_t past, int32_t heads,
                              int32_t kv_heads, int32_t head_dim);
+/* The launch shape qh_attention_splitk_list takes for a query at position context-1 over
+ * `count` caches with `kv_heads` kv heads: *h_slots runs of chunks per (cache, kv head) (1, 4,
+ * 16 or 64; with one the block writes the output itself and no merge launch runs) and
+ * *h_waves waves per run (1, 4 or 8). Host-only: it lets a test name the kernel a list call
+ * runs (no counterpart in the reference). */
+int qh_attention_list_plan(int32_t context, int32_t count, int32_t kv_heads, int32_t* h_slots,
+                           int32_t* h_waves);
 
 /* SWIGLU (kernels.js:502-515): gate = silu(gate) * up, in place. */
 int qh_swiglu(qh_ctx* ctx, float* d_gate, const float* d_up, int32_t n);
@@ -365,7 +375,8 @@ enum {
   QH_ROLE_HEAD = 6,      /* final rmsnorm + lm_head + argmax */
   QH_ROLE_COUNT = 7
 };
-/* As qh_decode, but with direct launches and a device event before every launch, so each
+/* As qh_decode, but with direct launches, each timed from its dispatch's own start to its end
+ * (the interval a kernel tracer reports, nothing enqueued between the launches), so each
  * kernel's in-situ time is measured (GpuContext.timed, src/gpu/device.js:301-338).
  * h_role_ms[QH_ROLE_COUNT] receives the summed milliseconds per role over all steps and
  * h_role_launches[QH_ROLE_COUNT] the launch counts. Tokens are identical to qh_decode's. */

@@ -17,6 +17,7 @@ this module's own.
 from __future__ import annotations
 
 import json
+import math
 import os
 from dataclasses import dataclass
 
@@ -49,7 +50,7 @@ class TensorInfo:
 
     @property
     def numel(self) -> int:
-        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
+        return math.prod(self.shape)  # exact Python integers: a huge shape cannot wrap to a small count
 
     @property
     def byte_length(self) -> int:

@@ -491,7 +491,7 @@ int qh_attention_splitk(qh_ctx* ctx, const float* d_q, const uint16_t* d_key_cac
   int rc = check_attention(ctx, d_q, d_key_cache, d_value_cache, capacity, d_out, seq, past, heads,
                            kv_heads, head_dim);
   if (rc) return rc;
-  const size_t bytes = qh::attention_partials_floats(seq, heads) * sizeof(float);
+  const size_t bytes = qh::attention_partials_floats(seq, heads, capacity) * sizeof(float);
   // Partials in the context scratch after its counter region; larger prefill shapes get a
   // temporary buffer.
   if (bytes <= ctx->scratch_bytes - qh_ctx::kScratchCounterBytes - 64) {
@@ -528,6 +528,17 @@ int qh_attention_splitk_list(qh_ctx* ctx, const float* d_q, const uint16_t* d_ke
                                                   static_cast<float*>(tmp));
   QH_HIP(hipFreeAsync(tmp, ctx->stream));
   QH_HIP(e);
+  return QH_OK;
+}
+
+int qh_attention_list_plan(int32_t context, int32_t count, int32_t kv_heads, int32_t* h_slots,
+                           int32_t* h_waves) {
+  QH_CHECK(context >= 1 && count >= 1 && kv_heads >= 1 && h_slots && h_waves, QH_ERR_INVALID,
+           "list plan needs context, count and kv_heads >= 1 and two outputs");
+  int slots = 0, waves = 0;
+  qh::attention_list_plan(context, count, kv_heads, &slots, &waves);
+  *h_slots = slots;
+  *h_waves = waves;
   return QH_OK;
 }
 

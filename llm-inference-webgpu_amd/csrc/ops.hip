@@ -478,10 +478,20 @@ hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t*
   return hipGetLastError();
 }
 
-size_t attention_partials_floats(int seq, int heads) {
-  return (size_t)seq * heads * kOpSlots * kPartStride;
+// Queries per launch of a long cache's 128 slots: their partials (476 KiB per query at 14
+// heads) are merged into the output before the next group reuses them.
+constexpr int kSplitkQueryGroup = 64;
+
+size_t attention_partials_floats(int seq, int heads, int capacity) {
+  const int rows = decode_attn_long(capacity) ? std::min(seq, kSplitkQueryGroup) : seq;
+  return (size_t)rows * heads * decode_attn_slots(capacity) * kPartStride;
 }
 
+// The decode step's attention (k_attn_gqa: one block per kv head and slot, the GQA group on
+// the f16 matrix cores, so each K/V chunk is read once per kv head), with the slot count the
+// capacity chooses, then the slot merge: k_attn_combine for up to kLongCapacity positions,
+// k_attn_merge_long past it. Every query's blocks do what a one-query launch at the same
+// capacity does, so prefill rows equal decode rows bit for bit.
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
                                    const uint16_t* vt, int capacity, float* out, int seq, int past,
                                    int heads, int kv_heads, float* partials) {
@@ -495,12 +505,22 @@ hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t
   a.vstride = value_stride(capacity);
   a.heads = heads;
   a.kv_heads = kv_heads;
-  a.max_slots = kOpSlots;
-  hipError_t e = launch_attn_slots<kOpSlots>(s, a, seq, 1);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_combine<false>, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
-                     kOpSlots, (size_t)0);
-  return hipGetLastError();
+  if (!decode_attn_long(capacity)) {
+    hipError_t e = launch_attn_decode(s, a, seq, 1);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_combine<true>, dim3(heads, seq), dim3(kWave), 0, s, partials, out, past, heads,
+                       kDecodeSlots, (size_t)0);
+    return hipGetLastError();
+  }
+  for (int t0 = 0; t0 < seq; t0 += kSplitkQueryGroup) {
+    const int n = std::min(kSplitkQueryGroup, seq - t0);
+    SlotArgs b = a;
+    b.q = q + (size_t)t0 * heads * kHeadDim;
+    b.past = past + t0;
+    hipError_t e = launch_attn_decode(s, b, n, 1, out + (size_t)t0 * heads * kHeadDim);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
@@ -538,6 +558,12 @@ static ListPlan list_plan(int ctx, int count, int kv_heads) {
   const int per = (steps + slots - 1) / slots;
   const int waves = per <= 8 ? 1 : per <= 32 ? 4 : 8;
   return {slots, waves};
+}
+
+void attention_list_plan(int ctx, int count, int kv_heads, int* slots, int* waves) {
+  const ListPlan p = list_plan(ctx, count, kv_heads);
+  *slots = p.slots;
+  *waves = p.waves;
 }
 
 size_t attention_list_partials_floats(int count, int heads, int kv_heads, int ctx) {

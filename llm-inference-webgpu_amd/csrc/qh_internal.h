@@ -149,12 +149,12 @@ hipError_t launch_attention_exact(hipStream_t s, const float* q, const uint16_t*
                                   const uint16_t* vt, int capacity, float* out, int seq, int past,
                                   int heads, int kv_heads, float* scores, int* counters);
 size_t attention_exact_floats(int seq, int heads, int past);
-// Split-K attention: slot partials, then a combine launch. `partials` holds
-// attention_partials_floats(seq, heads) floats (no initial contents needed).
+// Split-K attention (the decode step's GQA-group slots, then their merge). `partials` holds
+// attention_partials_floats(seq, heads, capacity) floats (no initial contents needed).
 hipError_t launch_attention_splitk(hipStream_t s, const float* q, const uint16_t* kc,
                                    const uint16_t* vt, int capacity, float* out, int seq, int past,
                                    int heads, int kv_heads, float* partials);
-size_t attention_partials_floats(int seq, int heads);
+size_t attention_partials_floats(int seq, int heads, int capacity);
 // Flash attention on the matrix cores (f16 MFMA, q and p split in two f16 terms).
 hipError_t launch_attention_mfma(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vt,
                                  int capacity, float* out, int seq, int past, int heads, int kv_heads);
@@ -165,6 +165,9 @@ hipError_t launch_attention_splitk_list(hipStream_t s, const float* q, const uin
                                         size_t list_k, size_t list_v, int count, int capacity, float* out,
                                         int past, int heads, int kv_heads, float* partials);
 size_t attention_list_partials_floats(int count, int heads, int kv_heads, int ctx);
+// The list operator's launch shape for a query at position ctx-1 over `count` caches: slots
+// per (cache, kv head) and waves per slot.
+void attention_list_plan(int ctx, int count, int kv_heads, int* slots, int* waves);
 // f64 rope tables for `positions` rows of head_dim/2 angles (src/core/ops.js:99-136).
 void rope_tables_f64(int head_dim, double theta, int positions, double* cos_t, double* sin_t);
 hipError_t launch_swiglu(hipStream_t s, float* gate, const float* up, int n);

@@ -36,10 +36,27 @@ class GpuContext {
   }
 }
 
+// [kvHeads, length, headDim] rows -> position-major [length, kvHeads * headDim]: the layout of
+// the reference's per-layer cache buffers (src/gpu/model.js:69-84, 336-338), which its forward()
+// returns as `present` (src/gpu/model.js:388-395).
+function positionMajor(headMajor, kvHeads, headDim) {
+  const length = headMajor.length / (kvHeads * headDim);
+  const kvDim = kvHeads * headDim;
+  const out = new Float32Array(headMajor.length);
+  for (let h = 0; h < kvHeads; h++) {
+    for (let t = 0; t < length; t++) {
+      const from = (h * length + t) * headDim;
+      out.set(headMajor.subarray(from, from + headDim), t * kvDim + h * headDim);
+    }
+  }
+  return out;
+}
+
 // One layer's keys or values of a cache, standing where the reference keeps a GPUBuffer per
 // layer (src/gpu/model.js:69-84). The device memory belongs to the cache; read() returns the
-// rows 0 .. length-1 as f32 [kv_heads, length, head_dim], and once every layer view of the
-// cache is destroyed, the cache's memory is freed.
+// rows 0 .. length-1 as the reference's buffer holds them, f32 position-major
+// [length, kvHeads * headDim], and once every layer view of the cache is destroyed, the cache's
+// memory is freed.
 class LayerBuffer {
   constructor(cache, layer, kind, byteLength) {
     this.cache = cache;
@@ -48,7 +65,7 @@ class LayerBuffer {
     this.size = byteLength;
     this.destroyed = false;
   }
-  read() { return this.cache.present(this.layer)[this.kind]; }
+  read() { return this.cache.layerRows(this.layer)[this.kind]; }
   destroy() {
     if (this.destroyed) return;
     this.destroyed = true;
@@ -77,8 +94,16 @@ class GpuKVCache {
   get length() { return addon.cacheLength(this.handle); }
   set length(n) { addon.cacheLength(this.handle, n); }
   reset() { this.length = 0; }
-  // {key, value} of one layer, f32 [kv_heads, length, head_dim] (the `present` layout).
+  // {key, value} of one layer, f32 [kv_heads, length, head_dim]: what the CPU cache's present()
+  // returns (src/cpu/cache.js:97-115), the ONNX `present` layout.
   present(layer) { return addon.cachePresent(this.model.handle, this.handle, layer); }
+  // {key, value} of one layer, f32 position-major [length, kv_heads * head_dim]: the reference
+  // GPU cache's rows (src/gpu/model.js:388-395).
+  layerRows(layer) {
+    const p = this.present(layer);
+    const kvHeads = this.model.dims.kvHeads, headDim = this.model.dims.hidden / this.model.dims.heads;
+    return { key: positionMajor(p.key, kvHeads, headDim), value: positionMajor(p.value, kvHeads, headDim) };
+  }
   release() {
     if (--this.live === 0) this.destroy();
   }
@@ -256,8 +281,10 @@ class GpuModel {
 
   // forward(hidden: Float32Array[seq*hidden], seq, {cache, wantLogits = true, wantPresent = false})
   //   -> Promise<{logits, present, hiddenBuffer}> (src/gpu/model.js:227-240, 401). present: per
-  //   layer {key, value} f32 [kv_heads, length, head_dim] after the pass; hiddenBuffer is null
-  //   (the residual rows stay in the library's workspace). One pass at a time.
+  //   layer {key, value} f32 position-major [length, kv_heads * head_dim] after the pass, as the
+  //   reference reads its cache buffers (src/gpu/model.js:388-395; its caller reshapes them,
+  //   web/model.html:49-60); hiddenBuffer is null (the residual rows stay in the library's
+  //   workspace). One pass at a time.
   async forward(hidden, seq, options) {
     if (this.running) throw new Error('forward() is already running; await it first');
     const o = options || {};
@@ -269,7 +296,7 @@ class GpuModel {
       let present = null;
       if (o.wantPresent) {
         present = [];
-        for (let L = 0; L < this.dims.layers; L++) present.push(o.cache.present(L));
+        for (let L = 0; L < this.dims.layers; L++) present.push(o.cache.layerRows(L));
       }
       return { logits: r.logits, present: present, hiddenBuffer: null, argmax: r.argmax };
     } finally {

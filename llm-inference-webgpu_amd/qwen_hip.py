@@ -252,6 +252,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "qh_swiglu": [vp, vp, vp, i32], "qh_add": [vp, vp, vp, i32],
         "qh_matmul_prefill": [vp, vp, vp, vp, vp, i32], "qh_matmul_prefill_noalloc": [vp, vp, vp, vp, vp, i32],
         "qh_attention_splitk_list": [vp, vp, vp, vp, sz, sz, i32, i32, vp, i32, i32, i32, i32],
+        "qh_attention_list_plan": [i32, i32, i32, vp, vp],
         "qh_argmax": [vp, vp, i32, vp],
         "qh_quantize_int8": [vp, i32, i32, vp, vp],
         "qh_quantize_int4": [vp, i32, i32, i32, vp, vp, vp],
@@ -319,6 +320,15 @@ def device_count() -> int:
     n = ctypes.c_int(0)
     _check(load_library().qh_device_count(ctypes.byref(n)))
     return n.value
+
+
+def attention_list_plan(context: int, count: int, kv_heads: int) -> tuple:
+    """(slots, waves) of the launch qh_attention_splitk_list makes for a query at position
+    context-1 over `count` caches (host-only)."""
+    slots, waves = ctypes.c_int32(), ctypes.c_int32()
+    _check(load_library().qh_attention_list_plan(context, count, kv_heads, ctypes.byref(slots),
+                                                 ctypes.byref(waves)))
+    return slots.value, waves.value
 
 
 def quantize_int8(w: np.ndarray):

@@ -4,19 +4,33 @@
 // (src/core/config.js, src/core/safetensors.js: plain properties; async readRaw / readF32),
 // GpuModel.load with quantize = null (f16 weights, the reference's format), host-side
 // embedding, forward() per token with the host argmax scan, wantPresent, and the cache's
-// per-layer keys / values buffers destroyed as the caller destroys them. Prints JSON for
-// tests/test_js_addon.py. Usage: node reference_caller.js
+// per-layer keys / values buffers destroyed as the caller destroys them. Two kv heads, so the
+// position-major `present` rows and web/model.html's reshape of them (toPresentLayout) differ
+// from the head-major layout. Prints JSON for tests/test_js_addon.py. Usage: node reference_caller.js
 const path = require('path');
 const qh = require(path.join(__dirname, '..', '..', 'llm-inference-webgpu_amd', 'js', 'gpu_model.js'));
 const { GpuContext, GpuModel } = qh;
 
 // What the reference's ModelConfig constructor leaves on the object (config.js:16-70).
 const config = {
-  modelType: 'qwen2', architectures: ['Qwen2ForCausalLM'], hiddenSize: 128, intermediateSize: 256, numLayers: 2,
-  numHeads: 2, numKVHeads: 1, vocabSize: 1000, maxPositionEmbeddings: 32768, ropeTheta: 1000000, rmsNormEps: 1e-6,
+  modelType: 'qwen2', architectures: ['Qwen2ForCausalLM'], hiddenSize: 256, intermediateSize: 256, numLayers: 2,
+  numHeads: 4, numKVHeads: 2, vocabSize: 1000, maxPositionEmbeddings: 32768, ropeTheta: 1000000, rmsNormEps: 1e-6,
   hiddenAct: 'silu', tieWordEmbeddings: true, useSlidingWindow: false, slidingWindow: null, bosTokenId: null,
-  eosTokenId: null, headDim: 64, kvGroupSize: 2, kvDim: 64,
+  eosTokenId: null, headDim: 64, kvGroupSize: 2, kvDim: 128,
 };
+
+// web/model.html's reshape of a present row block: [positions, kvHeads*headDim] into the ONNX
+// [kvHeads, positions, headDim] (written here for this test, same index map).
+function toPresentLayout(flat, positions, numKVHeads, headDim) {
+  const kvDim = numKVHeads * headDim;
+  const out = new Float32Array(numKVHeads * positions * headDim);
+  for (let t = 0; t < positions; t++) {
+    for (let h = 0; h < numKVHeads; h++) {
+      for (let i = 0; i < headDim; i++) out[(h * positions + t) * headDim + i] = flat[t * kvDim + h * headDim + i];
+    }
+  }
+  return out;
+}
 
 // A reader with the reference Safetensors' surface over an in-memory bf16 checkpoint; one
 // tensor's bytes come back at an odd offset, as a byte source may return them.
@@ -53,7 +67,7 @@ function referenceReader(ckpt) {
 }
 
 async function main() {
-  const dims = { hidden: 128, intermediate: 256, layers: 2, heads: 2, kvHeads: 1, vocab: 1000 };
+  const dims = { hidden: 256, intermediate: 256, layers: 2, heads: 4, kvHeads: 2, vocab: 1000 };
   const ckpt = qh.synthesizeCheckpoint(dims, 3);
   const st = referenceReader(ckpt);
   const ctx = GpuContext.create(0);
@@ -97,9 +111,16 @@ async function main() {
   const p = model.forward(embed([token]), 1, { cache: cache, wantLogits: false });
   try { await model.forward(embed([token]), 1, { cache: cache }); } catch (e) { busy = e.message; }
   await p;
+  const b64 = function (a) { return Buffer.from(a.buffer, a.byteOffset, a.byteLength).toString('base64'); };
+  const positions = cache.length - 1;
   const present = last.present.map(function (l) {
-    return { key: Buffer.from(l.key.buffer).toString('base64'), value: Buffer.from(l.value.buffer).toString('base64') };
+    return {
+      key: b64(l.key), value: b64(l.value),
+      keyOnnx: b64(toPresentLayout(l.key, positions, config.numKVHeads, config.headDim)),
+      valueOnnx: b64(toPresentLayout(l.value, positions, config.numKVHeads, config.headDim)),
+    };
   });
+  const rowsOk = cache.keys[1].read().length === (cache.length) * config.kvDim;
   let tiledOk = true;
   try { model.setMatmul('tiled'); model.setMatmul('batched'); } catch (e) { tiledOk = e.message; }
   let badMatmul = null;
@@ -107,7 +128,7 @@ async function main() {
   process.stdout.write(JSON.stringify({
     ticks: ticks, layers: layers, warmBytes: warmBytes, freed: freed, tokens: generated,
     firstLogits: Buffer.from(first.logits.buffer).toString('base64'), hiddenBuffer: first.hiddenBuffer,
-    present: present, presentLength: cache.length - 1, cacheLength: cache.length, busy: busy,
+    present: present, presentLength: positions, cacheLength: cache.length, busy: busy, rowsOk: rowsOk,
     tiles: [1, 2, 3, 4, 7, 8, 512].map(GpuModel.batchTileFor), tiled: tiledOk, badMatmul: badMatmul,
   }) + '\n');
   cache.destroy();

@@ -29,6 +29,21 @@ def test_library_exports_every_declared_symbol(hip):
     assert lib.qh_abi_version() == 1
 
 
+# (context, caches) -> (slots, waves) of the list launch: the four config-3 shapes the bench
+# times, the list lengths the GPU parity test uses for them, and short lists.
+LIST_PLANS = [((128, 8192), (1, 1)), ((1024, 1024), (1, 4)), ((4096, 256), (1, 8)), ((32768, 32), (4, 8)),
+              ((128, 128), (1, 1)), ((1024, 128), (1, 4)), ((4096, 128), (1, 8)), ((1000, 128), (1, 4)),
+              ((4000, 128), (1, 8)), ((1, 5), (4, 1)), ((100, 5), (4, 1)), ((1000, 5), (64, 1)),
+              ((5000, 5), (64, 1))]
+
+
+@pytest.mark.parametrize("shape,plan", LIST_PLANS)
+def test_attention_list_plan(hip, shape, plan):
+    assert hip.attention_list_plan(shape[0], shape[1], 2) == plan
+    with pytest.raises(hip.QwenHipError):
+        hip.attention_list_plan(0, shape[1], 2)
+
+
 def test_no_device_is_an_error_not_a_fallback(hip):
     if hip.device_count() > 0:
         pytest.skip("a device is present")

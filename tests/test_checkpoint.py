@@ -88,6 +88,9 @@ def raw_file(path, header, data=b"", header_len=None):
     ({"a": {"dtype": "F32", "shape": [2], "data_offsets": [0, 8]},
       "b": {"dtype": "F32", "shape": [1], "data_offsets": [4, 8]}}, b"\0" * 8, None,
      r"'b' \[4, 8\) overlaps 'a' \[0, 8\)"),
+    # a shape whose element count wraps to 0 in 64-bit arithmetic is still 2**64 elements
+    ({"t": {"dtype": "F32", "shape": [2 ** 32, 2 ** 32], "data_offsets": [0, 0]}}, b"", None,
+     "18446744073709551616 x F32 is 73786976294838206464 bytes, the record spans 0"),
     ({"t": 7}, b"", None, "the record is a JSON int"),
     ({"__metadata__": {"k": 1}}, b"", None, "__metadata__ is not an object of strings"),
 ])

@@ -358,6 +358,45 @@ def test_attention_list_matches_single_calls(ctx, hip, ctx_len):
     free(dk, dv, dq, dout)
 
 
+# Config 3's timed (context, list length) shapes -- the list lengths are the smallest that
+# keep the bench's launch shape -- and two ragged contexts: (slots, waves) per (cache, kv head).
+# With one slot the block writes the output itself; with four the slots are merged by a launch
+# of their own.
+TIMED_LIST_PLANS = [(128, 128, (1, 1)), (1024, 128, (1, 4)), (4096, 128, (1, 8)), (32768, 32, (4, 8)),
+                    (1000, 128, (1, 4)), (4000, 128, (1, 8))]
+
+
+@pytest.mark.parametrize("ctx_len,count,plan", TIMED_LIST_PLANS)
+def test_attention_list_timed_plans_match_oracle(ctx, hip, ctx_len, count, plan):
+    """The launch shapes config 3 times: every cache of the list gets the oracle's grouped
+    attention within the kernel tolerance (a sample of five caches is checked against the
+    oracle, each distinct, and every output is finite)."""
+    heads, kv_heads, cap = 14, 2, ctx_len
+    assert hip.attention_list_plan(ctx_len, count, kv_heads) == plan
+    vstride = hip.value_cache_bytes(cap, kv_heads) // (kv_heads * 64 * 2)
+    rng = np.random.default_rng(ctx_len * 7 + count)
+    kel, vel = kv_heads * cap * 64, kv_heads * 64 * vstride
+    keys = rng.standard_normal(count * kel, dtype=np.float32).astype(np.float16).view(np.uint16)
+    vals = rng.standard_normal(count * vel, dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(heads * 64).astype(np.float32)
+    print(f"list ctx {ctx_len} count {count} plan {plan}", flush=True)
+    dk, dv, dq, dout = ctx.upload(keys), ctx.upload(vals), ctx.upload(q), ctx.empty(count * heads * 64 * 4)
+    ctx.attention_list(dq, dk, dv, kel, vel, count, cap, dout, ctx_len - 1, heads, kv_heads)
+    got = dout.read(count=count * heads * 64).reshape(count, heads * 64)
+    assert np.all(np.isfinite(got))
+    sample = sorted({0, 1, count // 2, int(rng.integers(2, count - 1)), count - 1})
+    for i in sample:
+        kr = O.f16_to_f32(keys[i * kel:(i + 1) * kel]).reshape(kv_heads, cap, 64)
+        vr = O.f16_to_f32(vals[i * vel:(i + 1) * vel]).reshape(kv_heads, 64, vstride)[:, :, :ctx_len]
+        K = np.ascontiguousarray(kr.transpose(1, 0, 2).reshape(ctx_len, -1))
+        V = np.ascontiguousarray(vr.transpose(2, 0, 1).reshape(ctx_len, -1))
+        ref = O.grouped_attention(q, K, V, 1, ctx_len - 1, heads, kv_heads, 64)
+        err = rel_err(got[i], ref)
+        print(f"  cache {i}: rel {err:.2e}", flush=True)
+        assert err <= KERNEL_REL
+    free(dk, dv, dq, dout)
+
+
 @pytest.mark.parametrize("kind", KINDS)
 def test_decode_attention_32k(ctx, hip, kind):
     ctx_len, heads, kv_heads = 32768, 14, 2

@@ -133,15 +133,18 @@ def test_js_driver_matches_python_binding(addon_built, ctx, hip, scheme, numeric
 @pytest.mark.gpu
 def test_reference_shaped_caller_drives_the_backend(addon_built, ctx, hip):
     """web/bench.html's loop over objects shaped exactly like the reference's ModelConfig and
-    Safetensors (async readRaw, one tensor at an odd offset), f16 weights (quantize = null):
-    the logits equal the Python binding's bit for bit, the greedy tokens and the `present`
-    rows too; cache.keys / values destroy the cache once all are destroyed; a second forward
-    while one is pending is refused; batchTileFor and matmul 'tiled' are the reference's."""
+    Safetensors (async readRaw, one tensor at an odd offset), f16 weights (quantize = null),
+    two kv heads: the logits equal the Python binding's bit for bit, the greedy tokens too;
+    `present` comes back position-major [length, kv_dim] as the reference GPU forward returns
+    it (src/gpu/model.js:388-395), and web/model.html's reshape of it (toPresentLayout) gives
+    the head-major present rows; cache.keys / values destroy the cache once all are
+    destroyed; a second forward while one is pending is refused; batchTileFor and matmul
+    'tiled' are the reference's."""
     r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "reference_caller.js")],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr
     js = json.loads(r.stdout)
-    cfg = hip.ModelConfig(hidden=128, intermediate=256, layers=2, heads=2, kv_heads=1, vocab=1000)
+    cfg = hip.ModelConfig(hidden=256, intermediate=256, layers=2, heads=4, kv_heads=2, vocab=1000)
     ckpt = hip.synthesize_checkpoint(cfg, seed=3)
     model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "f16", 128, "f16"), cfg, maxPositions=64)
     prompt = hip.synth_tokens(3, "prompt", cfg.vocab, 12)
@@ -153,10 +156,14 @@ def test_reference_shaped_caller_drives_the_backend(addon_built, ctx, hip):
     assert js["tokens"] == [out["argmax"]] + list(gen)
     assert cache.length == js["presentLength"] == 18
     for L in range(cfg.layers):
-        pres = cache.present(L)
+        pres = cache.present(L)   # [kv_heads, length, head_dim]
         for kind in ("key", "value"):
-            got = np.frombuffer(base64.b64decode(js["present"][L][kind]), np.float32)
-            np.testing.assert_array_equal(got, pres[kind].ravel())
+            rows = np.frombuffer(base64.b64decode(js["present"][L][kind]), np.float32)
+            onnx = np.frombuffer(base64.b64decode(js["present"][L][kind + "Onnx"]), np.float32)
+            np.testing.assert_array_equal(rows.reshape(18, 128), pres[kind].transpose(1, 0, 2).reshape(18, 128))
+            np.testing.assert_array_equal(onnx, pres[kind].ravel())
+            assert not np.array_equal(rows, onnx)
+    assert js["rowsOk"] is True
     assert js["ticks"] == 26 and js["layers"] == 2 and js["warmBytes"] > 0 and js["freed"] is True
     assert js["hiddenBuffer"] is None and "already running" in js["busy"] and js["cacheLength"] == 19
     assert js["tiles"] == [1, 2, 2, 4, 4, 8, 8] and js["tiled"] is True and "matmul must be" in js["badMatmul"]

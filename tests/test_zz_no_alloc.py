@@ -2,10 +2,33 @@
 through the C ABI: the same kernels on the same inputs, so the outputs must be equal bit for bit.
 Two calls in a row on one context, the second smaller than the first (the shared static scratch
 keeps the first call's contents), then a call whose scratch would not fit is refused."""
+import ctypes
+
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+
+
+def _hip_runtime():
+    """The HIP runtime the library links (already loaded in this process)."""
+    rt = ctypes.CDLL("libamdhip64.so")
+    vp, pvp = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+    rt.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
+    rt.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    rt.hipStreamEndCapture.argtypes = [vp, pvp]
+    rt.hipGraphInstantiate.argtypes = [pvp, vp, vp, vp, ctypes.c_size_t]
+    rt.hipGraphLaunch.argtypes = [vp, vp]
+    rt.hipStreamSynchronize.argtypes = [vp]
+    rt.hipGraphExecDestroy.argtypes = [vp]
+    rt.hipGraphDestroy.argtypes = [vp]
+    return rt
+
+
+def _free_bytes(rt):
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert rt.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
 
 
 def _weights(hip, ctx, fmt, rows, cols, seed):
@@ -50,4 +73,49 @@ def test_noalloc_prefill_refuses_shapes_beyond_its_scratch(ctx, hip):
         ctx.matmul_prefill_noalloc(W, x, None, y, 4096)      # 4096 x 8192 digit planes: 96 MiB
     ctx.matmul_prefill_noalloc(W, x, None, y, 16)            # a fitting call still works after it
     for b in bufs + [x, y]:
+        b.free()
+
+
+def test_noalloc_prefill_allocates_nothing(ctx, hip):
+    """Warm calls leave the device's free memory where it was, and the call records into a
+    global-mode stream capture, in which the runtime refuses device allocation: the capture
+    ends cleanly, and its graph, replayed three times with eager work between the replays,
+    gives the eager call's bits every time."""
+    rt = _hip_runtime()
+    M, rows, cols = 128, 896, 4864
+    print(f"noalloc capture: int8 {rows}x{cols}, M={M}", flush=True)
+    W, bufs = _weights(hip, ctx, "int8", rows, cols, seed=5)
+    x = ctx.upload(np.random.default_rng(6).standard_normal((M, cols)).astype(np.float32))
+    y_eager, y_graph = ctx.empty(M * rows * 4), ctx.empty(M * rows * 4)
+    ctx.matmul_prefill_noalloc(W, x, None, y_eager, M)   # first call: code and scratch address resolved
+    ctx.done()
+    before = _free_bytes(rt)
+    for _ in range(3):
+        ctx.matmul_prefill_noalloc(W, x, None, y_eager, M)
+    ctx.done()
+    assert _free_bytes(rt) == before
+    eager = y_eager.read()
+    assert np.isfinite(eager).all()
+
+    stream = ctypes.c_void_p(ctx.stream)
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamBeginCapture(stream, 0) == 0      # hipStreamCaptureModeGlobal
+    try:
+        ctx.matmul_prefill_noalloc(W, x, None, y_graph, M)
+    finally:
+        ended = rt.hipStreamEndCapture(stream, ctypes.byref(graph))
+    assert ended == 0 and graph.value
+    assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+    try:
+        for rep in range(3):
+            ctx.matmul_prefill(W, x, None, y_graph, 7)       # eager work on the same stream between replays
+            ctx.done()
+            assert rt.hipGraphLaunch(exe, stream) == 0
+            assert rt.hipStreamSynchronize(stream) == 0
+            got = y_graph.read()
+            np.testing.assert_array_equal(got.view(np.uint32), eager.view(np.uint32), err_msg=f"replay {rep}")
+    finally:
+        rt.hipGraphExecDestroy(exe)
+        rt.hipGraphDestroy(graph)
+    for b in bufs + [x, y_eager, y_graph]:
         b.free()
