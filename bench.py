@@ -10,10 +10,12 @@ steps run and are rewound; then exactly K steps are timed with HIP events on the
 library's stream (and wall clock around them), inputs resident in HBM.
 
 Also reported on the same JSON line:
-  roofline       the dominant kernel of the step (by in-situ time), algorithmic
-                 bytes per launch over its average in-situ launch time, vs 8 TB/s
+  roofline       the dominant kernel of the step (the most in-situ time per token),
+                 algorithmic bytes per launch over its back-to-back launch duration, vs
+                 8 TB/s; the same figures for every role under "roles"
   per_kernel_us  in-situ microseconds per token by kernel role (events around
-                 every launch, the reference's decode-profile split)
+                 every launch, the reference's decode-profile split), and each role's
+                 launch duration back to back
   decode_bounds  what bounds the step on this device: the pure streaming-read ceiling, and
                  the cost of a graph-replayed launch that reads its predecessor's output (as
                  every decode launch does) times the step's launches
@@ -821,19 +823,28 @@ def main():
     for r in per_kernel:
         if r in back_to_back:
             per_kernel[r]["us_back_to_back"] = back_to_back[r]
-    # The dominant kernel: the most time per token by its back-to-back duration (launches per
-    # token x duration); the event-timed split above adds an event before every launch, which
-    # makes roles within a few % of each other (the attention and gate/up) trade places.
-    dominant = max((r for r in per_kernel if r in back_to_back),
-                   key=lambda r: per_kernel[r]["launches_per_token"] * back_to_back[r])
-    # The dominant kernel's own duration is its back-to-back launch time.
-    kernel_us = per_kernel[dominant]["us_back_to_back"]
-    kbytes = role_bytes(cfg, probe)[dominant]
-    achieved = kbytes / (kernel_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1),
-                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                "traffic": measured_traffic(dominant, args.context), "bytes_per_launch": kbytes,
-                "us_per_launch": round(kernel_us, 3)}
+    # Every role's roofline figure: algorithmic bytes per launch at the probe position over the
+    # role's back-to-back launch duration (240 of the step's own launches between two events, so
+    # no event sits between them; a kernel tracer's average over the same launches agrees within
+    # ~10%). The dominant kernel is the role with the most in-situ time per token (the event split
+    # above), which ranks the roles as a kernel trace of the step does; back-to-back durations of
+    # the attention, gate/up and down lie within a few % of each other and would trade places
+    # from run to run.
+    pb = role_bytes(cfg, probe)
+    roles_roof = {}
+    for r in ("qkv", "attention", "oproj", "gateup", "down", "head"):
+        if r not in per_kernel:
+            continue
+        us = back_to_back[r]
+        gbs = pb[r] / (us * 1e-6) / 1e9
+        roles_roof[r] = {"us_per_launch": us, "in_situ_us_per_token": per_kernel[r]["us_per_token"],
+                         "bytes_per_launch": pb[r], "achieved": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    dominant = max(roles_roof, key=lambda r: roles_roof[r]["in_situ_us_per_token"])
+    d = roles_roof[dominant]
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": d["achieved"],
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": d["frac"],
+                "traffic": measured_traffic(dominant, args.context), "bytes_per_launch": d["bytes_per_launch"],
+                "us_per_launch": d["us_per_launch"], "roles": roles_roof}
     log(f"per-kernel: {json.dumps(per_kernel)}")
 
     # What bounds the step; the cold launches against the read ceiling.

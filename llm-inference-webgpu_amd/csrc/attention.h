@@ -23,17 +23,14 @@
 // result matches the CPU to the bit apart from f64-order noise, so a device f16
 // cache and the CPU's same-f16 cache stay identical.
 //
-// Split-K online softmax (k_attn_slots + a combine), qh_attention_splitk: one
-// wave per (query, head, run of 64-position chunks), partials merged afterwards.
-// Exact to f32 rounding, not to the CPU's order; checked within the kernel
-// tolerance.
-//
-// The same split-K slots with the GQA group on the matrix cores (k_attn_gqa), the
-// decode step's and batched prefill's path (QH_NUMERICS_FAST) and the list
-// operator's: one block per (query, kv head, run of chunks), the group's query
-// heads as the columns of f16 MFMA products, so each K/V chunk is read once per kv
-// head. q and p go in as two f16 terms each (~1e-6 of the output). A flash form of
-// the same products (k_flash_prefill) serves the MFMA prompt path.
+// Split-K online softmax with the GQA group on the matrix cores (k_attn_gqa): the
+// decode step's and batched prefill's path (QH_NUMERICS_FAST), qh_attention_splitk's
+// and the list operator's: one block per (query, kv head, run of 64-position
+// chunks), the group's query heads as the columns of f16 MFMA products, so each K/V
+// chunk is read once per kv head; the runs' partials are merged afterwards. q and p
+// go in as two f16 terms each (~1e-6 of the output): exact to f32 rounding, not to
+// the CPU's order, and checked within the kernel tolerance. A flash form of the same
+// products (k_flash_prefill) serves the MFMA prompt path.
 #pragma once
 
 #include "device_common.h"
@@ -376,22 +373,18 @@ static __global__ __launch_bounds__(kBlock) void k_attn_exact(ExactArgs a) {
 }
 
 // -------------------------------------------------------------- split-K --
-// Split-K online softmax (the decode path's attention, and qh_attention_splitk).
-// The context is cut into 64-position chunks; a "slot" is every S-th chunk, and
-// one wave owns one (query, head, slot): lane p scores position p of
-// a chunk against the head's query (q as wave-uniform scalars, keys as f16 via
-// v_fma_mix), the wave keeps the running max m and sum l over its slot, and lane
-// d accumulates output dimension d over the chunk's positions with the chunk's
-// probabilities read lane by lane. The slot's partial (m, l, o[64]) goes to
-// `part`; a combine (k_attn_combine, or the decode o-projection's staging)
-// merges the slots of a head:
-//   M = max_s m_s,  L = sum_s l_s e^(m_s - M),  out = sum_s o_s e^(m_s - M) / L.
-// f32 throughout; agrees with groupedAttention (src/core/attention.js:32-66) to
-// f32 rounding. The chunks of a slot depend on the query's own context only, so
-// a prefill row and the same position decoded alone give the same bits.
+// Split-K online softmax. The context is cut into 64-position chunks; a "slot"
+// (run) is every S-th chunk of a query's context. A slot's partial state (m, l,
+// o[64]) per query head goes to `part`; a merge (k_attn_combine, k_attn_merge_long,
+// or the decode o-projection's staging) combines the slots of a head:
+//   M = max_s m_s,  L = sum_s l_s 2^(m_s - M),  out = sum_s o_s 2^(m_s - M) / L
+// (maxima in base-2 units). f32 throughout; agrees with groupedAttention
+// (src/core/attention.js:32-66) to f32 rounding. The chunks of a slot depend on the
+// query's own context only, so a prefill row and the same position decoded alone
+// give the same bits.
 constexpr int kPartStride = 68;   // floats per slot partial: m, l, 2 pad, o[64]
 constexpr int kDecodeSlots = 16;  // slots per head in the decode step (combined in staging)
-constexpr int kOpSlots = 64;      // slots per head in the standalone operator
+constexpr int kOpSlots = 64;      // most slots per head of the list operator
 
 __host__ __device__ inline int attn_chunks(int ctx) { return (ctx + kChunk - 1) / kChunk; }
 
@@ -431,165 +424,6 @@ __device__ __forceinline__ float team_max(float v) {
   if constexpr (TL >= 32) v = fmaxf(v, swz_xor16(v));
   if constexpr (TL >= 64) v = fmaxf(v, __shfl_xor(v, 32));
   return v;
-}
-
-// Loads chunk `c`: key row p0+lane and, for lane d, values of dimension d at
-// positions p0 .. p0+63 as eight 16-byte groups. Every load is unconditional and
-// in bounds -- rows past `lim` (the cache capacity) read row lim-1, groups past
-// it the group holding lim-1 (vstride >= lim rounded up to 64) -- so no load waits
-// on a branch; the caller masks what lies past the context.
-__device__ __forceinline__ void slot_load(const uint16_t* kb, const uint16_t* vrow, int c, int lim,
-                                          int lane, v4u (&kr)[8], v4u (&vr)[8]) {
-  const int p0 = c * kChunk;
-  const int p = min(p0 + lane, lim - 1);
-  const v4u* kp = reinterpret_cast<const v4u*>(kb + (size_t)p * kHeadDim);
-#pragma unroll
-  for (int j = 0; j < 8; j++) kr[j] = kp[j];
-  const int last = (lim - 1) & ~7;
-#pragma unroll
-  for (int j = 0; j < 8; j++) vr[j] = *reinterpret_cast<const v4u*>(vrow + min(p0 + 8 * j, last));
-}
-
-// One chunk of positions p0 .. p0+63 of a slot: scores (lane = position), the
-// online-softmax update of (m, l, o), and o += p * v over the chunk (lane =
-// output dimension, probabilities broadcast through the wave's LDS row `eb`).
-__device__ __forceinline__ void slot_chunk(const v4f (&q4)[kHeadDim / 4], const v4u (&kr)[8], v4u (&vr)[8],
-                                           int p0, int ctx, int lane, float* eb, float& m, float& l,
-                                           float& o) {
-  float dot = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const uint32_t u[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      dot = fmaf(q4[2 * j + e / 2][2 * (e % 2)], f16_lo(u[e]), dot);
-      dot = fmaf(q4[2 * j + e / 2][2 * (e % 2) + 1], f16_hi(u[e]), dot);
-    }
-  }
-  const bool valid = p0 + lane < ctx;
-  const float sc = valid ? dot * 0.125f : -INFINITY;  // scale 1/sqrt(64)
-  const float mn = fmaxf(m, team_max<64>(sc));
-  const float ex = valid ? expf(sc - mn) : 0.f;
-  const float alpha = expf(m - mn);  // 0 on the first chunk (m = -inf)
-  l = l * alpha + team_sum<64>(ex);
-  o *= alpha;
-  if (ctx - p0 < kChunk) {
-    // tail chunk: values past the context are not this chunk's (their weight is 0)
-    const int n = ctx - p0;
-#pragma unroll
-    for (int j = 0; j < 8; j++) {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int q0 = 8 * j + 2 * e;
-        uint32_t w = vr[j][e];
-        if (q0 >= n) w = 0;
-        else if (q0 + 1 >= n) w &= 0xffffu;
-        vr[j][e] = w;
-      }
-    }
-  }
-  // LDS operations of one wave complete in order: no block barrier is needed.
-  eb[lane] = ex;
-  __builtin_amdgcn_wave_barrier();
-  const v4f* e4 = reinterpret_cast<const v4f*>(eb);
-#pragma unroll
-  for (int j = 0; j < 8; j++) o = pv8(e4[2 * j], e4[2 * j + 1], vr[j], o);
-  __builtin_amdgcn_wave_barrier();
-  m = mn;
-}
-
-// One wave per block: a slot's loads (the query, 64 key rows, 64 value runs) are
-// all issued up front, and with one wave per CU they are not queued behind three
-// other waves' in the CU's load pipeline. grid (heads * MAXS, seq, list entries).
-//
-// Block order is XCD-aware: workgroups are dealt to the 8 XCDs round-robin (block b
-// to XCD b % 8), and the query heads of a GQA group read the same key/value chunk,
-// so the blocks of one (kv head, slot) -- one per query head of the group -- take
-// indices congruent mod 8 and share that XCD's L2 instead of fetching the chunk
-// once per XCD. Any other dealing only costs traffic: the map is a bijection.
-template <int MAXS>
-__device__ __forceinline__ void slot_of_block(int b, int heads, int kv_heads, int& h, int& sl) {
-  const int pairs = kv_heads * MAXS, group = heads / kv_heads;
-  if (pairs % 8 == 0) {
-    const int x = b & 7, j = b >> 3;
-    const int p = (j / group) * 8 + x;  // (kv head, slot) pair, XCD x
-    h = (p / MAXS) * group + j % group;
-    sl = p % MAXS;
-  } else {
-    h = b / MAXS;
-    sl = b % MAXS;
-  }
-}
-
-template <int MAXS>
-static __global__ __launch_bounds__(kWave) void k_attn_slots(SlotArgs a) {
-  __shared__ __attribute__((aligned(16))) float eb[kChunk];
-  const int lane = threadIdx.x;
-  const int t = blockIdx.y;
-  int h, sl;
-  slot_of_block<MAXS>(blockIdx.x, a.heads, a.kv_heads, h, sl);
-  if (h >= a.heads) return;
-  const int g = h / (a.heads / a.kv_heads);
-  const size_t z = blockIdx.z;
-
-  // Everything that does not depend on the position first: the head's query in
-  // VGPRs (a per-lane address keeps the compiler from holding 64 values in scalar
-  // registers) and the slot's first chunk.
-  int zero = 0;
-  asm volatile("" : "+v"(zero));
-  const v4f* qp = reinterpret_cast<const v4f*>(a.q + ((size_t)t * a.heads + h) * kHeadDim + zero);
-  v4f q4[kHeadDim / 4];
-#pragma unroll
-  for (int i = 0; i < kHeadDim / 4; i++) q4[i] = qp[i];
-  const uint16_t* kb = a.kc + z * a.list_k + (size_t)g * a.capacity * kHeadDim;
-  const uint16_t* vrow = a.vt + z * a.list_v + ((size_t)g * kHeadDim + lane) * a.vstride;
-  v4u ka[8], va[8], kb2[8], vb2[8];
-  slot_load(kb, vrow, sl, a.capacity, lane, ka, va);
-
-  const int past = a.d_pos ? *a.d_pos : a.past;
-  const int pos = past + t;
-  if (pos >= a.capacity) return;  // the host keeps positions inside the cache
-  const int ctx = pos + 1;
-  const int nch = attn_chunks(ctx);
-  float m = -INFINITY, l = 0.f, o = 0.f;
-  // This slot's chunks: sl, sl + MAXS, ... below nch (uniform over the wave). Each
-  // next chunk is loaded into the other named buffer before the current one is
-  // summed, so its loads stay in flight (no register copies wait on them); the
-  // last chunk is summed with no load behind it, so the wave ends on its own data.
-  int left = sl < nch ? (nch - 1 - sl) / MAXS + 1 : 0;
-  int c = sl;
-  while (left > 0) {
-    if (left == 1) {
-      slot_chunk(q4, ka, va, c * kChunk, ctx, lane, eb, m, l, o);
-      break;
-    }
-    slot_load(kb, vrow, c + MAXS, a.capacity, lane, kb2, vb2);
-    __builtin_amdgcn_sched_barrier(0);  // issue the next chunk's loads before this one's arithmetic
-    slot_chunk(q4, ka, va, c * kChunk, ctx, lane, eb, m, l, o);
-    c += MAXS;
-    if (--left == 1) {
-      slot_chunk(q4, kb2, vb2, c * kChunk, ctx, lane, eb, m, l, o);
-      break;
-    }
-    slot_load(kb, vrow, c + MAXS, a.capacity, lane, ka, va);
-    __builtin_amdgcn_sched_barrier(0);
-    slot_chunk(q4, kb2, vb2, c * kChunk, ctx, lane, eb, m, l, o);
-    c += MAXS;
-    --left;
-  }
-  float* dst = a.part + z * a.list_part + (((size_t)t * a.heads + h) * MAXS + sl) * kPartStride;
-  dst[4 + lane] = o;
-  if (lane == 0) {
-    dst[0] = m;
-    dst[1] = l;
-  }
-}
-
-// k_attn_slots over `seq` queries (grid.y) and `count` list entries (grid.z).
-template <int MAXS>
-static hipError_t launch_attn_slots(hipStream_t s, const SlotArgs& a, int seq, int count) {
-  hipLaunchKernelGGL(k_attn_slots<MAXS>, dim3(a.heads * MAXS, seq, count), dim3(kWave), 0, s, a);
-  return hipGetLastError();
 }
 
 // ------------------------------------------------ prefill on the matrix cores --
@@ -866,14 +700,14 @@ static inline hipError_t launch_flash_prefill(hipStream_t s, FlashArgs a) {
 }
 
 // --------------------------------------- GQA group per slot on the matrix cores --
-// The split-K slots of k_attn_slots with a whole GQA group per block: the group's query
+// The split-K slots with a whole GQA group per block: the group's query
 // heads are the columns of the MFMA products of the flash kernel above (heads/kv_heads
 // of the 16 used, the rest repeat head 0 and are dropped), so each key/value position
 // is read once for the group instead of once per query head. A slot's chunks are
 // walked in steps of 32 keys -- S^T for 2 tiles of 16 keys (8 MFMAs), the online
 // softmax per head column, O^T += V^T P^T (8 MFMAs). Writes (m, l, o) slot partials in
-// the layout of k_attn_slots, with the maxima in base-2 units (merged by CombineIn in
-// the decode step, k_attn_combine<true> for the list operator). q and p are split into
+// the layout above, with the maxima in base-2 units (merged by CombineIn in
+// the decode step, k_attn_combine<true> for the operators). q and p are split into
 // two f16 terms as in the flash kernel (~1e-6 of the output).
 // Step i of slot sl: 32 keys starting at p0 (chunk sl + (i/2)*MAXS, half i%2).
 template <int MAXS>
@@ -881,9 +715,9 @@ __device__ __forceinline__ int gqa_p0(int sl, int i) {
   return (sl + (i >> 1) * MAXS) * kChunk + (i & 1) * 32;
 }
 
-// grid (kv_heads * MAXS, queries, list entries), W waves per block; SlotArgs as for
-// k_attn_slots. Block (kv head, slot) walks the slot's steps with step i on wave i % W
-// (each wave with the next step's loads in flight), and the waves' (m, l, o) states merge
+// grid (kv_heads * MAXS, queries, list entries), W waves per block. Block (kv head,
+// slot) walks the slot's steps with step i on wave i % W (each wave with the next
+// step's loads in flight), and the waves' (m, l, o) states merge
 // through LDS in wave order, as in k_flash_prefill; the merged state is the slot's
 // partial. Query t (blockIdx.y) is at position past + t, and its blocks do exactly what a
 // launch for that query alone does, so a batch of queries gets the bits of one-query
