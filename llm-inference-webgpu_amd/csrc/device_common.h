@@ -37,10 +37,12 @@ constexpr int kBlock = 256;
 // Butterflies inside a team of TL lanes (TL = 16, 32 or 64): steps of 1, 2, 4
 // and 8 lanes on DPP (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
 // row_half_mirror, row_mirror), 16 on ds_swizzle, 32 on a bpermute. Each step
-// adds a symmetric pair, so every lane ends with the same bits.
+// adds a symmetric pair, so every lane ends with the same bits. These patterns only
+// read lanes of the same row, so bound_ctrl (zero for a missing source lane) never
+// applies; set, it lets the compiler fold the move into the add (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp32(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
 }
 template <int CTRL>
 __device__ __forceinline__ double dpp64(double v) {
