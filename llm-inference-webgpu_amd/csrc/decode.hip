@@ -65,24 +65,31 @@ struct FusedArgs {
   size_t list_w, list_s, list_out, list_part;
 };
 
-// Rows of work item `it`. QKV: a rope pair (j, j+32) of a q or k head, or two
-// consecutive v rows. SWIGLU: gate row and up row (2j, 2j+1). Otherwise R
-// consecutive rows, clamped to the matrix.
+// Rows of work item `it`. QKV: R/2 consecutive rope pairs (j, j+32) of one q or k
+// head, or R consecutive v rows. SWIGLU: gate and up rows (2j, 2j+1) pairwise.
+// Otherwise R consecutive rows, clamped to the matrix.
+template <int R>
+__device__ __forceinline__ int qkv_rope_items(const FusedArgs& a) {
+  return (a.heads + a.kv_heads) * 32 / (R / 2);
+}
 template <int EPI, int R>
 __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows)[R]) {
   if constexpr (EPI == EPI_QKV) {
-    static_assert(R == 2, "qkv items are row pairs");
+    static_assert(R == 2 || R == 4, "qkv items are one or two rope pairs");
+    constexpr int P = R / 2;  // divides 32, so an item's pairs share one head
     const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
-    const int rope_pairs = (a.heads + a.kv_heads) * 32;
-    if (it < rope_pairs) {
-      const int head = it / 32, j = it % 32;  // heads 0..heads-1 are q, then k heads
+    if (it < qkv_rope_items<R>(a)) {
+      const int head = it * P / 32, j = it * P % 32;  // heads 0..heads-1 are q, then k heads
       const int base = head < a.heads ? head * kHeadDim : hidden + (head - a.heads) * kHeadDim;
-      rows[0] = base + j;
-      rows[1] = base + j + 32;
+#pragma unroll
+      for (int k = 0; k < P; k++) {
+        rows[2 * k] = base + j + k;
+        rows[2 * k + 1] = base + j + k + 32;
+      }
     } else {
-      const int v = it - rope_pairs;
-      rows[0] = hidden + kvd + 2 * v;
-      rows[1] = hidden + kvd + 2 * v + 1;
+      const int v = it - qkv_rope_items<R>(a);
+#pragma unroll
+      for (int i = 0; i < R; i++) rows[i] = hidden + kvd + R * v + i;
     }
   } else {
 #pragma unroll
@@ -91,12 +98,13 @@ __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows
 }
 
 // Operands of an item's epilogue that do not depend on its sums, loaded with its
-// weights: QKV the two rows' biases and the rope angle of the pair at the current
+// weights: QKV the rows' biases and the rope angles of its pairs at the current
 // position; RESIDUAL the rows' residual inputs.
 template <int EPI, int R>
 struct EpiIn {
-  float bias[2];
-  double cs, sn;
+  static constexpr int kPairs = R / 2 > 0 ? R / 2 : 1;
+  float bias[R];
+  double cs[kPairs], sn[kPairs];
   float res[R];
 };
 
@@ -104,11 +112,14 @@ template <int EPI, int R>
 __device__ __forceinline__ void epi_load(const FusedArgs& a, int it, int pos, const int (&rows)[R],
                                          EpiIn<EPI, R>& e) {
   if constexpr (EPI == EPI_QKV) {
-    e.bias[0] = a.bias[rows[0]];
-    e.bias[1] = a.bias[rows[1]];
-    const int j = it & 31;  // the rope pair of a q/k item (unused by v items)
-    e.cs = a.rope_cos[(size_t)pos * 32 + j];
-    e.sn = a.rope_sin[(size_t)pos * 32 + j];
+#pragma unroll
+    for (int i = 0; i < R; i++) e.bias[i] = a.bias[rows[i]];
+    const int j = it * (R / 2) & 31;  // the first rope pair of a q/k item (unused by v items)
+#pragma unroll
+    for (int k = 0; k < R / 2; k++) {
+      e.cs[k] = a.rope_cos[(size_t)pos * 32 + j + k];
+      e.sn[k] = a.rope_sin[(size_t)pos * 32 + j + k];
+    }
   }
   if constexpr (EPI == EPI_RESIDUAL) {
 #pragma unroll
@@ -125,28 +136,33 @@ __device__ __forceinline__ void epilogue(const FusedArgs& a, int it, int pos, co
   constexpr bool kF32 = std::is_same<Acc, float>::value;
   if constexpr (EPI == EPI_QKV) {
     // q/k/v = f32(sum + bias) (the bias is where the CPU's f64 sum starts; f32: one add).
-    const float v0 = kF32 ? __fadd_rn((float)acc[0], e.bias[0]) : (float)((double)acc[0] + (double)e.bias[0]);
-    const float v1 = kF32 ? __fadd_rn((float)acc[1], e.bias[1]) : (float)((double)acc[1] + (double)e.bias[1]);
+    float v[R];
+#pragma unroll
+    for (int i = 0; i < R; i++)
+      v[i] = kF32 ? __fadd_rn((float)acc[i], e.bias[i]) : (float)((double)acc[i] + (double)e.bias[i]);
     const int hidden = a.heads * kHeadDim, kvd = a.kv_heads * kHeadDim;
-    const int rope_pairs = (a.heads + a.kv_heads) * 32;
     if (pos >= a.capacity) return;  // the host keeps positions inside the cache
-    if (it < rope_pairs) {
-      const int head = it / 32, j = it % 32;
-      float lo, hi;
-      rope_pair(v0, v1, e.cs, e.sn, &lo, &hi);
-      if (head < a.heads) {
-        a.out[head * kHeadDim + j] = lo;
-        a.out[head * kHeadDim + j + 32] = hi;
-      } else {
-        uint16_t* k = a.kc + ((size_t)(head - a.heads) * a.capacity + pos) * kHeadDim;
-        k[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
-        k[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
+    if (it < qkv_rope_items<R>(a)) {
+      const int head = it * (R / 2) / 32, j0 = it * (R / 2) % 32;
+#pragma unroll
+      for (int k = 0; k < R / 2; k++) {
+        const int j = j0 + k;
+        float lo, hi;
+        rope_pair(v[2 * k], v[2 * k + 1], e.cs[k], e.sn[k], &lo, &hi);
+        if (head < a.heads) {
+          a.out[head * kHeadDim + j] = lo;
+          a.out[head * kHeadDim + j + 32] = hi;
+        } else {
+          uint16_t* kr = a.kc + ((size_t)(head - a.heads) * a.capacity + pos) * kHeadDim;
+          kr[j] = __builtin_bit_cast(uint16_t, (_Float16)lo);
+          kr[j + 32] = __builtin_bit_cast(uint16_t, (_Float16)hi);
+        }
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
+      for (int i = 0; i < R; i++) {
         const int el = rows[i] - hidden - kvd;  // kv head el/64, dimension el%64
-        a.vt[(size_t)el * a.vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)(i == 0 ? v0 : v1));
+        a.vt[(size_t)el * a.vstride + pos] = __builtin_bit_cast(uint16_t, (_Float16)v[i]);
       }
     }
   }
@@ -197,23 +213,47 @@ struct Item {
   int rows[R];
   WTile<FMT, R, KC> w;
   EpiIn<EPI, R> e;
+  // EPI_OPS: also the epilogue operands (the one-item form; the loop form loads them per
+  // group, see k_fused).
+  template <bool EPI_OPS>
   __device__ __forceinline__ void load(const FusedArgs& a, int it, int pos, int lane) {
     const int i = min(it, a.items - 1);
     item_rows<EPI, R>(a, i, rows);
     wtile_load<FMT, R, KC, TL>(a.w, rows, lane, w);
-    epi_load<EPI, R>(a, i, pos, rows, e);
+    if constexpr (EPI_OPS) epi_load<EPI, R>(a, i, pos, rows, e);
   }
 };
 
-// LOOP: a team has several items (the output head): two named item buffers
-// alternate, so the next item's loads are in flight during this one's arithmetic
-// without register copies that would wait on them. F32: the fast-numerics core
-// (f32 staging with chunk sums, f32 sums); else f64 as the CPU path sums.
-template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool LOOP, bool F32>
+// How a team walks its items (k_fused's LOOP): one item; a ring of two buffers over
+// all of them, each item's epilogue on lane 0; groups of kLoopGroup items whose
+// epilogues run together.
+enum { LOOP_ONE = 0, LOOP_RING = 1, LOOP_GROUP = 2 };
+constexpr int kLoopBuffers = 2;     // item buffers of a group (loads kLoopBuffers - 1 items ahead)
+constexpr int kLoopGroup = 8;       // items of a team per straight-line group
+
+// LOOP_ONE: one item per team, its epilogue on lane 0 with operands loaded alongside
+// its weights. LOOP_RING (the output head; streaming grids of rows with little
+// epilogue work): two named item buffers alternate, so the next item's loads are in
+// flight during this one's arithmetic, each epilogue on lane 0. LOOP_GROUP (streaming
+// grids whose epilogues cost more): groups of kLoopGroup items, each group
+// straight-line code with a ring of kLoopBuffers buffers whose loads are issued and
+// consumed inside it (loads left in flight across a loop's back edge land in registers
+// that the loop header reassigns, and the compiler then waits for all of them there);
+// the group's epilogues run together at its end: lane 0 leaves each item's row sums
+// in LDS and lane j of the team runs item j's epilogue, its operands loaded at the
+// group's start -- one pass of epilogue instructions and one load per operand for
+// kLoopGroup items. F32: the fast-numerics core (f32 staging with chunk sums, f32
+// sums); else f64 as the CPU path sums.
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, int LOOP, bool F32>
 __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
+  constexpr int NBUF = LOOP == LOOP_GROUP ? kLoopBuffers : LOOP == LOOP_RING ? 2 : 1;
   extern __shared__ double smem[];
   __shared__ double red[kBlock / kWave];
-  __shared__ ArgPair tbest[kBlock / TL];
+  constexpr bool kGroup = LOOP == LOOP_GROUP;
+  constexpr int kBestPerTeam = kGroup ? kLoopGroup : 1;  // lanes of a team that track a best logit
+  __shared__ ArgPair tbest[kBlock / TL * kBestPerTeam];
+  __shared__ typename std::conditional<F32, float, double>::type
+      gsum[kGroup ? kBlock / TL : 1][kGroup ? kLoopGroup : 1][R];
   __shared__ float wl[PRO == PRO_COMBINE ? kBlock : 1];
   using Acc = typename std::conditional<F32, float, double>::type;
   using T = Teams<TL>;
@@ -238,8 +278,8 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   Pro pin;
   if constexpr (PRO == PRO_COMBINE) pin.load(a.in, a.heads);
   else pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
-  Item<FMT, TL, R, KC, EPI> A, B;
-  A.load(a, it, pos, lane);
+  Item<FMT, TL, R, KC, EPI> ring[NBUF];
+  if constexpr (!kGroup) ring[0].template load<true>(a, it, pos, lane);
   if constexpr (F32) {
     float* xs = reinterpret_cast<float*>(smem);
     const XLayoutF lay = chunk_layout_f<FMT>(a.w.nchunks);
@@ -262,33 +302,71 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   float bv = NAN;
   int bi = 0x7fffffff;
   Acc acc[R];
-  if constexpr (!LOOP) {
+  if constexpr (LOOP == LOOP_ONE) {
     if (it < a.items) {
-      dot(A.w, acc);
-      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, A.rows, acc, A.e, bv, bi);
+      dot(ring[0].w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, ring[0].rows, acc, ring[0].e, bv, bi);
     }
-  } else {
+  } else if constexpr (LOOP == LOOP_RING) {
     while (it < a.items) {
-      B.load(a, it + stride, pos, lane);
+      ring[1].template load<true>(a, it + stride, pos, lane);
       __builtin_amdgcn_sched_barrier(0);
-      dot(A.w, acc);
-      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, A.rows, acc, A.e, bv, bi);
+      dot(ring[0].w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, ring[0].rows, acc, ring[0].e, bv, bi);
       it += stride;
       if (it >= a.items) break;
-      A.load(a, it + stride, pos, lane);
+      ring[0].template load<true>(a, it + stride, pos, lane);
       __builtin_amdgcn_sched_barrier(0);
-      dot(B.w, acc);
-      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, B.rows, acc, B.e, bv, bi);
+      dot(ring[1].w, acc);
+      if (lane == 0) epilogue<R, EPI, Acc>(a, it, pos, ring[1].rows, acc, ring[1].e, bv, bi);
       it += stride;
+    }
+  } else {
+    // Item j of a group (it + j*stride) lives in ring[j % NBUF]; past the team's last
+    // item the loads re-read it and the arithmetic is skipped. Lane j < kLoopGroup of
+    // the team runs item j's epilogue (gl: the lanes past the group repeat its last).
+    const int team = T::team(), gl = min(lane, kLoopGroup - 1);
+    for (; it < a.items; it += kLoopGroup * stride) {
+      const int ie = it + gl * stride;
+      int erows[R];
+      EpiIn<EPI, R> e;
+      item_rows<EPI, R>(a, min(ie, a.items - 1), erows);
+      epi_load<EPI, R>(a, min(ie, a.items - 1), pos, erows, e);
+#pragma unroll
+      for (int j = 0; j + 1 < NBUF; j++) ring[j].template load<false>(a, it + j * stride, pos, lane);
+#pragma unroll
+      for (int j = 0; j < kLoopGroup; j++) {
+        constexpr int kAhead = NBUF - 1;
+        if (j + kAhead < kLoopGroup)
+          ring[(j + kAhead) % NBUF].template load<false>(a, it + (j + kAhead) * stride, pos, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        if (it + j * stride < a.items) {  // uniform over the team (the butterfly in dot)
+          dot(ring[j % NBUF].w, acc);
+          if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < R; i++) gsum[team][j][i] = acc[i];
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // a team is inside one wave: lane 0's LDS stores land first
+      if (lane < kLoopGroup && ie < a.items) {
+        Acc sums[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) sums[i] = gsum[team][lane][i];
+        epilogue<R, EPI, Acc>(a, ie, pos, erows, sums, e, bv, bi);
+      }
+      __builtin_amdgcn_wave_barrier();  // read before the next group's stores
     }
   }
   if constexpr (EPI == EPI_LOGITS) {
-    if (lane == 0) tbest[T::team()] = {bv, bi};
+    // Each tracking lane's best (argmax_better is a total order, so the merge order
+    // does not change the result).
+    if (lane < kBestPerTeam) tbest[T::team() * kBestPerTeam + lane] = {bv, bi};
     __syncthreads();
     if (threadIdx.x == 0) {
       float v = NAN;
       int i = 0x7fffffff;
-      for (int t = 0; t < T::kTeams; t++) {
+      for (int t = 0; t < T::kTeams * kBestPerTeam; t++) {
         if (argmax_better(tbest[t].v, tbest[t].i, v, i)) {
           v = tbest[t].v;
           i = tbest[t].i;
@@ -398,7 +476,14 @@ static int fused_blocks(int items, int teams, int max_blocks) {
   return blocks > max_blocks ? max_blocks : blocks;
 }
 
-template <int FMT, int TL, int R, int KC, int PRO, int EPI, bool F32>
+// Which forms of k_fused a launch site can use, so each site instantiates only those:
+// GRID_ONE, one item per team (the decode step's layer launches: their grid always covers
+// the items); GRID_RING and GRID_GROUP, teams walking several items in that loop form
+// (streaming grids); GRID_ANY, one item per team or the ring, whichever the grid needs
+// (the output head).
+enum { GRID_ONE = 0, GRID_RING = 1, GRID_GROUP = 2, GRID_ANY = 3 };
+
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, int GRID, bool F32>
 static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks) {
   using T = Teams<TL>;
   a.items = items;
@@ -406,40 +491,48 @@ static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks)
   const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
                          : (size_t)a.w.cols * sizeof(double);
   const dim3 grid(blocks, a.list_count > 1 ? a.list_count : 1);
-  if ((size_t)blocks * T::kTeams >= (size_t)items) {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, false, F32>), grid, dim3(kBlock), lds, s, a);
+  const bool one = (size_t)blocks * T::kTeams >= (size_t)items;
+  if constexpr (GRID == GRID_ONE) {
+    if (!one) return hipErrorInvalidValue;
+  }
+  constexpr int kLoop = GRID == GRID_GROUP ? LOOP_GROUP : LOOP_RING;
+  if constexpr (GRID == GRID_ONE) {
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_ONE, F32>), grid, dim3(kBlock), lds, s, a);
+  } else if constexpr (GRID == GRID_ANY) {
+    if (one) hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_ONE, F32>), grid, dim3(kBlock), lds, s, a);
+    else hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_RING, F32>), grid, dim3(kBlock), lds, s, a);
   } else {
-    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, true, F32>), grid, dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL((k_fused<FMT, TL, R, KC, PRO, EPI, kLoop, F32>), grid, dim3(kBlock), lds, s, a);
   }
   return hipGetLastError();
 }
 
-template <int FMT, int TL, int R, int KC, int PRO, int EPI>
+template <int FMT, int TL, int R, int KC, int PRO, int EPI, int GRID>
 static hipError_t fused_t(hipStream_t s, const FusedArgs& a, int items, int max_blocks) {
-  if (a.f32) return fused_l<FMT, TL, R, KC, PRO, EPI, true>(s, a, items, max_blocks);
-  return fused_l<FMT, TL, R, KC, PRO, EPI, false>(s, a, items, max_blocks);
+  if (a.f32) return fused_l<FMT, TL, R, KC, PRO, EPI, GRID, true>(s, a, items, max_blocks);
+  return fused_l<FMT, TL, R, KC, PRO, EPI, GRID, false>(s, a, items, max_blocks);
 }
 
-template <int FMT, int R, int PRO, int EPI>
+template <int FMT, int R, int PRO, int EPI, int GRID>
 static hipError_t fused_f(hipStream_t s, const FusedArgs& a, int items, int max_blocks) {
-  if (team_width(a.w.nchunks) == 32) return fused_t<FMT, 32, R, 1, PRO, EPI>(s, a, items, max_blocks);
+  if (team_width(a.w.nchunks) == 32) return fused_t<FMT, 32, R, 1, PRO, EPI, GRID>(s, a, items, max_blocks);
   switch (kc_for(a.w.nchunks)) {
-    case 1: return fused_t<FMT, 64, R, 1, PRO, EPI>(s, a, items, max_blocks);
-    case 2: return fused_t<FMT, 64, R, 2, PRO, EPI>(s, a, items, max_blocks);
-    case 3: return fused_t<FMT, 64, R, 3, PRO, EPI>(s, a, items, max_blocks);
-    case 5: return fused_t<FMT, 64, R, 5, PRO, EPI>(s, a, items, max_blocks);
-    case 8: return fused_t<FMT, 64, R, 8, PRO, EPI>(s, a, items, max_blocks);
-    case 16: return fused_t<FMT, 64, R, 16, PRO, EPI>(s, a, items, max_blocks);
+    case 1: return fused_t<FMT, 64, R, 1, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case 2: return fused_t<FMT, 64, R, 2, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case 3: return fused_t<FMT, 64, R, 3, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case 5: return fused_t<FMT, 64, R, 5, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case 8: return fused_t<FMT, 64, R, 8, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case 16: return fused_t<FMT, 64, R, 16, PRO, EPI, GRID>(s, a, items, max_blocks);
     default: return hipErrorInvalidValue;  // rows longer than the model limits allow
   }
 }
 
-template <int R, int PRO, int EPI>
-static hipError_t fused(hipStream_t s, const FusedArgs& a, int items, int max_blocks = 1 << 30) {
+template <int R, int PRO, int EPI, int GRID>
+static hipError_t fused(hipStream_t s, const FusedArgs& a, int items, int max_blocks) {
   switch (a.w.format) {
-    case QH_FMT_F16: return fused_f<QH_FMT_F16, R, PRO, EPI>(s, a, items, max_blocks);
-    case QH_FMT_INT8: return fused_f<QH_FMT_INT8, R, PRO, EPI>(s, a, items, max_blocks);
-    default: return fused_f<QH_FMT_INT4, R, PRO, EPI>(s, a, items, max_blocks);
+    case QH_FMT_F16: return fused_f<QH_FMT_F16, R, PRO, EPI, GRID>(s, a, items, max_blocks);
+    case QH_FMT_INT8: return fused_f<QH_FMT_INT8, R, PRO, EPI, GRID>(s, a, items, max_blocks);
+    default: return fused_f<QH_FMT_INT4, R, PRO, EPI, GRID>(s, a, items, max_blocks);
   }
 }
 
@@ -489,7 +582,12 @@ static void apply_list(FusedArgs& f, const RoleList* list) {
 // same launch over a list of copies of its weights (matrix roles only).
 static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role,
                              const RoleList* list = nullptr) {
-  const int mb = list && list->max_blocks > 0 ? list->max_blocks : 1 << 30;  // blocks per copy
+  // A streaming grid (blocks per copy given) takes more rows per work item where that helps: each
+  // team then walks many items, and the rows of one item share its loop overhead. A row is
+  // summed in the same order either way (its chunks per lane and the butterfly depend on the
+  // row length only).
+  const bool stream = list && list->max_blocks > 0;
+  const int mb = stream ? list->max_blocks : 1 << 30;  // blocks per copy
   const int kv_dim = m.kv_heads * m.head_dim;
   const LayerDev& l = m.layers_host[L];
   uint16_t* kc = c.kv + (size_t)L * c.layer_elems;
@@ -515,7 +613,9 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.state = c.state;
       f.capacity = c.capacity;
       apply_list(f, list);
-      return fused<2, PRO_RMSNORM, EPI_QKV>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2, mb);
+      if (stream)
+        return fused<4, PRO_RMSNORM, EPI_QKV, GRID_GROUP>(s, f, ((m.heads + m.kv_heads) * 64 + kv_dim) / 4, mb);
+      return fused<2, PRO_RMSNORM, EPI_QKV, GRID_ONE>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2, mb);
     case QH_ROLE_ATTENTION:
       if (m.numerics == QH_NUMERICS_FAST) {
         SlotArgs a{};
@@ -560,16 +660,19 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
         f.heads = m.heads;
         f.state = c.state;
         apply_list(f, list);
-        return fused<1, PRO_COMBINE, EPI_RESIDUAL>(s, f, l.o.rows, mb);
+        if (stream) return fused<4, PRO_COMBINE, EPI_RESIDUAL, GRID_GROUP>(s, f, (l.o.rows + 3) / 4, mb);
+        return fused<1, PRO_COMBINE, EPI_RESIDUAL, GRID_ONE>(s, f, l.o.rows, mb);
       }
       if (m.numerics == QH_NUMERICS_FAST) {  // a long cache: the attention output is merged already
         f.in = c.attn;
         apply_list(f, list);
-        return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.o.rows, mb);
+        if (stream) return fused<1, PRO_COPY, EPI_RESIDUAL, GRID_RING>(s, f, l.o.rows, mb);
+        return fused<1, PRO_COPY, EPI_RESIDUAL, GRID_ONE>(s, f, l.o.rows, mb);
       }
       f.in = c.attn;
       apply_list(f, list);
-      return fused<2, PRO_COPY, EPI_RESIDUAL>(s, f, (l.o.rows + 1) / 2, mb);
+      if (stream) return fused<1, PRO_COPY, EPI_RESIDUAL, GRID_RING>(s, f, l.o.rows, mb);
+      return fused<2, PRO_COPY, EPI_RESIDUAL, GRID_ONE>(s, f, (l.o.rows + 1) / 2, mb);
     case QH_ROLE_GATEUP:
       f.eps = m.eps;
       f.w = l.gu;
@@ -577,13 +680,15 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       f.gain = l.post_norm;
       f.out = c.h;
       apply_list(f, list);
-      return fused<2, PRO_RMSNORM, EPI_SWIGLU>(s, f, l.gu.rows / 2, mb);
+      if (stream) return fused<4, PRO_RMSNORM, EPI_SWIGLU, GRID_GROUP>(s, f, l.gu.rows / 4, mb);
+      return fused<2, PRO_RMSNORM, EPI_SWIGLU, GRID_ONE>(s, f, l.gu.rows / 2, mb);
     case QH_ROLE_DOWN:
       f.w = l.down;
       f.in = c.h;
       f.out = c.x;
       apply_list(f, list);
-      return fused<1, PRO_COPY, EPI_RESIDUAL>(s, f, l.down.rows, mb);
+      if (stream) return fused<1, PRO_COPY, EPI_RESIDUAL, GRID_RING>(s, f, l.down.rows, mb);
+      return fused<1, PRO_COPY, EPI_RESIDUAL, GRID_ONE>(s, f, l.down.rows, mb);
     default:
       return hipErrorInvalidValue;
   }
@@ -601,7 +706,7 @@ static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& 
   f.partials = static_cast<ArgPair*>(c.lm_partials);
   apply_list(f, list);
   const int mb = list && list->max_blocks > 0 ? std::min(list->max_blocks, kLmMaxBlocks) : kLmMaxBlocks;
-  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS>(s, f, (m.vocab + kLmRows - 1) / kLmRows, mb);
+  return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS, GRID_ANY>(s, f, (m.vocab + kLmRows - 1) / kLmRows, mb);
 }
 
 hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list) {

@@ -1137,6 +1137,7 @@ int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t 
   int count = 1;
   std::function<hipError_t()> launch;
   qh::RoleList list{};
+  size_t out_len = 0, ostride = 0;  // matrix roles: floats of one copy's output, and between copies
   if (role == QH_ROLE_ATTENTION) {
     const size_t elems = cd.layer_elems, stride = round256(elems * 2) / 2;
     count = (int)std::max<size_t>(1, (min_bytes + elems * 2 - 1) / (elems * 2));
@@ -1158,8 +1159,8 @@ int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t 
     const size_t per = data + nscale * 4 * (w.format == QH_FMT_INT4 ? 2 : 1);
     count = (int)std::max<size_t>(1, (min_bytes + per - 1) / per);
     const size_t dstride = round256(data), sstride = round256(nscale * 4) / 4;
-    const size_t out_len = role == QH_ROLE_HEAD ? md.vocab : role == QH_ROLE_GATEUP ? md.intermediate : md.hidden;
-    const size_t ostride = round256(out_len * 4) / 4;
+    out_len = role == QH_ROLE_HEAD ? md.vocab : role == QH_ROLE_GATEUP ? md.intermediate : md.hidden;
+    ostride = round256(out_len * 4) / 4;
     uint8_t* d = nullptr;
     float *sc = nullptr, *zr = nullptr, *out = nullptr;
     void* partials = nullptr;
@@ -1202,9 +1203,33 @@ int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t 
   if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
   if (e0) hipEventDestroy(e0);
   if (e1) hipEventDestroy(e1);
+  // A streaming grid runs the loop form of the kernel, with more rows per work item for some
+  // roles; each row is summed in the same order, so its outputs must equal those of the decode
+  // step's own launch shape (blocks_per_copy 0) bit for bit. Checked on the first and the last
+  // copy, each form launched once from zeroed outputs (the residual roles add into them).
+  bool differs = false;
+  if (err == hipSuccess && role != QH_ROLE_ATTENTION && blocks_per_copy > 0) {
+    std::vector<float> got(2 * out_len), want(2 * out_len);
+    auto run_once = [&](int max_blocks, float* host) -> hipError_t {
+      list.max_blocks = max_blocks;
+      hipError_t e = hipMemsetAsync(list.out, 0, (size_t)count * ostride * 4, s);
+      if (e == hipSuccess) e = qh::enqueue_role_list(s, md, cd, role, list);
+      if (e == hipSuccess) e = hipMemcpyAsync(host, list.out, out_len * 4, hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(host + out_len, list.out + (size_t)(count - 1) * ostride, out_len * 4,
+                           hipMemcpyDeviceToHost, s);
+      if (e == hipSuccess) e = hipStreamSynchronize(s);
+      return e;
+    };
+    err = run_once(blocks_per_copy, got.data());
+    if (err == hipSuccess) err = run_once(0, want.data());
+    differs = err == hipSuccess && std::memcmp(got.data(), want.data(), got.size() * sizeof(float)) != 0;
+  }
   hipStreamSynchronize(s);
   for (void* p : held) hipFree(p);
   QH_HIP(err);
+  QH_CHECK(!differs, QH_ERR_STATE, "role %d: the streaming grid's outputs differ from the decode step's launch",
+           role);
   *us_per_launch = ms * 1e3f / reps;
   *copies = count;
   return QH_OK;
