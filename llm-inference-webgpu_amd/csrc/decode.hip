@@ -72,7 +72,7 @@ template <int R>
 __device__ __forceinline__ int qkv_rope_items(const FusedArgs& a) {
   return (a.heads + a.kv_heads) * 32 / (R / 2);
 }
-template <int EPI, int R>
+template <int EPI, int R, bool CLAMP = true>
 __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows)[R]) {
   if constexpr (EPI == EPI_QKV) {
     static_assert(R == 2 || R == 4, "qkv items are one or two rope pairs");
@@ -93,7 +93,7 @@ __device__ __forceinline__ void item_rows(const FusedArgs& a, int it, int (&rows
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < R; i++) rows[i] = min(it * R + i, a.w.rows - 1);
+    for (int i = 0; i < R; i++) rows[i] = CLAMP ? min(it * R + i, a.w.rows - 1) : it * R + i;
   }
 }
 
@@ -222,6 +222,12 @@ struct Item {
     wtile_load<FMT, R, KC, TL>(a.w, rows, lane, w);
     if constexpr (EPI_OPS) epi_load<EPI, R>(a, i, pos, rows, e);
   }
+  // The weights of item `it`, which may lie past the last item (CLAMP off: rows past the
+  // matrix read as zeros through the buffer resources).
+  __device__ __forceinline__ void load_buf(const FusedArgs& a, const BufMat& b, int it, int lane) {
+    item_rows<EPI, R, false>(a, it, rows);
+    wtile_load_buf<FMT, R, KC, TL>(a.w, b, rows, lane, w);
+  }
 };
 
 // How a team walks its items (k_fused's LOOP): one item; a ring of two buffers over
@@ -299,6 +305,15 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
     if constexpr (F32) wtile_dot_f32<FMT, R, KC, TL>(a.w, w, reinterpret_cast<const float*>(smem), lane, acc);
     else wtile_dot<FMT, R, KC, TL>(a.w, w, smem, lane, acc);
   };
+  // The grouped loop with one chunk per lane (f32 core) sums every item against the same
+  // staged chunk, so the lane reads it into registers once.
+  constexpr bool kXReg = kGroup && F32 && KC == 1;
+  [[maybe_unused]] XChunk<FMT> xr;
+  if constexpr (kXReg) {
+    const float* xs = reinterpret_cast<const float*>(smem);
+    const int c = min(lane, a.w.nchunks - 1);
+    xr.load(xs + 4 * c, 4 * a.w.nchunks, FMT == QH_FMT_F16 ? 0.f : xs[a.w.cols + c]);
+  }
   float bv = NAN;
   int bi = 0x7fffffff;
   Acc acc[R];
@@ -326,6 +341,7 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
     // item the loads re-read it and the arithmetic is skipped. Lane j < kLoopGroup of
     // the team runs item j's epilogue (gl: the lanes past the group repeat its last).
     const int team = T::team(), gl = min(lane, kLoopGroup - 1);
+    const BufMat bm = buf_mat(a.w);
     for (; it < a.items; it += kLoopGroup * stride) {
       const int ie = it + gl * stride;
       int erows[R];
@@ -333,15 +349,15 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
       item_rows<EPI, R>(a, min(ie, a.items - 1), erows);
       epi_load<EPI, R>(a, min(ie, a.items - 1), pos, erows, e);
 #pragma unroll
-      for (int j = 0; j + 1 < NBUF; j++) ring[j].template load<false>(a, it + j * stride, pos, lane);
+      for (int j = 0; j + 1 < NBUF; j++) ring[j].load_buf(a, bm, it + j * stride, lane);
 #pragma unroll
       for (int j = 0; j < kLoopGroup; j++) {
         constexpr int kAhead = NBUF - 1;
-        if (j + kAhead < kLoopGroup)
-          ring[(j + kAhead) % NBUF].template load<false>(a, it + (j + kAhead) * stride, pos, lane);
+        if (j + kAhead < kLoopGroup) ring[(j + kAhead) % NBUF].load_buf(a, bm, it + (j + kAhead) * stride, lane);
         __builtin_amdgcn_sched_barrier(0);
         if (it + j * stride < a.items) {  // uniform over the team (the butterfly in dot)
-          dot(ring[j % NBUF].w, acc);
+          if constexpr (kXReg) wtile_dot_f32_x<FMT, R, TL>(a.w, ring[j % NBUF].w, xr, lane, acc);
+          else dot(ring[j % NBUF].w, acc);
           if (lane == 0) {
 #pragma unroll
             for (int i = 0; i < R; i++) gsum[team][j][i] = acc[i];
@@ -492,6 +508,8 @@ static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks)
                          : (size_t)a.w.cols * sizeof(double);
   const dim3 grid(blocks, a.list_count > 1 ? a.list_count : 1);
   const bool one = (size_t)blocks * T::kTeams >= (size_t)items;
+  // the grouped loop addresses the matrix through 32-bit buffer offsets
+  if (GRID == GRID_GROUP && (size_t)a.w.rows * a.w.row_bytes >= ((size_t)1 << 31)) return hipErrorInvalidValue;
   if constexpr (GRID == GRID_ONE) {
     if (!one) return hipErrorInvalidValue;
   }

@@ -421,6 +421,57 @@ __device__ __forceinline__ void wtile_load(const DMat& m, const int (&rows)[R], 
   }
 }
 
+// A matrix's arrays as buffer resources. A load through one takes a 32-bit per-lane
+// byte offset, and the hardware checks it against the array's size: a read past the
+// end returns zeros instead of touching memory. (The check covers the per-lane offset
+// and the instruction's immediate, not the scalar offset, so every offset here is
+// per-lane and the scalar offset is 0.) The arrays must be under 4 GiB.
+struct BufMat {
+  __amdgpu_buffer_rsrc_t data, scales, zeros;
+};
+constexpr int kRawBufferWord3 = 0x00020000;  // raw (unformatted) buffer, stride 0
+constexpr int kLoadNonTemporal = 2;          // the load's cache policy: streamed, not kept
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)(uint32_t)bytes, kRawBufferWord3);
+}
+__device__ __forceinline__ BufMat buf_mat(const DMat& m) {
+  const size_t n = (size_t)m.rows * (m.format == QH_FMT_INT4 ? m.gpr : 1) * sizeof(float);
+  BufMat b;
+  b.data = raw_buffer(m.data, (size_t)m.rows * m.row_bytes);
+  b.scales = raw_buffer(m.scales, m.format == QH_FMT_F16 ? 0 : n);
+  b.zeros = raw_buffer(m.zeros, m.format == QH_FMT_INT4 ? n : 0);
+  return b;
+}
+
+// wtile_load through buffer resources, for rows that may lie past the matrix (a loop
+// over rows that loads ahead): no clamping, 32-bit offsets, and what lies past the end
+// reads as zeros (those rows' sums are never used; nor are chunks past a row's end).
+template <int FMT, int R, int KC, int TL>
+__device__ __forceinline__ void wtile_load_buf(const DMat& m, const BufMat& b, const int (&rows)[R], int tl,
+                                               WTile<FMT, R, KC>& t) {
+#pragma unroll
+  for (int k = 0; k < KC; k++) {
+    const int c = tl + k * TL;
+#pragma unroll
+    for (int i = 0; i < R; i++)
+      t.w[k][i] = __builtin_amdgcn_raw_buffer_load_b128(b.data, rows[i] * m.row_bytes + 16 * c, 0, kLoadNonTemporal);
+    if constexpr (FMT == QH_FMT_INT4) {
+      const int g = c / m.cpg;
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const int off = (rows[i] * m.gpr + g) * (int)sizeof(float);
+        t.s[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.scales, off, 0, 0));
+        t.z[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.zeros, off, 0, 0));
+      }
+    }
+  }
+  if constexpr (FMT == QH_FMT_INT8) {
+#pragma unroll
+    for (int i = 0; i < R; i++)
+      t.s[0][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.scales, rows[i] * 4, 0, 0));
+  }
+}
+
 // xs is chunk-transposed (chunk_layout<FMT>(m.nchunks)).
 template <int FMT, int R, int KC, int TL>
 __device__ __forceinline__ void wtile_dot(const DMat& m, const WTile<FMT, R, KC>& t, const double* xs,
@@ -513,16 +564,29 @@ __device__ __forceinline__ void stage_group_f32(v4f v, int gi, bool valid, float
   }
 }
 
-// acc[r] += the f32 dot of chunk row w[r] with the staged chunk at p (group g at
-// p + g*gs), for R rows element-major. s/z: int4 group scale and zero point of each
-// row (int8 takes its row scale after the team sum); sx the chunk sum.
+// One staged chunk of an f32 activation in registers: its 4-element groups (read from
+// p + g*gs, group g of the chunk) and, for quantized formats, its chunk sum.
+template <int FMT>
+struct XChunk {
+  v4f g[Fmt<FMT>::kW / 4];
+  float sx;
+  __device__ __forceinline__ void load(const float* __restrict__ p, int gs, float chunk_sum) {
+#pragma unroll
+    for (int k = 0; k < Fmt<FMT>::kW / 4; k++) g[k] = *reinterpret_cast<const v4f*>(p + k * gs);
+    sx = chunk_sum;
+  }
+};
+
+// acc[r] += the f32 dot of chunk row w[r] with the chunk x, for R rows element-major.
+// s/z: int4 group scale and zero point of each row (int8 takes its row scale after the
+// team sum).
 template <int FMT, int R>
-__device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* __restrict__ p, int gs,
-                                               const float (&s)[R], const float (&z)[R], float sx,
-                                               float (&acc)[R]) {
+__device__ __forceinline__ void chunk_rows_f32_x(const v4u (&w)[R], const XChunk<FMT>& x, const float (&s)[R],
+                                                 const float (&z)[R], float (&acc)[R]) {
+  const float sx = x.sx;
   if constexpr (FMT == QH_FMT_F16) {
-    const v4f x0 = *reinterpret_cast<const v4f*>(p);
-    const v4f x1 = *reinterpret_cast<const v4f*>(p + gs);
+    const v4f x0 = x.g[0];
+    const v4f x1 = x.g[1];
     const float xe[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -533,9 +597,7 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
     }
   } else if constexpr (FMT == QH_FMT_INT8) {
     const float c0 = -128.f * sx;  // exact
-    v4f xg[4];  // the chunk's activations, all read before any arithmetic
-#pragma unroll
-    for (int k = 0; k < 4; k++) xg[k] = *reinterpret_cast<const v4f*>(p + k * gs);
+    const v4f(&xg)[4] = x.g;
     float d[R];
 #pragma unroll
     for (int r = 0; r < R; r++) d[r] = c0;
@@ -561,9 +623,7 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
       pe[r] = -z[r] * sx * 0x1p-24f;
       po[r] = 0.f;
     }
-    v4f xg[8];  // the chunk's activations, all read before any arithmetic
-#pragma unroll
-    for (int k = 0; k < 8; k++) xg[k] = *reinterpret_cast<const v4f*>(p + k * gs);
+    const v4f(&xg)[8] = x.g;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
       // dword k holds elements 8k .. 8k+7: byte b = (element 8k+2b) | (element 8k+2b+1) << 4.
@@ -587,6 +647,17 @@ __device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* _
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = fmaf(s[r] * 0x1p24f, fmaf(po[r], 0.0625f, pe[r]), acc[r]);
   }
+}
+
+// The same with the chunk read from LDS (group g at p + g*gs, all read before any
+// arithmetic) and its chunk sum sx.
+template <int FMT, int R>
+__device__ __forceinline__ void chunk_rows_f32(const v4u (&w)[R], const float* __restrict__ p, int gs,
+                                               const float (&s)[R], const float (&z)[R], float sx,
+                                               float (&acc)[R]) {
+  XChunk<FMT> x;
+  x.load(p, gs, sx);
+  chunk_rows_f32_x<FMT, R>(w, x, s, z, acc);
 }
 
 // a * b rounded on its own: never fused into a multiply-add with the operation that
@@ -621,6 +692,18 @@ __device__ __forceinline__ void wtile_dot_f32(const DMat& m, const WTile<FMT, R,
       chunk_rows_f32<FMT, R>(t.w[k], xs + 4 * c, 4 * m.nchunks, t.s[k], t.z[k], sx, acc);
     }
   }
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = row_out_f32<FMT>(team_sum<TL>(acc[i]), t.s[0][i]);
+}
+
+// wtile_dot_f32 for one chunk per lane (KC = 1) whose staged chunk is already in
+// registers (x: chunk tl, read once by a team that sums many items against it).
+template <int FMT, int R, int TL>
+__device__ __forceinline__ void wtile_dot_f32_x(const DMat& m, const WTile<FMT, R, 1>& t, const XChunk<FMT>& x,
+                                                int tl, float (&acc)[R]) {
+#pragma unroll
+  for (int i = 0; i < R; i++) acc[i] = 0.f;
+  if (tl < m.nchunks) chunk_rows_f32_x<FMT, R>(t.w[0], x, t.s[0], t.z[0], acc);
 #pragma unroll
   for (int i = 0; i < R; i++) acc[i] = row_out_f32<FMT>(team_sum<TL>(acc[i]), t.s[0][i]);
 }
