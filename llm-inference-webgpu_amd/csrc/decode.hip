@@ -63,6 +63,12 @@ struct FusedArgs {
   // argmax partials + z * list_part). 0: the one matrix of the decode step.
   int list_count;
   size_t list_w, list_s, list_out, list_part;
+  size_t list_k, list_v;  // EPI_QKV: f16 elements between consecutive copies' key / value append targets
+  // A flat list (the grouped loop only; grid.y 1): the items of all list_count copies in
+  // one sequence, item g being item g % items of copy g / items, and each block walks
+  // list_flat consecutive ones of it (a whole number of groups of every team). 0: one
+  // copy per blockIdx.y.
+  int list_flat;
 };
 
 // Rows of work item `it`. QKV: R/2 consecutive rope pairs (j, j+32) of one q or k
@@ -224,9 +230,10 @@ struct Item {
   }
   // The weights of item `it`, which may lie past the last item (CLAMP off: rows past the
   // matrix read as zeros through the buffer resources).
-  __device__ __forceinline__ void load_buf(const FusedArgs& a, const BufMat& b, int it, int lane) {
+  __device__ __forceinline__ void load_buf(const FusedArgs& a, const BufMat& b, int it, int lane, int wbase,
+                                           int sbase) {
     item_rows<EPI, R, false>(a, it, rows);
-    wtile_load_buf<FMT, R, KC, TL>(a.w, b, rows, lane, w);
+    wtile_load_buf<FMT, R, KC, TL>(a.w, b, rows, lane, wbase, sbase, w);
   }
 };
 
@@ -270,6 +277,8 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
     if (a.w.zeros) a.w.zeros += z * a.list_s;
     a.out += z * a.list_out;
     if (a.partials) a.partials += z * a.list_part;
+    if (a.kc) a.kc += z * a.list_k;
+    if (a.vt) a.vt += z * a.list_v;
   }
   const int lane = T::lane();
   const int stride = gridDim.x * T::kTeams;
@@ -337,25 +346,70 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
       it += stride;
     }
   } else {
-    // Item j of a group (it + j*stride) lives in ring[j % NBUF]; past the team's last
-    // item the loads re-read it and the arithmetic is skipped. Lane j < kLoopGroup of
-    // the team runs item j's epilogue (gl: the lanes past the group repeat its last).
+    constexpr int kPastEnd = 0x7fff0000;  // a byte offset past any flat list
+    // The team's items are g0, g0 + gs, ... below gend: items of this block's copy, or
+    // of a flat list (the block's share of it; item g is item g % items of copy
+    // g / items). Item j of a group (g0 + j*gs) lives in ring[j % NBUF]; past the end
+    // its loads read zeros or unused rows and the arithmetic is skipped. Lane j <
+    // kLoopGroup of the team runs item j's epilogue (gl: the lanes past the group
+    // repeat its last).
     const int team = T::team(), gl = min(lane, kLoopGroup - 1);
-    const BufMat bm = buf_mat(a.w);
-    for (; it < a.items; it += kLoopGroup * stride) {
-      const int ie = it + gl * stride;
+    const bool flat = a.list_flat > 0;
+    int g0 = it, gs = stride, gend = a.items;
+    BufMat bm;
+    if (flat) {
+      const int total = a.items * a.list_count;
+      g0 = blockIdx.x * a.list_flat + team;
+      gs = T::kTeams;
+      gend = min(total, (blockIdx.x + 1) * a.list_flat);
+      bm = buf_mat(a.w, a.list_count, a.list_w, a.list_s);
+    } else {
+      bm = buf_mat(a.w);
+    }
+    // (copy, item) of sequence entry g; of g0 + d from g0's by carrying into the next copies
+    auto split = [&](int g, int& z, int& l) {
+      z = flat ? g / a.items : 0;
+      l = g - z * a.items;
+    };
+    for (; g0 < gend; g0 += kLoopGroup * gs) {
+      int z0, l0;
+      split(g0, z0, l0);
+      auto step = [&](int d, int& z, int& l) {
+        z = z0;
+        l = l0 + d;
+        if (flat)
+          while (l >= a.items) {
+            l -= a.items;
+            z++;
+          }
+      };
+      int ze, le;
+      split(min(g0 + gl * gs, gend - 1), ze, le);
+      FusedArgs ae = a;  // this lane's epilogue item's copy
+      ae.out = a.out + (size_t)ze * a.list_out;
+      if (a.kc) ae.kc = a.kc + (size_t)ze * a.list_k;
+      if (a.vt) ae.vt = a.vt + (size_t)ze * a.list_v;
       int erows[R];
       EpiIn<EPI, R> e;
-      item_rows<EPI, R>(a, min(ie, a.items - 1), erows);
-      epi_load<EPI, R>(a, min(ie, a.items - 1), pos, erows, e);
+      item_rows<EPI, R>(ae, le, erows);
+      epi_load<EPI, R>(ae, le, pos, erows, e);
+      auto load = [&](Item<FMT, TL, R, KC, EPI>& item, int j) {
+        int z, l;
+        step(j * gs, z, l);
+        // past the block's share of a flat list: offsets beyond the resources, which read
+        // zeros without touching memory (the list is under 2 GiB)
+        const bool live = !flat || g0 + j * gs < gend;
+        item.load_buf(a, bm, live ? l : 0, lane, live ? z * (int)a.list_w : kPastEnd,
+                      live ? z * (int)a.list_s * (int)sizeof(float) : kPastEnd);
+      };
 #pragma unroll
-      for (int j = 0; j + 1 < NBUF; j++) ring[j].load_buf(a, bm, it + j * stride, lane);
+      for (int j = 0; j + 1 < NBUF; j++) load(ring[j], j);
 #pragma unroll
       for (int j = 0; j < kLoopGroup; j++) {
         constexpr int kAhead = NBUF - 1;
-        if (j + kAhead < kLoopGroup) ring[(j + kAhead) % NBUF].load_buf(a, bm, it + (j + kAhead) * stride, lane);
+        if (j + kAhead < kLoopGroup) load(ring[(j + kAhead) % NBUF], j + kAhead);
         __builtin_amdgcn_sched_barrier(0);
-        if (it + j * stride < a.items) {  // uniform over the team (the butterfly in dot)
+        if (g0 + j * gs < gend) {  // uniform over the team (the butterfly in dot)
           if constexpr (kXReg) wtile_dot_f32_x<FMT, R, TL>(a.w, ring[j % NBUF].w, xr, lane, acc);
           else dot(ring[j % NBUF].w, acc);
           if (lane == 0) {
@@ -365,11 +419,11 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
         }
       }
       __builtin_amdgcn_wave_barrier();  // a team is inside one wave: lane 0's LDS stores land first
-      if (lane < kLoopGroup && ie < a.items) {
+      if (lane < kLoopGroup && g0 + gl * gs < gend) {
         Acc sums[R];
 #pragma unroll
         for (int i = 0; i < R; i++) sums[i] = gsum[team][lane][i];
-        epilogue<R, EPI, Acc>(a, ie, pos, erows, sums, e, bv, bi);
+        epilogue<R, EPI, Acc>(ae, le, pos, erows, sums, e, bv, bi);
       }
       __builtin_amdgcn_wave_barrier();  // read before the next group's stores
     }
@@ -503,6 +557,30 @@ template <int FMT, int TL, int R, int KC, int PRO, int EPI, int GRID, bool F32>
 static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks) {
   using T = Teams<TL>;
   a.items = items;
+  a.list_flat = 0;
+  if constexpr (GRID == GRID_GROUP) {
+    if (a.list_count > 1 && (size_t)a.list_count * a.list_w < ((size_t)1 << 31) &&
+        (size_t)a.list_count * a.list_s * sizeof(float) < ((size_t)1 << 31)) {
+    // A weight list on the grouped loop runs flat: as many blocks as the device holds at
+    // once share all the copies' items equally (one block per copy leaves the copies'
+    // blocks outnumbering the resident slots by a fraction, and the last round runs on
+    // part of the device).
+    const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
+                           : (size_t)a.w.cols * sizeof(double);
+    auto kernel = k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_GROUP, F32>;
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, lds);
+    if (e != hipSuccess) return e;
+    const size_t total = (size_t)items * a.list_count, teams = T::kTeams;
+    const size_t resident = std::max(1, cus * per_cu);
+    const size_t per = ((total + resident - 1) / resident + teams - 1) / teams * teams;
+    a.list_flat = (int)per;
+    hipLaunchKernelGGL(kernel, dim3((total + per - 1) / per, 1), dim3(kBlock), lds, s, a);
+    return hipGetLastError();
+    }
+  }
   const int blocks = fused_blocks(items, T::kTeams, max_blocks);
   const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
                          : (size_t)a.w.cols * sizeof(double);
@@ -594,6 +672,12 @@ static void apply_list(FusedArgs& f, const RoleList* list) {
   f.list_part = list->part_stride;
   f.out = list->out;
   if (list->partials) f.partials = static_cast<ArgPair*>(list->partials);
+  if (list->kc) {  // the q|k|v copies' own K/V append targets
+    f.kc = list->kc;
+    f.vt = list->vt;
+    f.list_k = list->k_stride;
+    f.list_v = list->v_stride;
+  }
 }
 
 // The launch of `role` (QKV, ATTENTION, OPROJ, GATEUP or DOWN) for layer L; with `list`, the

@@ -1189,6 +1189,23 @@ int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t 
     list.out = out;
     list.partials = partials;
     list.max_blocks = blocks_per_copy;
+    if (role == QH_ROLE_QKV && err == hipSuccess) {
+      // Each copy appends its key and value rows where no other copy does, as each layer
+      // appends to its own cache in the step (all copies appending to one cache would put
+      // every copy's stores on the same few cache lines): copy z's key rows and value
+      // entries land 64 elements (one 128-byte line) after copy z-1's, in an area shaped
+      // like one layer's cache and longer by that shift. The cache itself is untouched.
+      const size_t shift = 64, ke = cd.key_elems + (size_t)count * shift,
+                   ve = cd.layer_elems - cd.key_elems + (size_t)count * shift;
+      uint16_t* kv = nullptr;
+      err = grab((ke + ve) * sizeof(uint16_t), (void**)&kv);
+      if (err == hipSuccess) {
+        list.kc = kv;
+        list.vt = kv + ke;
+        list.k_stride = shift;
+        list.v_stride = shift;
+      }
+    }
     launch = [&]() { return qh::enqueue_role_list(s, md, cd, role, list); };
   }
   hipEvent_t e0 = nullptr, e1 = nullptr;

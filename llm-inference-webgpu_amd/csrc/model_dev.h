@@ -129,6 +129,11 @@ struct RoleList {
   float* out;
   void* partials;
   int max_blocks;  // blocks per copy (0: the decode step's own grid)
+  // QH_ROLE_QKV: where copy z appends its key and value rows: kc + z * k_stride and
+  // vt + z * v_stride, laid out as the cache's (null: the cache itself).
+  uint16_t* kc;
+  uint16_t* vt;
+  size_t k_stride, v_stride;
 };
 // The launch of QH_ROLE_QKV, OPROJ, GATEUP, DOWN (layer 0's operands otherwise) or HEAD over a list.
 hipError_t enqueue_role_list(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, const RoleList& list);
