@@ -205,9 +205,12 @@ class _Ptr:
 def stream_decode_kernels(model, cache, cfg, ctx_len, ceiling, reps=5, totals=(512, 1024, 2048)):
     """The decode step's matrix kernels over the same >= 512 MiB of operand copies as
     cold_decode_kernels, on a grid sized for streaming instead of for one step's latency
-    (qh_decode_kernel_time_stream): blocks_per_copy blocks per copy, so that the launch has about
-    `total` blocks; each block stages its activation once and walks many rows with the next rows'
-    loads in flight. Same kernel code and arithmetic as the step; the best total is reported."""
+    (qh_decode_kernel_time_stream); each block stages its activation once and walks many rows
+    with the next rows' loads in flight. down and the head: blocks_per_copy blocks per copy, so
+    that the launch has about `total` blocks (the best total is reported). qkv, o-proj and
+    gate|up run as a flat list, whose grid the library sizes to the device's resident blocks
+    (blocks_per_copy does not change it). The library checks each list launch's outputs bit for
+    bit against the step's own launch shape."""
     d, kv, ffn, V = cfg.hidden, cfg.kv_dim, cfg.intermediate, cfg.vocab
     int4 = lambda r, c: r * c // 2 + r * (c // 128) * 8
     per_copy = {"qkv": int4(d + 2 * kv, d), "oproj": int4(d, d), "gateup": int4(2 * ffn, d),
@@ -222,7 +225,7 @@ def stream_decode_kernels(model, cache, cfg, ctx_len, ceiling, reps=5, totals=(5
             us, copies = model.kernel_time_stream(cache, role, bpc, 512 << 20, reps)
             gbs = copies * per_copy[role] / (us * 1e-6) / 1e9
             if best is None or gbs > best["GBps"]:
-                best = {"blocks_per_copy": bpc, "blocks": bpc * copies, "copies": copies,
+                best = {"blocks_per_copy": bpc, "copies": copies,
                         "bytes_per_launch": copies * per_copy[role], "us_per_launch": round(us, 2),
                         "GBps": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
         if ceiling:
