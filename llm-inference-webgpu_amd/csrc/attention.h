@@ -946,27 +946,33 @@ static __global__ __launch_bounds__(kWave) void k_attn_combine(const float* __re
 
 // The decode step's combine, run by the o-projection while it stages its input:
 // xs[lay.pos(i)] = attention output i (i = h*64 + d) as f64, for a single query
-// whose slot partials (kDecodeSlots = 16 per head, empty ones neutral, written by
+// whose slot partials (kDecodeSlots <= 16 per head, empty ones neutral, written by
 // k_attn_gqa with the maxima in base-2 units) are at `part`. Thread i < heads*16
-// owns head h = i/16: it reads the (m, l) of slot i%16 and the four output
-// dimensions 4*(i%16) .. +3 of every slot; the 16 lanes of a head form one DPP
-// team, so M, L and the slot weights 2^(m_s - M) / L stay
+// owns head h = i/16: it reads the (m, l) of slot i%16 (neutral past the slots) and
+// the four output dimensions 4*(i%16) .. +3 of every slot; the 16 lanes of a head
+// form one DPP team, so M, L and the slot weights 2^(m_s - M) / L stay
 // inside it (shared through the wave's own LDS slice). Nothing here depends on
 // the position. heads <= 16. Loads (CombineIn::load) and arithmetic are split as
 // for StageIn.
+constexpr int kCombineLanes = 16;  // lanes per head in the combine: four output dimensions each
 struct CombineIn {
   v4f ov[kDecodeSlots];
   float mv, lv;
   __device__ __forceinline__ void load(const float* __restrict__ part, int heads) {
-    static_assert(kDecodeSlots == 16, "one 16-lane team per head");
+    static_assert(kDecodeSlots <= kCombineLanes, "one lane per slot of a head");
     const int i = threadIdx.x;
-    const int h = min(i / kDecodeSlots, heads - 1), k = i % kDecodeSlots;
+    const int h = min(i / kCombineLanes, heads - 1), k = i % kCombineLanes;
     const float* ph = part + (size_t)h * kDecodeSlots * kPartStride;
 #pragma unroll
     for (int s = 0; s < kDecodeSlots; s++)
       ov[s] = *reinterpret_cast<const v4f*>(ph + (size_t)s * kPartStride + 4 + 4 * k);
-    mv = ph[(size_t)k * kPartStride];
-    lv = ph[(size_t)k * kPartStride + 1];
+    const int ks = min(k, kDecodeSlots - 1);  // lanes past the slots hold the neutral partial
+    mv = ph[(size_t)ks * kPartStride];
+    lv = ph[(size_t)ks * kPartStride + 1];
+    if (k >= kDecodeSlots) {
+      mv = -INFINITY;
+      lv = 0.f;
+    }
   }
 };
 
@@ -980,7 +986,7 @@ __device__ __forceinline__ v4f attn_combine_quad(const CombineIn& in, float* wl)
   const float L = team_sum<16>(w * in.lv);
   wl[i] = w / L;
   __builtin_amdgcn_wave_barrier();
-  const float* wh = wl + (i & ~(kDecodeSlots - 1));
+  const float* wh = wl + (i & ~(kCombineLanes - 1));
   v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < kDecodeSlots; s++) {
@@ -997,8 +1003,8 @@ __device__ __forceinline__ void stage_attn_combine(const CombineIn& in, int head
                                                    float* wl) {
   const v4f acc = attn_combine_quad(in, wl);
   const int i = threadIdx.x;
-  if (i < heads * kDecodeSlots) {
-    const int j = (i / kDecodeSlots) * kHeadDim + 4 * (i % kDecodeSlots);
+  if (i < heads * kCombineLanes) {
+    const int j = (i / kCombineLanes) * kHeadDim + 4 * (i % kCombineLanes);
     xs[lay.pos(j)] = (double)acc.x;
     xs[lay.pos(j + 1)] = (double)acc.y;
     xs[lay.pos(j + 2)] = (double)acc.z;
@@ -1015,7 +1021,7 @@ __device__ __forceinline__ void stage_attn_combine_f32(const CombineIn& in, int 
                                                        float* wl) {
   const v4f acc = attn_combine_quad(in, wl);
   const int i = threadIdx.x;
-  stage_group_f32<FMT>(acc, i, i < heads * kDecodeSlots, xs, xs + heads * kHeadDim, lay);
+  stage_group_f32<FMT>(acc, i, i < heads * kCombineLanes, xs, xs + heads * kHeadDim, lay);
   __syncthreads();
 }
 

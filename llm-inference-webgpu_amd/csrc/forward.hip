@@ -108,8 +108,8 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge_rows(const float* __restr
   in.load(part + (size_t)t * heads * kDecodeSlots * kPartStride, heads);
   const v4f acc = attn_combine_quad(in, wl);
   const int i = threadIdx.x;
-  if (i < heads * kDecodeSlots) {
-    float* o = out + (size_t)t * heads * kHeadDim + (i / kDecodeSlots) * kHeadDim + 4 * (i % kDecodeSlots);
+  if (i < heads * kCombineLanes) {
+    float* o = out + (size_t)t * heads * kHeadDim + (i / kCombineLanes) * kHeadDim + 4 * (i % kCombineLanes);
     o[0] = acc.x;
     o[1] = acc.y;
     o[2] = acc.z;
