@@ -398,11 +398,15 @@ int qh_decode_kernel_time(qh_model* m, qh_cache* c, int32_t role, int32_t reps, 
 int qh_decode_kernel_time_cold(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
                                float* us_per_launch, int32_t* copies);
 /* qh_decode_kernel_time_cold with the launch's grid sized for streaming instead of for one
- * step's latency: blocks_per_copy blocks per copy (matrix roles; 0 = the step's own grid), each
- * staging its activation vector once and then walking many rows with the next rows' loads in
- * flight -- the same kernel and arithmetic as the step (the decode kernel's multi-item form, as
- * the output head runs in the step), showing what it streams when its grid is not bound by
- * latency. No counterpart in the reference. */
+ * step's latency (matrix roles; blocks_per_copy 0 = the step's own grid): each block stages its
+ * activation vector once and then walks many rows with the next rows' loads in flight, in the
+ * decode kernel's multi-item forms -- down and the head blocks_per_copy blocks per copy; q|k|v,
+ * o-proj and gate|up as one flat list over the device's resident blocks (blocks_per_copy does
+ * not change that grid), their epilogues batched per group of rows. q|k|v copies append their
+ * key/value rows to scratch rows of their own, not to the cache. Every row is summed as the
+ * step sums it: the call checks the first and the last copy's outputs against the step's own
+ * launch shape bit for bit and fails with QH_ERR_STATE if they differ. Shows what the step's
+ * kernels stream when latency does not size their grid. No counterpart in the reference. */
 int qh_decode_kernel_time_stream(qh_model* m, qh_cache* c, int32_t role, size_t min_bytes, int32_t reps,
                                  int32_t blocks_per_copy, float* us_per_launch, int32_t* copies);
 /* What bounds a batch-1 launch, measured on this device (no counterpart in the reference, which
