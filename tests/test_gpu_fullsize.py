@@ -163,8 +163,9 @@ def test_config5_512_prefill_batched_and_mfma_match_oracle(ctx, hip, full_ckpt):
       - batched: logits within 1e-4 of the oracle's own prefill (bitwise equal to one decode
         step per position, tested elsewhere);
       - MFMA: within 1e-4 of the same-f16 oracle (the oracle attending to the MFMA run's own
-        cache rows), same argmax; its distance from the independent oracle is reported, and
-        the same-f16 comparison of the batched path is given beside it;
+        cache rows), same argmax; and within 1e-4 of the independent oracle too (observed
+        ~4.5e-5), so a drift of the contraction's error shows here; the same-f16 comparison of
+        the batched path is given beside it;
       - both: every layer's stored f16 K/V within half an f16 unit of the CPU's value."""
     cfg = hip.QWEN25_05B
     P = 512
@@ -192,6 +193,7 @@ def test_config5_512_prefill_batched_and_mfma_match_oracle(ctx, hip, full_ckpt):
         assert res[mode][1] <= LOGIT_REL
         same_f16_layers(cfg, c, same, P, f"config5 {mode}")
     assert res["batched"][0] <= LOGIT_REL
+    assert res["mfma"][0] <= LOGIT_REL
     for _, c in runs.values():
         c.destroy()
     model.destroy()
