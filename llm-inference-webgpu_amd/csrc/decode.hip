@@ -561,24 +561,24 @@ static hipError_t fused_l(hipStream_t s, FusedArgs a, int items, int max_blocks)
   if constexpr (GRID == GRID_GROUP) {
     if (a.list_count > 1 && (size_t)a.list_count * a.list_w < ((size_t)1 << 31) &&
         (size_t)a.list_count * a.list_s * sizeof(float) < ((size_t)1 << 31)) {
-    // A weight list on the grouped loop runs flat: as many blocks as the device holds at
-    // once share all the copies' items equally (one block per copy leaves the copies'
-    // blocks outnumbering the resident slots by a fraction, and the last round runs on
-    // part of the device).
-    const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
-                           : (size_t)a.w.cols * sizeof(double);
-    auto kernel = k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_GROUP, F32>;
-    int dev = 0, cus = 0, per_cu = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, lds);
-    if (e != hipSuccess) return e;
-    const size_t total = (size_t)items * a.list_count, teams = T::kTeams;
-    const size_t resident = std::max(1, cus * per_cu);
-    const size_t per = ((total + resident - 1) / resident + teams - 1) / teams * teams;
-    a.list_flat = (int)per;
-    hipLaunchKernelGGL(kernel, dim3((total + per - 1) / per, 1), dim3(kBlock), lds, s, a);
-    return hipGetLastError();
+      // A weight list on the grouped loop runs flat: as many blocks as the device holds at
+      // once share all the copies' items equally (one block per copy leaves the copies'
+      // blocks outnumbering the resident slots by a fraction, and the last round runs on
+      // part of the device).
+      const size_t lds = F32 ? (size_t)staged_f32_floats(a.w.cols, a.w.nchunks) * sizeof(float)
+                             : (size_t)a.w.cols * sizeof(double);
+      auto kernel = k_fused<FMT, TL, R, KC, PRO, EPI, LOOP_GROUP, F32>;
+      int dev = 0, cus = 0, per_cu = 0;
+      hipError_t e = hipGetDevice(&dev);
+      if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, lds);
+      if (e != hipSuccess) return e;
+      const size_t total = (size_t)items * a.list_count, teams = T::kTeams;
+      const size_t resident = std::max(1, cus * per_cu);
+      const size_t per = ((total + resident - 1) / resident + teams - 1) / teams * teams;
+      a.list_flat = (int)per;
+      hipLaunchKernelGGL(kernel, dim3((total + per - 1) / per, 1), dim3(kBlock), lds, s, a);
+      return hipGetLastError();
     }
   }
   const int blocks = fused_blocks(items, T::kTeams, max_blocks);
