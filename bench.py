@@ -63,6 +63,7 @@ sys.path.insert(0, os.path.join(ROOT, "llm-inference-webgpu_amd"))
 import qwen_hip as H  # noqa: E402
 
 PEAK_HBM_GBS = 8000.0
+PROBE_AFTER = 64  # the roofline probe's row: this many positions past the prompt (at most the timed steps)
 LOGIT_REL = 1e-4        # test/model.test.js:40; web/scaling.html:122-127 holds its non-bitwise path to it
 METRIC = "batch-1 decode tok/s, Qwen2.5-0.5B int4/int8; matvec HBM GB/s vs peak"
 
@@ -793,11 +794,13 @@ def main():
     tok_s = args.steps / (ms / 1e3)
     log(f"decode: {args.steps} steps in {ms:.2f} ms (events), {wall * 1e3:.2f} ms (wall): {tok_s:.0f} tok/s")
 
-    # Each role's own launches probed at the row after the timed tokens (they append K/V at
-    # their position, so the rows the decode stored stay as decoded): 240 of the step's launches
-    # of it back to back on the library's stream between two events (no event between launches;
-    # its 24 weight sets cache-resident), then one launch cold over >= 512 MiB of copies.
-    probe = args.context + args.steps
+    # Each role's own launches probed at a fixed row, the 65th after the prompt whatever the
+    # number of timed tokens (so the line and the committed traces, taken over 64 steps, describe
+    # the same launch; the rows the decode stored below it stay as decoded, since a role launch
+    # appends K/V at its own position only): 240 of the step's launches of it back to back on the
+    # library's stream between two events (no event between launches; its 24 weight sets
+    # cache-resident), then one launch cold over >= 512 MiB of copies.
+    probe = args.context + min(args.steps, PROBE_AFTER)
     cache.length = probe
     back_to_back = {r: round(model.kernel_time(cache, r, 240), 3)
                     for r in ("qkv", "attention", "oproj", "gateup", "down", "head")}
