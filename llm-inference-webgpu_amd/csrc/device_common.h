@@ -434,32 +434,38 @@ constexpr int kLoadNonTemporal = 2;          // the load's cache policy: streame
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* p, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)(uint32_t)bytes, kRawBufferWord3);
 }
-__device__ __forceinline__ BufMat buf_mat(const DMat& m) {
-  const size_t n = (size_t)m.rows * (m.format == QH_FMT_INT4 ? m.gpr : 1) * sizeof(float);
+// The matrix, or `copies` copies of it laid out copy_w bytes (data) and copy_s floats
+// (scales, zero points) apart.
+__device__ __forceinline__ BufMat buf_mat(const DMat& m, int copies = 1, size_t copy_w = 0, size_t copy_s = 0) {
+  const size_t n = (size_t)m.rows * (m.format == QH_FMT_INT4 ? m.gpr : 1);
+  const size_t nw = (size_t)m.rows * m.row_bytes;
+  const size_t ns = ((size_t)(copies - 1) * copy_s + n) * sizeof(float);
   BufMat b;
-  b.data = raw_buffer(m.data, (size_t)m.rows * m.row_bytes);
-  b.scales = raw_buffer(m.scales, m.format == QH_FMT_F16 ? 0 : n);
-  b.zeros = raw_buffer(m.zeros, m.format == QH_FMT_INT4 ? n : 0);
+  b.data = raw_buffer(m.data, (size_t)(copies - 1) * copy_w + nw);
+  b.scales = raw_buffer(m.scales, m.format == QH_FMT_F16 ? 0 : ns);
+  b.zeros = raw_buffer(m.zeros, m.format == QH_FMT_INT4 ? ns : 0);
   return b;
 }
 
 // wtile_load through buffer resources, for rows that may lie past the matrix (a loop
 // over rows that loads ahead): no clamping, 32-bit offsets, and what lies past the end
 // reads as zeros (those rows' sums are never used; nor are chunks past a row's end).
+// wbase / sbase: byte offsets of the matrix's data and scales inside the resources.
 template <int FMT, int R, int KC, int TL>
 __device__ __forceinline__ void wtile_load_buf(const DMat& m, const BufMat& b, const int (&rows)[R], int tl,
-                                               WTile<FMT, R, KC>& t) {
+                                               int wbase, int sbase, WTile<FMT, R, KC>& t) {
 #pragma unroll
   for (int k = 0; k < KC; k++) {
     const int c = tl + k * TL;
 #pragma unroll
     for (int i = 0; i < R; i++)
-      t.w[k][i] = __builtin_amdgcn_raw_buffer_load_b128(b.data, rows[i] * m.row_bytes + 16 * c, 0, kLoadNonTemporal);
+      t.w[k][i] =
+          __builtin_amdgcn_raw_buffer_load_b128(b.data, wbase + rows[i] * m.row_bytes + 16 * c, 0, kLoadNonTemporal);
     if constexpr (FMT == QH_FMT_INT4) {
       const int g = c / m.cpg;
 #pragma unroll
       for (int i = 0; i < R; i++) {
-        const int off = (rows[i] * m.gpr + g) * (int)sizeof(float);
+        const int off = sbase + (rows[i] * m.gpr + g) * (int)sizeof(float);
         t.s[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.scales, off, 0, 0));
         t.z[k][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.zeros, off, 0, 0));
       }
@@ -468,7 +474,7 @@ __device__ __forceinline__ void wtile_load_buf(const DMat& m, const BufMat& b, c
   if constexpr (FMT == QH_FMT_INT8) {
 #pragma unroll
     for (int i = 0; i < R; i++)
-      t.s[0][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.scales, rows[i] * 4, 0, 0));
+      t.s[0][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b.scales, sbase + rows[i] * 4, 0, 0));
   }
 }
 
