@@ -165,6 +165,30 @@ __device__ __forceinline__ uint32_t code_int4(float x, double inverse, double ze
   return (uint32_t)min(max(round_away(t) + (int)zero, 0), 15);
 }
 
+// The same codes from an f32 product where that is safe. t32 = x * f32(inverse) differs from
+// the f64 product t the expressions above round by at most |t| 2^-23 (the two roundings to f32,
+// 2^-24 each relative; f32(inverse) is never subnormal: |x| < 2^128 bounds the scale), and
+// |t| <= 16 (int4) or 128 (int8). So wherever t32 lies farther than kSafe from every
+// half-integer, t rounds half away from zero to the integer nearest t32; nearer a half-integer,
+// and for NaN or an infinite t32, the f64 expression decides. The codes are those of the f64
+// expressions bit for bit, at a fraction of their arithmetic.
+constexpr float kSafeInt4 = 0x1p-16f;  // > 16 * 2^-23
+constexpr float kSafeInt8 = 0x1p-13f;  // > 128 * 2^-23
+__device__ __forceinline__ int code_int8_f32(float x, float inv32, double inverse) {
+#pragma clang fp contract(off)
+  const float t = x * inv32;
+  const float r = __builtin_rintf(t);
+  if (!(fabsf(t - r) <= 0.5f - kSafeInt8)) return code_int8(x, inverse);
+  return (int)fminf(fmaxf(r, -127.f), 127.f);
+}
+__device__ __forceinline__ uint32_t code_int4_f32(float x, float inv32, double inverse, double zero, float zf) {
+#pragma clang fp contract(off)
+  const float t = x * inv32;
+  const float r = __builtin_rintf(t);
+  if (!(fabsf(t - r) <= 0.5f - kSafeInt4)) return code_int4(x, inverse, zero);
+  return (uint32_t)fminf(fmaxf(r + zf, 0.f), 15.f);  // r and the zero point are small integers: exact
+}
+
 // src/core/quantize.js:36-58, one wave per row, four rows per block; MAXC chunks per lane.
 template <bool BF16, int MAXC>
 __global__ __launch_bounds__(kQBlock) void k_quant_int8_rows(const void* __restrict__ src, int rows, int cols,
@@ -188,6 +212,7 @@ __global__ __launch_bounds__(kQBlock) void k_quant_int8_rows(const void* __restr
   const double scale = (double)peak / 127;
   if (lane == 0) scales[row] = (float)scale;
   const double inverse = 1 / scale;
+  const float inv32 = (float)inverse;
   int8_t* out = q + (size_t)row * cols;
 #pragma unroll
   for (int k = 0; k < MAXC; k++) {
@@ -196,7 +221,7 @@ __global__ __launch_bounds__(kQBlock) void k_quant_int8_rows(const void* __restr
     uint32_t w[C::kVals / 4];
 #pragma unroll
     for (int j = 0; j < C::kVals; j++) {
-      const uint32_t b = scale != 0 ? (uint32_t)(uint8_t)(int8_t)code_int8(C::at(c[k], j), inverse) : 0u;
+      const uint32_t b = scale != 0 ? (uint32_t)(uint8_t)(int8_t)code_int8_f32(C::at(c[k], j), inv32, inverse) : 0u;
       if (j % 4 == 0) w[j / 4] = b;
       else w[j / 4] |= b << (8 * (j % 4));
     }
@@ -251,10 +276,11 @@ __global__ __launch_bounds__(kQBlock) void k_quant_int4_rows(const void* __restr
       zeros[gi] = (float)zero;
     }
     const double inverse = 1 / scale;
+    const float inv32 = (float)inverse, zf = (float)zero;
     uint32_t w = 0;
     if (scale != 0) {
 #pragma unroll
-      for (int j = 0; j < C::kVals; j++) w |= code_int4(C::at(c[k], j), inverse, zero) << (4 * j);
+      for (int j = 0; j < C::kVals; j++) w |= code_int4_f32(C::at(c[k], j), inv32, inverse, zero, zf) << (4 * j);
     }
     if constexpr (BF16) *reinterpret_cast<uint32_t*>(out + (size_t)ci * 4) = w;
     else *reinterpret_cast<uint16_t*>(out + (size_t)ci * 2) = (uint16_t)w;

@@ -33,6 +33,22 @@ def planted_f32(rows, cols, seed):
     w[9, :] = np.float32(1e-44) * np.sign(w[9, :])   # f32 scale underflows, f64 scale does not
     w[10, :] = np.abs(w[10, :])           # one-signed rows / groups
     w[11, :] = -np.abs(w[11, :])
+    if rows > 15:
+        # Products exactly on a half-integer, rounded half away from zero (k + 1/2 is exact in
+        # bf16 too): int8, a row peak of 127 makes the scale 1 (row 13); int4, every group of
+        # 16 or more aligned elements spanning 0 .. 15 does (row 15).
+        ties = np.arange(cols) % 32 - 15.5
+        ties[::32] = 127.0
+        w[13, :] = ties
+        span = np.arange(cols) % 16 - 1.5
+        span[::16] = 0.0
+        span[1::16] = 15.0
+        w[15, :] = span
+        # A scale of 3 (peak 381), whose inverse is inexact in f32 and f64 alike: odd multiples
+        # of 1.5 give products on, or within rounding of, k + 1/2 in both.
+        odd = 1.5 * (2 * (np.arange(cols) % 40) - 39)
+        odd[::40] = 381.0
+        w[14, :] = odd
     return w
 
 
