@@ -38,3 +38,23 @@ def test_streaming_grids_match_the_step_launch(ctx, hip, fmt, numerics, hidden, 
     a.destroy()
     b.destroy()
     model.destroy()
+
+
+def test_streaming_grids_outside_the_flat_list(ctx, hip):
+    """The grouped loop's other branch, one copy per grid row: a list of one copy, and a list
+    whose weight bytes pass the 2 GiB a flat list's 32-bit buffer offsets reach (2.5 GiB of
+    q|k|v copies, 286,720 weight bytes each). Both checked by the library against the step's
+    launch shape as above."""
+    cfg = hip.ModelConfig(hidden=640, intermediate=1280, layers=1, heads=10, kv_heads=2, vocab=1000)
+    ckpt = hip.synthesize_checkpoint(cfg, seed=22)
+    model = hip.GpuModel.load(ctx, hip.device_tensors(ckpt, cfg, "int4", 128, "int8"), cfg, maxPositions=64)
+    c = model.newCache(48)
+    model.forward_tokens(hip.synth_tokens(22, "stream.one", cfg.vocab, 20), c)
+    for role in ("qkv", "oproj", "gateup"):
+        us, copies = model.kernel_time_stream(c, role, 2, 1, 1)
+        assert us > 0 and copies == 1, (role, us, copies)
+    us, copies = model.kernel_time_stream(c, "qkv", 2, 5 << 29, 1)
+    print(f"qkv over {copies} copies: {us:.1f} us")
+    assert us > 0 and copies * (896 * 320) >= 1 << 31, copies
+    c.destroy()
+    model.destroy()
