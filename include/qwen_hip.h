@@ -335,14 +335,17 @@ int qh_forward(qh_model* m, qh_cache* c, const float* h_hidden, int32_t seq, flo
 /* As qh_forward, with the embedding gather done on the device from token ids. */
 int qh_forward_tokens(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t seq,
                       float* h_logits, int32_t* h_argmax);
-/* Greedy decode (the loop of web/bench.html:121-134) as `steps` replays of a hipGraph-captured
- * decode step: token -> gather -> 24 layers -> lm_head -> argmax -> next token, all on the device.
- * h_tokens [steps] receives the generated ids; the first step consumes `first_token`. */
+/* Greedy decode (the loop of web/bench.html:121-134) as `steps` replays of hipGraph-captured
+ * decode steps: token -> gather -> 24 layers -> lm_head -> argmax -> next token, all on the
+ * device (each step's argmax and the next token's gather made by the next step's first launch,
+ * the last step's by a launch of its own). h_tokens [steps] receives the generated ids; the
+ * first step consumes `first_token`. */
 int qh_decode(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps, int32_t* h_tokens);
 /* Enqueue the graph replays without waiting (for timing); qh_decode_collect waits and copies. */
 int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t steps);
 int qh_decode_collect(qh_model* m, qh_cache* c, int32_t steps, int32_t* h_tokens);
-/* Captures and uploads the cache's decode graphs (one step, and a run of 8 steps) now instead
+/* Captures and uploads the cache's decode graphs (a first step, one later step, and a run of 8
+ * later steps) now instead
  * of at the first decode that needs them, so a timed decode replays graphs that are already
  * resident. Optional: qh_decode_launch captures whatever is missing. No counterpart in the
  * reference, which records every step anew (src/gpu/model.js:261). */

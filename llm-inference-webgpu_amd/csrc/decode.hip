@@ -32,7 +32,9 @@
 
 namespace qh {
 
-enum { PRO_RMSNORM = 0, PRO_COPY = 1, PRO_COMBINE = 2 };
+// PRO_PICK: rmsnorm of the embedding row of the token that the previous step's head picked
+// (the pick of k_pick, made in the prologue of the step's first launch).
+enum { PRO_RMSNORM = 0, PRO_COPY = 1, PRO_COMBINE = 2, PRO_PICK = 3 };
 enum { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 struct FusedArgs {
@@ -55,6 +57,17 @@ struct FusedArgs {
   int capacity;
   // EPI_LOGITS
   ArgPair* partials;     // [blocks]: each block's best (value, index)
+  int* advance;          // the decode state whose position the step's head advances, or null
+  // PRO_PICK: the previous step's head partials and first logit, the step's tokens and
+  // predictions, the embedding, and x (written by block 0: the residual the layer adds to)
+  const ArgPair* pick_parts;
+  int pick_nparts;
+  const float* pick_logits;
+  int* tokens;
+  int* pred;
+  int vocab;
+  const uint16_t* embed;
+  float* x;
   int f32;              // fast numerics: the f32 matvec core
   // PRO_COMBINE: `in` holds the attention slot partials of the current position
   // A list of list_count copies of the weights, one per blockIdx.y (the launch timed over a
@@ -237,6 +250,69 @@ struct Item {
   }
 };
 
+constexpr int kLmRows = 4;          // rows per team in the output head
+constexpr int kLmMaxBlocks = 1024;  // the head's blocks (see fused_blocks)
+constexpr int kPickLoads = 4;       // partial loads per thread of a pick
+static_assert(kLmMaxBlocks <= kPickLoads * kBlock, "one round of partial loads");
+
+// The pick that ends a step with logits, from its output head's block partials: the token is
+// the best of them (lowest index among equal maxima, NaN logits -> 0, the reference's
+// host-side scan of src/gpu/model.js:372-382). The head has advanced the position to
+// q = state[0], so the pick is the prediction at q - 1 (recorded in pred) and, from the
+// forced length on, the token at q; the next input is the caller's token at q below the
+// forced length, else the pick. Block-wide: every thread of the block takes part.
+struct Pick {
+  ArgPair part[kPickLoads];
+  int q, forced, given;
+  float first;
+  // Every load that does not depend on the argmax: all the partials at once (from clamped
+  // indices -- a repeated pair does not change the best), the position, the forced length,
+  // the caller's token at q and the first logit.
+  __device__ __forceinline__ void load(const ArgPair* __restrict__ parts, int nparts, const float* __restrict__ logits,
+                                       const int* state, const int* tokens, int capacity) {
+#pragma unroll
+    for (int k = 0; k < kPickLoads; k++) part[k] = parts[min((int)threadIdx.x + k * kBlock, nparts - 1)];
+    q = state[0];
+    forced = state[1];
+    given = tokens[min(q, capacity)];
+    first = logits[0];
+  }
+  // The next input token, known to every thread after one barrier (`red`: a pair per wave,
+  // each thread reducing the waves' bests); `record`: this block writes pred and tokens.
+  __device__ __forceinline__ int finish(ArgPair* red, bool record, int* pred, int* tokens, int capacity,
+                                        int vocab) const {
+    float v = part[0].v;
+    int i = part[0].i;
+#pragma unroll
+    for (int k = 1; k < kPickLoads; k++) {
+      if (argmax_better(part[k].v, part[k].i, v, i)) {
+        v = part[k].v;
+        i = part[k].i;
+      }
+    }
+    argmax_wave(v, i);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = {v, i};
+    __syncthreads();
+    v = red[0].v;
+    i = red[0].i;
+#pragma unroll
+    for (int w = 1; w < kBlock / kWave; w++) {
+      if (argmax_better(red[w].v, red[w].i, v, i)) {
+        v = red[w].v;
+        i = red[w].i;
+      }
+    }
+    const int tok = (first != first) ? 0 : i;
+    if (record && threadIdx.x == 0) {
+      if (q >= 1 && q - 1 < capacity) pred[q - 1] = tok;
+      if (q >= forced && q <= capacity) tokens[q] = tok;
+    }
+    const bool caller = q < forced && q <= capacity;
+    const int t = caller ? given : tok;
+    return (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
+  }
+};
+
 // How a team walks its items (k_fused's LOOP): one item; a ring of two buffers over
 // all of them, each item's epilogue on lane 0; groups of kLoopGroup items whose
 // epilogues run together.
@@ -268,6 +344,7 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   __shared__ typename std::conditional<F32, float, double>::type
       gsum[kGroup ? kBlock / TL : 1][kGroup ? kLoopGroup : 1][R];
   __shared__ float wl[PRO == PRO_COMBINE ? kBlock : 1];
+  __shared__ ArgPair pick_red[PRO == PRO_PICK ? kBlock / kWave : 1];
   using Acc = typename std::conditional<F32, float, double>::type;
   using T = Teams<TL>;
   if (blockIdx.y) {  // a copy of a weight list (block-uniform; never in the decode step)
@@ -285,27 +362,47 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   int it = blockIdx.x * T::kTeams + T::team();
   int pos = 0;
   if constexpr (EPI == EPI_QKV) pos = a.state[0];
+  if constexpr (EPI == EPI_LOGITS) {
+    // The step's head moves the position on (no block of this launch reads it).
+    if (a.advance && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) a.advance[0] = a.advance[0] + 1;
+  }
 
   // Loads in this order: the activations (the previous launch's output), then this
   // team's first item -- vector loads return in issue order, so the staging below
   // waits for the activations only, while the weights are still in flight.
+  // PRO_PICK: the pick's loads, then the weights, then its token's row once the partials
+  // are reduced (the row's wait then covers the weights too, issued a round trip earlier).
   using Pro = typename std::conditional<PRO == PRO_COMBINE, CombineIn, StageIn>::type;
   Pro pin;
-  if constexpr (PRO == PRO_COMBINE) pin.load(a.in, a.heads);
-  else pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
+  [[maybe_unused]] Pick pk;
+  if constexpr (PRO == PRO_COMBINE) {
+    pin.load(a.in, a.heads);
+  } else if constexpr (PRO == PRO_PICK) {
+    pk.load(a.pick_parts, a.pick_nparts, a.pick_logits, a.state, a.tokens, a.capacity);
+    pin.load_gain(a.gain, a.w.cols);
+  } else {
+    pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
+  }
   Item<FMT, TL, R, KC, EPI> ring[NBUF];
   if constexpr (!kGroup) ring[0].template load<true>(a, it, pos, lane);
+  if constexpr (PRO == PRO_PICK) {
+    const bool first_block = blockIdx.x == 0 && blockIdx.y == 0;
+    const int t = pk.finish(pick_red, first_block, a.pred, a.tokens, a.capacity, a.vocab);
+    pin.load_bf16(a.embed + (size_t)t * a.w.cols, a.w.cols);
+    if (first_block) pin.store(a.x, a.w.cols);
+  }
+  constexpr bool kNorm = PRO == PRO_RMSNORM || PRO == PRO_PICK;
   if constexpr (F32) {
     float* xs = reinterpret_cast<float*>(smem);
     const XLayoutF lay = chunk_layout_f<FMT>(a.w.nchunks);
-    if constexpr (PRO == PRO_RMSNORM)
+    if constexpr (kNorm)
       stage_rmsnorm_finish_f32<FMT>(pin, (float)a.eps, a.w.cols, xs, reinterpret_cast<float*>(red), lay);
     else if constexpr (PRO == PRO_COMBINE) stage_attn_combine_f32<FMT>(pin, a.heads, xs, lay, wl);
     else stage_copy_finish_f32<FMT>(pin, a.w.cols, xs, lay);
   } else {
     double* xs = smem;
     const XLayout lay = chunk_layout<FMT>(a.w.nchunks);
-    if constexpr (PRO == PRO_RMSNORM) stage_rmsnorm_finish(pin, a.eps, a.w.cols, xs, red, lay);
+    if constexpr (kNorm) stage_rmsnorm_finish(pin, a.eps, a.w.cols, xs, red, lay);
     else if constexpr (PRO == PRO_COMBINE) stage_attn_combine(pin, a.heads, xs, lay, wl);
     else stage_copy_finish(pin, a.w.cols, xs, lay);
   }
@@ -447,63 +544,18 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
   }
 }
 
-constexpr int kLmRows = 4;          // rows per team in the output head
-constexpr int kLmMaxBlocks = 1024;  // the head's blocks (see fused_blocks)
-constexpr int kPickLoads = 4;       // partial loads per thread of k_pick
-
-// The end of a step with logits: the best of the head's block partials is the
-// token (lowest index among equal maxima, NaN logits -> 0, the reference's
-// host-side scan of src/gpu/model.js:372-382); it is recorded, the position
-// advances, and x becomes the embedding of the next position's token -- the
-// caller's below the forced length, else this one -- so the next step needs no
-// gather launch of its own.
+// The pick ending a step whose next step does not make it in its first launch (a decode
+// call's last step, a prefill with logits, a scored position): the Pick above, and x becomes
+// the embedding of the next input token.
 __global__ __launch_bounds__(kBlock) void k_pick(const ArgPair* __restrict__ partials, int nparts,
-                                                 const float* __restrict__ logits, int* state,
+                                                 const float* __restrict__ logits, const int* state,
                                                  int* tokens, int* pred, int capacity,
                                                  const uint16_t* __restrict__ embed, int hidden,
                                                  int vocab, float* __restrict__ x) {
-  static_assert(kLmMaxBlocks <= kPickLoads * kBlock, "one round of partial loads");
   __shared__ ArgPair wred[kBlock / kWave];
-  // Every load that does not depend on the argmax is issued first: the partials (all
-  // of them at once, from clamped indices -- a repeated pair does not change the
-  // best), the position, the forced length and the caller's token at the next position.
-  ArgPair q[kPickLoads];
-#pragma unroll
-  for (int k = 0; k < kPickLoads; k++) q[k] = partials[min((int)threadIdx.x + k * kBlock, nparts - 1)];
-  const int p = state[0], forced = state[1];
-  const bool caller = p + 1 < forced && p + 1 <= capacity;  // the next input is the caller's token
-  const int given = tokens[min(p + 1, capacity)];
-  const float first = logits[0];
-  float v = q[0].v;
-  int i = q[0].i;
-#pragma unroll
-  for (int k = 1; k < kPickLoads; k++) {
-    if (argmax_better(q[k].v, q[k].i, v, i)) {
-      v = q[k].v;
-      i = q[k].i;
-    }
-  }
-  // The block's best, known to every thread after one barrier (each reduces the waves' bests).
-  argmax_wave(v, i);
-  if ((threadIdx.x & (kWave - 1)) == 0) wred[threadIdx.x / kWave] = {v, i};
-  __syncthreads();
-  v = wred[0].v;
-  i = wred[0].i;
-#pragma unroll
-  for (int w = 1; w < kBlock / kWave; w++) {
-    if (argmax_better(wred[w].v, wred[w].i, v, i)) {
-      v = wred[w].v;
-      i = wred[w].i;
-    }
-  }
-  const int tok = (first != first) ? 0 : i;
-  if (threadIdx.x == 0) {
-    if (p < capacity) pred[p] = tok;
-    if (p + 1 >= forced && p + 1 <= capacity) tokens[p + 1] = tok;
-    state[0] = p + 1;
-  }
-  int t = caller ? given : tok;
-  t = (t < 0 || t >= vocab) ? 0 : t;  // ids are validated on the host
+  Pick pk;
+  pk.load(partials, nparts, logits, state, tokens, capacity);
+  const int t = pk.finish(wred, true, pred, tokens, capacity, vocab);
   const uint16_t* row = embed + (size_t)t * hidden;
   for (int k = threadIdx.x; k < hidden; k += kBlock) x[k] = __builtin_bit_cast(float, (uint32_t)row[k] << 16);
 }
@@ -681,9 +733,10 @@ static void apply_list(FusedArgs& f, const RoleList* list) {
 }
 
 // The launch of `role` (QKV, ATTENTION, OPROJ, GATEUP or DOWN) for layer L; with `list`, the
-// same launch over a list of copies of its weights (matrix roles only).
+// same launch over a list of copies of its weights (matrix roles only); `pick` (QKV): the
+// previous step's pick made in this launch's prologue, its input row the picked token's.
 static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int L, int role,
-                             const RoleList* list = nullptr) {
+                             const RoleList* list = nullptr, bool pick = false) {
   // A streaming grid (blocks per copy given) takes more rows per work item where that helps: each
   // team then walks many items, and the rows of one item share its loop overhead. A row is
   // summed in the same order either way (its chunks per lane and the butterfly depend on the
@@ -717,6 +770,18 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
       apply_list(f, list);
       if (stream)
         return fused<4, PRO_RMSNORM, EPI_QKV, GRID_GROUP>(s, f, ((m.heads + m.kv_heads) * 64 + kv_dim) / 4, mb);
+      if (pick) {
+        if (list) return hipErrorInvalidValue;
+        f.pick_parts = static_cast<const ArgPair*>(c.lm_partials);
+        f.pick_nparts = lm_head_blocks(m);
+        f.pick_logits = c.logits;
+        f.tokens = c.tokens;
+        f.pred = c.pred;
+        f.vocab = m.vocab;
+        f.embed = m.embed;
+        f.x = c.x;
+        return fused<2, PRO_PICK, EPI_QKV, GRID_ONE>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2, mb);
+      }
       return fused<2, PRO_RMSNORM, EPI_QKV, GRID_ONE>(s, f, (m.heads + m.kv_heads) * 32 + kv_dim / 2, mb);
     case QH_ROLE_ATTENTION:
       if (m.numerics == QH_NUMERICS_FAST) {
@@ -796,8 +861,10 @@ static hipError_t layer_role(hipStream_t s, const ModelDev& m, const CacheDev& c
   }
 }
 
-// The output head's matvec alone (final rmsnorm, lm_head, logits, block argmax partials).
-static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c, const RoleList* list = nullptr) {
+// The output head's matvec alone (final rmsnorm, lm_head, logits, block argmax partials);
+// `advance`: the step's head, which moves the position on for the pick that follows.
+static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& c, const RoleList* list = nullptr,
+                              bool advance = false) {
   FusedArgs f{};
   f.f32 = m.numerics == QH_NUMERICS_FAST;
   f.eps = m.eps;
@@ -806,6 +873,7 @@ static hipError_t head_matvec(hipStream_t s, const ModelDev& m, const CacheDev& 
   f.gain = m.final_norm;
   f.out = c.logits;
   f.partials = static_cast<ArgPair*>(c.lm_partials);
+  if (advance && !list) f.advance = c.state;
   apply_list(f, list);
   const int mb = list && list->max_blocks > 0 ? std::min(list->max_blocks, kLmMaxBlocks) : kLmMaxBlocks;
   return fused<kLmRows, PRO_RMSNORM, EPI_LOGITS, GRID_ANY>(s, f, (m.vocab + kLmRows - 1) / kLmRows, mb);
@@ -842,7 +910,7 @@ hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int
 }
 
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
-                        bool logits, StepTimer* timer) {
+                        bool logits, StepTimer* timer, bool defer_pick) {
   hipError_t e;
   if (in == STEP_GATHER) {
     if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
@@ -850,14 +918,18 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
   }
   for (int L = 0; L < m.layers; L++) {
     for (int role : {QH_ROLE_QKV, QH_ROLE_ATTENTION, QH_ROLE_OPROJ, QH_ROLE_GATEUP, QH_ROLE_DOWN}) {
+      const bool pick = in == STEP_PICK && L == 0 && role == QH_ROLE_QKV;
       if ((e = mark(s, timer, role)) != hipSuccess) return e;
-      if ((e = layer_role(s, m, c, L, role)) != hipSuccess) return e;
+      if ((e = layer_role(s, m, c, L, role, nullptr, pick)) != hipSuccess) return e;
     }
   }
   if (!logits) {
     if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
     hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, c.state);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+  } else if (defer_pick) {
+    if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
+    if ((e = head_matvec(s, m, c, nullptr, true)) != hipSuccess) return e;
   } else if ((e = enqueue_head(s, m, c, timer)) != hipSuccess) {
     return e;
   }
@@ -867,9 +939,13 @@ hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, Ste
 hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer) {
   hipError_t e;
   if ((e = mark(s, timer, QH_ROLE_HEAD)) != hipSuccess) return e;
-  if ((e = head_matvec(s, m, c)) != hipSuccess) return e;
+  if ((e = head_matvec(s, m, c, nullptr, true)) != hipSuccess) return e;
   // The pick gathers the next input row, so it is timed with the gathers.
   if ((e = mark(s, timer, QH_ROLE_EMBED)) != hipSuccess) return e;
+  return enqueue_pick(s, m, c);
+}
+
+hipError_t enqueue_pick(hipStream_t s, const ModelDev& m, const CacheDev& c) {
   hipLaunchKernelGGL(k_pick, dim3(1), dim3(kBlock), 0, s, static_cast<const ArgPair*>(c.lm_partials),
                      lm_head_blocks(m), c.logits, c.state, c.tokens, c.pred, c.capacity, m.embed, m.hidden,
                      m.vocab, c.x);

@@ -795,6 +795,37 @@ struct StageIn {
       }
     }
   }
+  // The gain alone; x follows from load_bf16 once its row is known.
+  __device__ __forceinline__ void load_gain(const float* __restrict__ gain, int n) {
+    const int n4 = n >> 2;
+#pragma unroll
+    for (int j = 0; j < kStageVec; j++) {
+      const int i = threadIdx.x + j * kBlock;
+      if (i < n4) g[j] = reinterpret_cast<const v4f*>(gain)[i];
+    }
+  }
+  // x = the bf16 values of `row` widened exactly (row 8-byte aligned).
+  __device__ __forceinline__ void load_bf16(const uint16_t* __restrict__ row, int n) {
+    const int n4 = n >> 2;
+#pragma unroll
+    for (int j = 0; j < kStageVec; j++) {
+      const int i = threadIdx.x + j * kBlock;
+      if (i < n4) {
+        const uint2 u = reinterpret_cast<const uint2*>(row)[i];  // little-endian: element 4i in u.x's low half
+        v[j] = v4f{__builtin_bit_cast(float, u.x << 16), __builtin_bit_cast(float, u.x & 0xffff0000u),
+                   __builtin_bit_cast(float, u.y << 16), __builtin_bit_cast(float, u.y & 0xffff0000u)};
+      }
+    }
+  }
+  // x[0 .. n-1] = the staged values.
+  __device__ __forceinline__ void store(float* __restrict__ x, int n) const {
+    const int n4 = n >> 2;
+#pragma unroll
+    for (int j = 0; j < kStageVec; j++) {
+      const int i = threadIdx.x + j * kBlock;
+      if (i < n4) reinterpret_cast<v4f*>(x)[i] = v[j];
+    }
+  }
 };
 
 // xs = x / sqrt(mean(x^2) + eps) * gain as f64 values of the f32 result, with

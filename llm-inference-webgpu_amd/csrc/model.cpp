@@ -122,9 +122,11 @@ struct qh_cache {
   qh::CacheDev dev{};
   int length = 0;
   std::vector<void*> allocs;
-  hipGraph_t graph = nullptr;          // one carried decode step
+  hipGraph_t graph_first = nullptr;    // a decode call's first step: carried input, pick deferred
+  hipGraphExec_t exec_first = nullptr;
+  hipGraph_t graph = nullptr;          // one later step: the previous pick in its first launch
   hipGraphExec_t exec = nullptr;
-  hipGraph_t graph_run = nullptr;      // kGraphRun carried steps back to back
+  hipGraph_t graph_run = nullptr;      // kGraphRun such steps back to back
   hipGraphExec_t exec_run = nullptr;
   bool use_graph = true;  // false: decode enqueues every kernel directly
   bool busy = false;
@@ -638,6 +640,8 @@ int qh_cache_free(qh_cache* c) {
   QH_CHECK(!c->busy, QH_ERR_BUSY, "cache has a decode in flight; collect it first");
   hipSetDevice(c->m->ctx->device);
   hipStreamSynchronize(c->m->ctx->stream);
+  if (c->exec_first) hipGraphExecDestroy(c->exec_first);
+  if (c->graph_first) hipGraphDestroy(c->graph_first);
   if (c->exec) hipGraphExecDestroy(c->exec);
   if (c->graph) hipGraphDestroy(c->graph);
   if (c->exec_run) hipGraphExecDestroy(c->exec_run);
@@ -972,16 +976,20 @@ int qh_score(qh_model* m, qh_cache* c, const int32_t* h_ids, int32_t n, double* 
 
 constexpr int kGraphRun = 8;  // decode steps per replayed run graph
 
-// Captures the cache's decode graphs that are not captured yet: one carried step, and
-// (`run`) kGraphRun carried steps back to back. Each is uploaded to the device once, so
-// its first replay costs what every later one does.
+// A decode call of n steps: a gather of the first input row, a first step that takes it and
+// leaves its pick to the next step's first launch, n - 1 steps that make their predecessor's
+// pick in that launch and leave theirs to the next, and the last step's pick on its own.
+//
+// Captures the cache's decode graphs that are not captured yet: the first step, one later
+// step, and (`run`) kGraphRun later steps back to back. Each is uploaded to the device once,
+// so its first replay costs what every later one does.
 static int capture_graphs(qh_model* m, qh_cache* c, bool run) {
   hipStream_t s = m->ctx->stream;
-  auto capture = [&](int n, hipGraph_t* graph, hipGraphExec_t* exec) -> int {
+  auto capture = [&](int n, qh::StepInput in, hipGraph_t* graph, hipGraphExec_t* exec) -> int {
     QH_HIP(hipStreamSynchronize(s));
     QH_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed));
     hipError_t e = hipSuccess;
-    for (int i = 0; i < n && e == hipSuccess; i++) e = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true);
+    for (int i = 0; i < n && e == hipSuccess; i++) e = qh::enqueue_step(s, m->dev, c->dev, in, true, nullptr, true);
     hipGraph_t g = nullptr;
     hipError_t e2 = hipStreamEndCapture(s, &g);
     QH_HIP(e);
@@ -993,8 +1001,9 @@ static int capture_graphs(qh_model* m, qh_cache* c, bool run) {
     return QH_OK;
   };
   int rc = QH_OK;
-  if (!c->exec && (rc = capture(1, &c->graph, &c->exec))) return rc;
-  if (run && !c->exec_run && (rc = capture(kGraphRun, &c->graph_run, &c->exec_run))) return rc;
+  if (!c->exec_first && (rc = capture(1, qh::STEP_CARRIED, &c->graph_first, &c->exec_first))) return rc;
+  if (!c->exec && (rc = capture(1, qh::STEP_PICK, &c->graph, &c->exec))) return rc;
+  if (run && !c->exec_run && (rc = capture(kGraphRun, qh::STEP_PICK, &c->graph_run, &c->exec_run))) return rc;
   return QH_OK;
 }
 
@@ -1016,25 +1025,27 @@ int qh_decode_launch(qh_model* m, qh_cache* c, int32_t first_token, int32_t step
   if (rc) return rc;
   QH_HIP(hipSetDevice(m->ctx->device));
   hipStream_t s = m->ctx->stream;
-  // Carried steps are identical launches (position and tokens live on the device), so a
-  // graph of kGraphRun of them replays runs of steps with one launch each.
-  if (c->use_graph && (rc = capture_graphs(m, c, steps >= kGraphRun))) return rc;
+  // The steps after the first are identical launches (position and tokens live on the
+  // device), so a graph of kGraphRun of them replays runs of steps with one launch each.
+  if (c->use_graph && (rc = capture_graphs(m, c, steps - 1 >= kGraphRun))) return rc;
   c->h_pinned[3] = first_token;
   QH_HIP(hipMemcpyAsync(c->dev.tokens + c->length, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s));
   if ((rc = set_state(c, c->length, c->length + 1))) return rc;
-  // Each replayed step starts from the row its predecessor's pick gathered; the
-  // first starts from this gather.
+  // The launches of capture_graphs' decode call.
   QH_HIP(qh::enqueue_gather(s, m->dev, c->dev));
-  for (int i = 0; i < steps;) {
+  if (c->use_graph) QH_HIP(hipGraphLaunch(c->exec_first, s));
+  else QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true, nullptr, true));
+  for (int i = 1; i < steps;) {
     if (c->use_graph && steps - i >= kGraphRun) {
       QH_HIP(hipGraphLaunch(c->exec_run, s));
       i += kGraphRun;
       continue;
     }
     if (c->use_graph) QH_HIP(hipGraphLaunch(c->exec, s));
-    else QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true));
+    else QH_HIP(qh::enqueue_step(s, m->dev, c->dev, qh::STEP_PICK, true, nullptr, true));
     i++;
   }
+  QH_HIP(qh::enqueue_pick(s, m->dev, c->dev));
   c->busy = true;
   c->pending_start = c->length;
   c->pending_steps = steps;
@@ -1343,11 +1354,11 @@ int qh_decode_profile(qh_model* m, qh_cache* c, int32_t first_token, int32_t ste
   c->h_pinned[3] = first_token;
   hipError_t err = hipMemcpyAsync(c->dev.tokens + start, c->h_pinned + 3, 4, hipMemcpyHostToDevice, s);
   if (err == hipSuccess && (rc = set_state(c, start, start + 1))) err = hipErrorUnknown;
-  // The same launches as a decode replay: one gather, then steps that carry their input.
+  // The same launches as a decode call (capture_graphs), the last step ending with its pick.
   if (err == hipSuccess) err = qh::enqueue_gather(s, m->dev, c->dev);
   for (int i = 0; i < steps && err == hipSuccess; i++) {
     qh::StepTimer t{ev.data(), roles.data(), n_ev, 0};
-    err = qh::enqueue_step(s, m->dev, c->dev, qh::STEP_CARRIED, true, &t);
+    err = qh::enqueue_step(s, m->dev, c->dev, i == 0 ? qh::STEP_CARRIED : qh::STEP_PICK, true, &t, i + 1 < steps);
     if (err == hipSuccess) err = hipStreamSynchronize(s);
     for (int k = 0; err == hipSuccess && k + 1 < t.n; k++) {
       float ms = 0.f;

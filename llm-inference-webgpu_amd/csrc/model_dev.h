@@ -58,9 +58,10 @@ struct CacheDev {
 };
 
 // How a step obtains its input row: gathered from the embedding of tokens[pos],
-// written into cache.x by the caller, or carried over from the previous step
-// (whose output head ends by gathering the embedding of the token it chose).
-enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1, STEP_CARRIED = 2 };
+// written into cache.x by the caller, carried over from the previous step (whose
+// pick gathered the embedding of the token it chose), or picked in this step's first
+// launch from the previous step's head (STEP_PICK: that step deferred its pick).
+enum StepInput { STEP_GATHER = 0, STEP_HIDDEN = 1, STEP_CARRIED = 2, STEP_PICK = 3 };
 
 // Optional per-launch timing: an event is recorded before every launch (tagged with
 // its QH_ROLE_*) and one after the last, so launch i took events[i+1] - events[i].
@@ -102,14 +103,17 @@ hipError_t enqueue_prefill_layers(hipStream_t s, const ModelDev& m, const CacheD
 hipError_t enqueue_embed_rows(hipStream_t s, const ModelDev& m, const CacheDev& c, const PrefillDev& p, int past,
                               int seq);
 
-// Launches one decode position: [gather] -> layers -> (lm_head, then the argmax
-// pick that advances the position and gathers the next input row; or a position
-// advance alone when `logits` is false).
+// Launches one decode position: [gather] -> layers -> (lm_head, which advances the position,
+// then the argmax pick that records the token and gathers the next input row -- left to the
+// next step's first launch with `defer_pick`, which that step then takes as STEP_PICK; or a
+// position advance alone when `logits` is false).
 hipError_t enqueue_step(hipStream_t s, const ModelDev& m, const CacheDev& c, StepInput in,
-                        bool logits, StepTimer* timer = nullptr);
-// The output head of the position state[0] over cache.x: final rmsnorm, lm_head, logits and
-// the pick (token recorded, position advanced, next input row gathered).
+                        bool logits, StepTimer* timer = nullptr, bool defer_pick = false);
+// The output head of the position state[0] over cache.x: final rmsnorm, lm_head, logits, the
+// position advanced, and the pick (token recorded, next input row gathered).
 hipError_t enqueue_head(hipStream_t s, const ModelDev& m, const CacheDev& c, StepTimer* timer = nullptr);
+// The pick alone, after a head whose step deferred it (and that no STEP_PICK step follows).
+hipError_t enqueue_pick(hipStream_t s, const ModelDev& m, const CacheDev& c);
 // One launch of a decode role's kernel: QKV, ATTENTION, OPROJ, GATEUP or DOWN of `layer`, or
 // HEAD (the output head's matvec, without the pick) -- the launches the step makes.
 hipError_t enqueue_role(hipStream_t s, const ModelDev& m, const CacheDev& c, int role, int layer);

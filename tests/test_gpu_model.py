@@ -94,6 +94,44 @@ def test_graph_replay_equals_direct_steps(hip, tiny_model):
     c2.destroy()
 
 
+def test_decode_calls_of_every_length_equal_one_token_forwards(hip, tiny_model):
+    """A decode call is a gather, a first step, steps that each make their predecessor's pick
+    in their own first launch (replayed in runs of 8, one at a time, or launched directly) and
+    a pick launch for the last step. Calls of 1, 2, 8, 9 and 3 steps, replayed and launched
+    directly, give the tokens, lengths and K/V of one-token forwards, each of which picks at the
+    end of its own step."""
+    cfg, model, _, _ = tiny_model
+    prompt = hip.synth_tokens(9, "calls", cfg.vocab, 5)
+    graph, direct, single = model.newCache(40), model.newCache(40), model.newCache(40)
+    model.decode_use_graph(direct, False)
+    first = model.forward_tokens(prompt, graph)["argmax"]
+    for c in (direct, single):
+        assert model.forward_tokens(prompt, c)["argmax"] == first
+    lengths = [1, 2, 8, 9, 3]
+    got = {"graph": [], "direct": []}
+    for name, c in (("graph", graph), ("direct", direct)):
+        tok = first
+        for n in lengths:
+            out = list(model.decode(c, tok, n))
+            assert len(out) == n
+            got[name] += out
+            tok = out[-1]
+    want, tok = [], first
+    for _ in range(sum(lengths)):
+        tok = model.forward_tokens([tok], single)["argmax"]
+        want.append(tok)
+    assert got["graph"] == want and got["direct"] == want
+    assert graph.length == direct.length == single.length == len(prompt) + sum(lengths)
+    for L in range(cfg.layers):
+        ref = single.present(L)
+        for c in (graph, direct):
+            p = c.present(L)
+            np.testing.assert_array_equal(p["key"].view(np.uint32), ref["key"].view(np.uint32))
+            np.testing.assert_array_equal(p["value"].view(np.uint32), ref["value"].view(np.uint32))
+    for c in (graph, direct, single):
+        c.destroy()
+
+
 def test_hidden_input_equals_token_gather(hip, tiny_model):
     cfg, model, _, _ = tiny_model
     ckpt_embed = hip.synthesize_checkpoint(cfg, seed=3)["model.embed_tokens.weight"]
