@@ -233,12 +233,12 @@ struct Item {
   WTile<FMT, R, KC> w;
   EpiIn<EPI, R> e;
   // EPI_OPS: also the epilogue operands (the one-item form; the loop form loads them per
-  // group, see k_fused).
-  template <bool EPI_OPS>
+  // group, see k_fused). STREAM_S: scales and zero points streamed (wtile_load).
+  template <bool EPI_OPS, bool STREAM_S = false>
   __device__ __forceinline__ void load(const FusedArgs& a, int it, int pos, int lane) {
     const int i = min(it, a.items - 1);
     item_rows<EPI, R>(a, i, rows);
-    wtile_load<FMT, R, KC, TL>(a.w, rows, lane, w);
+    wtile_load<FMT, R, KC, TL, STREAM_S>(a.w, rows, lane, w);
     if constexpr (EPI_OPS) epi_load<EPI, R>(a, i, pos, rows, e);
   }
   // The weights of item `it`, which may lie past the last item (CLAMP off: rows past the
@@ -384,7 +384,7 @@ __global__ __launch_bounds__(kBlock) void k_fused(FusedArgs a) {
     pin.load(a.in, PRO == PRO_RMSNORM ? a.gain : nullptr, a.w.cols);
   }
   Item<FMT, TL, R, KC, EPI> ring[NBUF];
-  if constexpr (!kGroup) ring[0].template load<true>(a, it, pos, lane);
+  if constexpr (!kGroup) ring[0].template load<true, LOOP == LOOP_ONE>(a, it, pos, lane);
   if constexpr (PRO == PRO_PICK) {
     const bool first_block = blockIdx.x == 0 && blockIdx.y == 0;
     const int t = pk.finish(pick_red, first_block, a.pred, a.tokens, a.capacity, a.vocab);
