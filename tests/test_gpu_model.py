@@ -99,15 +99,16 @@ def test_decode_calls_of_every_length_equal_one_token_forwards(hip, tiny_model):
     in their own first launch (replayed in runs of 8, one at a time, or launched directly) and
     a pick launch for the last step. Calls of 1, 2, 8, 9 and 3 steps, replayed and launched
     directly, give the tokens, lengths and K/V of one-token forwards, each of which picks at the
-    end of its own step."""
+    end of its own step. The last call fills the caches to their capacity."""
     cfg, model, _, _ = tiny_model
     prompt = hip.synth_tokens(9, "calls", cfg.vocab, 5)
-    graph, direct, single = model.newCache(40), model.newCache(40), model.newCache(40)
+    lengths = [1, 2, 8, 9, 3]
+    capacity = len(prompt) + sum(lengths)
+    graph, direct, single = (model.newCache(capacity) for _ in range(3))
     model.decode_use_graph(direct, False)
     first = model.forward_tokens(prompt, graph)["argmax"]
     for c in (direct, single):
         assert model.forward_tokens(prompt, c)["argmax"] == first
-    lengths = [1, 2, 8, 9, 3]
     got = {"graph": [], "direct": []}
     for name, c in (("graph", graph), ("direct", direct)):
         tok = first
@@ -121,7 +122,7 @@ def test_decode_calls_of_every_length_equal_one_token_forwards(hip, tiny_model):
         tok = model.forward_tokens([tok], single)["argmax"]
         want.append(tok)
     assert got["graph"] == want and got["direct"] == want
-    assert graph.length == direct.length == single.length == len(prompt) + sum(lengths)
+    assert graph.length == direct.length == single.length == capacity
     for L in range(cfg.layers):
         ref = single.present(L)
         for c in (graph, direct):
