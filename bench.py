@@ -4,7 +4,9 @@ with int4-g128 layer weights and an int8 output head,
 on one MI355X through libqwen_hip.so.
 
 A step is one decode token: one replay of the hipGraph-captured decode step
-(gather -> 24 layers -> lm_head -> argmax -> next token, all on the device). The
+(24 layers -> lm_head -> argmax -> next token, all on the device; each step's argmax and
+the next token's gather are made by the next step's first launch, and a decode call ends
+with one pick launch of its own). The
 KV cache is first filled from a seeded 1024-token prompt (untimed); W warmup
 steps run and are rewound; then exactly K steps are timed with HIP events on the
 library's stream (and wall clock around them), inputs resident in HBM.
